@@ -1,0 +1,587 @@
+// C ABI of the device library (include/cpde_hip.h).
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "common.hpp"
+
+struct cpde_device_s : cpde::Device {};
+struct cpde_net_s : cpde::Net {};
+struct cpde_plan_s : cpde::Plan {};
+struct cpde_program_s : cpde::Program {};
+
+namespace cpde {
+
+static thread_local std::string last_error;
+
+void set_error(const std::string& message) { last_error = message; }
+
+void check_hip(hipError_t status, const char* what, const char* file, int line) {
+    if (status == hipSuccess) return;
+    char buf[512];
+    std::snprintf(buf, sizeof buf, "%s:%d: %s failed: %s (%d)", file, line, what, hipGetErrorString(status),
+                  int(status));
+    throw device_error(buf);
+}
+
+void Device::reserve_costs(int costs) {
+    require(costs >= 0, "invalid cost count");
+    if (costs <= cost_capacity) return;
+    HIP_CHECK(hipStreamSynchronize(stream));
+    if (cost_totals) HIP_CHECK(hipFree(cost_totals));
+    if (host_costs) HIP_CHECK(hipHostFree(host_costs));
+    cost_totals = nullptr;
+    host_costs = nullptr;
+    HIP_CHECK(hipMalloc(&cost_totals, sizeof(CostStats) * costs));
+    HIP_CHECK(hipHostMalloc(&host_costs, sizeof(CostStats) * costs, hipHostMallocDefault));
+    cost_capacity = costs;
+}
+
+void Device::reserve_grads(int layers) {
+    if (layers <= grad_capacity) return;
+    HIP_CHECK(hipStreamSynchronize(stream));
+    if (grad_totals) HIP_CHECK(hipFree(grad_totals));
+    if (host_grads) HIP_CHECK(hipHostFree(host_grads));
+    grad_totals = nullptr;
+    host_grads = nullptr;
+    HIP_CHECK(hipMalloc(&grad_totals, sizeof(GradStats) * layers));
+    HIP_CHECK(hipHostMalloc(&host_grads, sizeof(GradStats) * layers, hipHostMallocDefault));
+    grad_capacity = layers;
+}
+
+// Grow the network's shared stack arena for a plan (Server::reserve,
+// cuda/cpde_server.cu:128-147: contexts are views, growth invalidates them).
+static void reserve_arena(Net& net, const Plan& p) {
+    bool grow = false;
+    for (int l = 0; l < net.layers; ++l)
+        if (p.columns() * net.neurons[l] > net.capacity[l]) grow = true;
+    if (!grow) return;
+    HIP_CHECK(hipStreamSynchronize(net.dev->stream));
+    for (int l = 0; l < net.layers; ++l) {
+        const size_t need = std::max(net.capacity[l], p.columns() * net.neurons[l]);
+        if (need == net.capacity[l]) continue;
+        for (auto* v : {&net.z, &net.y, &net.g}) {
+            if ((*v)[l]) HIP_CHECK(hipFree((*v)[l]));
+            (*v)[l] = nullptr;
+        }
+        HIP_CHECK(hipMalloc(&net.z[l], need * sizeof(float)));
+        if (!net.linear[l]) HIP_CHECK(hipMalloc(&net.y[l], need * sizeof(float)));
+        if (l > 0) HIP_CHECK(hipMalloc(&net.g[l], need * sizeof(float)));
+        net.capacity[l] = need;
+    }
+    ++net.generation;
+}
+
+template <class F>
+static int guarded(F body) {
+    try {
+        body();
+        return CPDE_OK;
+    } catch (const invalid& e) {
+        set_error(e.what());
+        return CPDE_EINVAL;
+    } catch (const compile_error& e) {
+        set_error(e.what());
+        return CPDE_ECOMPILE;
+    } catch (const device_error& e) {
+        set_error(e.what());
+        return CPDE_EDEVICE;
+    } catch (const std::bad_alloc&) {
+        set_error("host allocation failed");
+        return CPDE_EDEVICE;
+    } catch (const std::exception& e) {
+        set_error(e.what());
+        return CPDE_EDEVICE;
+    }
+}
+
+static const float* activations(const Net& net, int l) { return net.linear[l] ? net.z[l] : net.y[l]; }
+
+// Device copy of a host row map; re-uploaded only when it changes (the map is
+// fixed for a cost, so a training loop uploads it once).
+static const int* plan_rows(Plan& p, const int* rows) {
+    std::vector<int> map(rows, rows + p.rows);
+    if (map != p.host_rows) {
+        HIP_CHECK(hipStreamSynchronize(p.net->dev->stream));
+        HIP_CHECK(hipMemcpy(p.dev_rows, map.data(), map.size() * sizeof(int), hipMemcpyHostToDevice));
+        p.host_rows = map;
+    }
+    return p.dev_rows;
+}
+
+}  // namespace cpde
+
+using namespace cpde;
+
+extern "C" {
+
+const char* cpde_last_error(void) { return cpde::last_error.c_str(); }
+
+int cpde_device_open(int ordinal, cpde_device** out) {
+    return guarded([&] {
+        require(out != nullptr, "null output");
+        int count = 0;
+        HIP_CHECK(hipGetDeviceCount(&count));
+        require(ordinal >= 0 && ordinal < count, "invalid device ordinal");
+        HIP_CHECK(hipSetDevice(ordinal));
+        auto d = std::make_unique<cpde_device>();
+        d->ordinal = ordinal;
+        hipDeviceProp_t prop;
+        HIP_CHECK(hipGetDeviceProperties(&prop, ordinal));
+        d->compute_units = prop.multiProcessorCount;
+        HIP_CHECK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+        HIP_CHECK(hipMalloc(&d->cost_blocks, sizeof(CostStats) * kMaxCostBlocks));
+        HIP_CHECK(hipMalloc(&d->grad_blocks, sizeof(GradStats) * kMaxCostBlocks));
+        for (auto& e : d->marks) HIP_CHECK(hipEventCreate(&e));
+        d->reserve_costs(8);
+        d->reserve_grads(8);
+        *out = d.release();
+    });
+}
+
+int cpde_device_close(cpde_device* dev) {
+    return guarded([&] {
+        if (!dev) return;
+        (void)hipStreamSynchronize(dev->stream);
+        for (auto& e : dev->marks) (void)hipEventDestroy(e);
+        (void)hipFree(dev->cost_blocks);
+        (void)hipFree(dev->grad_blocks);
+        (void)hipFree(dev->cost_totals);
+        (void)hipFree(dev->grad_totals);
+        (void)hipHostFree(dev->host_costs);
+        (void)hipHostFree(dev->host_grads);
+        (void)hipStreamDestroy(dev->stream);
+        delete dev;
+    });
+}
+
+int cpde_device_synchronize(cpde_device* dev) {
+    return guarded([&] { HIP_CHECK(hipStreamSynchronize(dev->stream)); });
+}
+
+int cpde_device_info(cpde_device* dev, char* name, size_t capacity, int* compute_units) {
+    return guarded([&] {
+        hipDeviceProp_t prop;
+        HIP_CHECK(hipGetDeviceProperties(&prop, dev->ordinal));
+        if (name && capacity) {
+            std::snprintf(name, capacity, "%s (%s)", prop.name, prop.gcnArchName);
+        }
+        if (compute_units) *compute_units = prop.multiProcessorCount;
+    });
+}
+
+int cpde_buffer_alloc(cpde_device* dev, size_t bytes, void** out) {
+    return guarded([&] {
+        require(out != nullptr, "null output");
+        *out = nullptr;
+        if (bytes) HIP_CHECK(hipMalloc(out, bytes));
+        (void)dev;
+    });
+}
+
+int cpde_buffer_free(cpde_device* dev, void* ptr) {
+    return guarded([&] {
+        if (!ptr) return;
+        HIP_CHECK(hipStreamSynchronize(dev->stream));
+        HIP_CHECK(hipFree(ptr));
+    });
+}
+
+int cpde_buffer_upload(cpde_device* dev, void* dst, const void* src, size_t bytes) {
+    return guarded([&] {
+        if (!bytes) return;
+        HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream));
+        HIP_CHECK(hipStreamSynchronize(dev->stream));
+    });
+}
+
+int cpde_buffer_download(cpde_device* dev, void* dst, const void* src, size_t bytes) {
+    return guarded([&] {
+        if (!bytes) return;
+        HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream));
+        HIP_CHECK(hipStreamSynchronize(dev->stream));
+    });
+}
+
+int cpde_buffer_copy(cpde_device* dev, void* dst, const void* src, size_t bytes) {
+    return guarded([&] {
+        if (!bytes) return;
+        HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, dev->stream));
+    });
+}
+
+// ---- network --------------------------------------------------------------------------
+int cpde_net_create(cpde_device* dev, int layers, const int* neurons, const int* linear, const float* const* initial,
+                    cpde_net** out) {
+    return guarded([&] {
+        require(out && neurons && linear, "null argument");
+        require(layers >= 2 && layers <= 256, "invalid architecture");
+        for (int l = 0; l < layers; ++l) require(neurons[l] > 0 && (linear[l] == 0 || linear[l] == 1), "invalid layer");
+        require(linear[0] == 1 && linear[layers - 1] == 1, "input and output layers must be linear");
+        auto n = std::make_unique<cpde_net>();
+        n->dev = dev;
+        n->layers = layers;
+        n->neurons.assign(neurons, neurons + layers);
+        n->linear.assign(linear, linear + layers);
+        const int T = layers - 1;
+        for (auto& s : n->state) s.assign(T, nullptr);
+        n->active.assign(T, 1);
+        n->z.assign(layers, nullptr);
+        n->y.assign(layers, nullptr);
+        n->g.assign(layers, nullptr);
+        n->capacity.assign(layers, 0);
+        for (int t = 0; t < T; ++t) {
+            const size_t count = n->param_count(t);
+            for (int b = 0; b < 4; ++b) HIP_CHECK(hipMalloc(&n->state[b][t], count * sizeof(float)));
+            if (initial && initial[t])
+                HIP_CHECK(hipMemcpyAsync(n->state[0][t], initial[t], count * sizeof(float), hipMemcpyHostToDevice,
+                                         dev->stream));
+            else
+                HIP_CHECK(hipMemsetAsync(n->state[0][t], 0, count * sizeof(float), dev->stream));
+            HIP_CHECK(hipMemsetAsync(n->state[1][t], 0, count * sizeof(float), dev->stream));
+            HIP_CHECK(hipMemsetAsync(n->state[2][t], 0, count * sizeof(float), dev->stream));
+            launch_fill(*dev, n->state[3][t], count, 0.002f);
+        }
+        dev->reserve_grads(T);
+        HIP_CHECK(hipStreamSynchronize(dev->stream));
+        *out = n.release();
+    });
+}
+
+int cpde_net_destroy(cpde_net* net) {
+    return guarded([&] {
+        if (!net) return;
+        (void)hipStreamSynchronize(net->dev->stream);
+        for (auto& s : net->state)
+            for (float* p : s) (void)hipFree(p);
+        for (auto* v : {&net->z, &net->y, &net->g})
+            for (float* p : *v) (void)hipFree(p);
+        (void)hipFree(net->partials);
+        delete net;
+    });
+}
+
+int cpde_net_state(cpde_net* net, int transition, int buffer, float** device_ptr, int* count) {
+    return guarded([&] {
+        require(transition >= 0 && transition < net->layers - 1 && buffer >= 0 && buffer < 4, "invalid state buffer");
+        if (device_ptr) *device_ptr = net->state[buffer][transition];
+        if (count) *count = net->param_count(transition);
+    });
+}
+
+int cpde_net_active(cpde_net* net, int transition) {
+    if (!net || transition < 0 || transition >= net->layers - 1) return -1;
+    return net->active[transition];
+}
+
+int cpde_net_set_active(cpde_net* net, int transition, int active) {
+    return guarded([&] {
+        require(transition >= 0 && transition < net->layers - 1 && (active == 1 || active == 2),
+                "invalid active gradient buffer");
+        net->active[transition] = active;
+    });
+}
+
+uint64_t cpde_net_generation(cpde_net* net) { return net ? net->generation : 0; }
+
+// ---- plans ----------------------------------------------------------------------------
+int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, int width, int backward,
+                     cpde_plan** out) {
+    return guarded([&] {
+        require(net && table && out, "null argument");
+        require(width > 0, "invalid chunk size");
+        auto p = std::make_unique<cpde_plan>();
+        p->net = net;
+        p->rows = rows;
+        p->variables = variables;
+        p->width = width;
+        p->backward = backward ? 1 : 0;
+        p->tables = build_tables(rows, variables, table);
+        for (int l = 0; l < net->layers; ++l)
+            require(double(width) * rows * net->neurons[l] < double(1ull << 40), "context exceeds device capacity");
+        std::vector<int> blob = p->tables.words;
+        blob.insert(blob.end(), p->tables.fwd_offset.begin(), p->tables.fwd_offset.end());
+        HIP_CHECK(hipMalloc(&p->dev_tables, blob.size() * sizeof(int)));
+        HIP_CHECK(hipMalloc(&p->dev_rows, size_t(rows) * sizeof(int)));
+        HIP_CHECK(hipMemcpyAsync(p->dev_tables, blob.data(), blob.size() * sizeof(int), hipMemcpyHostToDevice,
+                                 net->dev->stream));
+        reserve_arena(*net, *p);
+        HIP_CHECK(hipStreamSynchronize(net->dev->stream));
+        *out = p.release();
+    });
+}
+
+int cpde_plan_destroy(cpde_plan* plan) {
+    return guarded([&] {
+        if (!plan) return;
+        (void)hipStreamSynchronize(plan->net->dev->stream);
+        (void)hipFree(plan->dev_tables);
+        (void)hipFree(plan->dev_rows);
+        delete plan;
+    });
+}
+
+int cpde_plan_stack(cpde_plan* plan, int layer, int kind, float** device_ptr) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        require(layer >= 0 && layer < n.layers && kind >= 0 && kind <= 2, "invalid stack");
+        float* p = kind == 0 ? n.z[layer] : kind == 1 ? n.y[layer] : n.g[layer];
+        require(p != nullptr, "stack not present for this layer");
+        *device_ptr = p;
+    });
+}
+
+// ---- hot path ------------------------------------------------------------------------------
+int cpde_activate(cpde_plan* plan, const float* data, int data_width, const int* rows, int offset, int valid) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        require(valid >= 0 && valid <= plan->width && offset >= 0 && offset + valid <= data_width,
+                "invalid chunk range");
+        reserve_arena(n, *plan);
+        launch_activate(d, n.z[0], data, data_width, n.neurons[0], plan_rows(*plan, rows), plan->rows, plan->width,
+                        offset, valid);
+    });
+}
+
+int cpde_forward(cpde_plan* plan) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        const int cols = int(plan->columns());
+        for (int t = 0; t + 1 < n.layers; ++t) {
+            const int ni = n.neurons[t], no = n.neurons[t + 1];
+            if (!n.linear[t]) launch_compose_forward(d, *plan, n.z[t], n.y[t], ni);
+            const float* W = n.state[0][t];
+            launch_gemm(d, no, cols, ni, W, no, false, activations(n, t), ni, false, n.z[t + 1], no,
+                        W + size_t(no) * ni, plan->rows);
+        }
+    });
+}
+
+int cpde_output(cpde_plan* plan, float* dest, int dest_width, const int* rows, int offset, int valid) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        require(valid >= 0 && valid <= plan->width && offset + valid <= dest_width, "invalid chunk range");
+        launch_output(d, dest, n.z[n.layers - 1], dest_width, n.neurons.back(), plan_rows(*plan, rows), plan->rows,
+                      plan->width, offset, valid);
+    });
+}
+
+int cpde_costs_begin(cpde_device* dev, int costs) {
+    return guarded([&] { launch_costs_begin(*dev, costs); });
+}
+
+int cpde_cost_matching(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
+                       const float* weights, int weight_samples, int offset, int valid, int cost_index, int collect,
+                       int gradient) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
+        require(!gradient || plan->backward, "plan has no adjoint storage");
+        const int L = n.layers;
+        launch_matching(d, *plan, n.z[L - 1], gradient ? n.g[L - 1] : nullptr, target, target_width, target_rows,
+                        weights, weight_samples, offset, valid, cost_index, collect != 0, gradient != 0);
+    });
+}
+
+int cpde_cost_polynomial(cpde_plan* plan, const cpde_poly_term* terms, int term_count, const float* coefficients,
+                         const float* rhs, const float* weights, int equations, int samples, int offset, int valid,
+                         int cost_index, int collect, int gradient) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
+        require(!gradient || plan->backward, "plan has no adjoint storage");
+        const int L = n.layers;
+        launch_polynomial(d, *plan, n.z[L - 1], gradient ? n.g[L - 1] : nullptr, terms, term_count, coefficients, rhs,
+                          weights, equations, samples, offset, valid, cost_index, collect != 0, gradient != 0);
+    });
+}
+
+int cpde_scale_adjoint(cpde_plan* plan, const double* multiplier) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        launch_scale_adjoint(*n.dev, *plan, n.g[n.layers - 1], multiplier);
+    });
+}
+
+int cpde_backward(cpde_plan* plan, int accumulate) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        require(plan->backward, "plan has no adjoint storage");
+        const int cols = int(plan->columns());
+        for (int t = n.layers - 2; t >= 0; --t) {
+            const int ni = n.neurons[t], no = n.neurons[t + 1];
+            float* grad = n.state[n.active[t]][t];
+            launch_wgrad(d, n, no, ni, cols, n.g[t + 1], activations(n, t), grad, accumulate != 0);
+            launch_bias_grad(d, no, plan->width, plan->rows, n.g[t + 1], grad + size_t(no) * ni, accumulate != 0);
+            if (t > 0) {
+                launch_gemm(d, ni, cols, no, n.state[0][t], no, true, n.g[t + 1], no, false, n.g[t], ni, nullptr, 1);
+                if (!n.linear[t]) launch_compose_adjoint(d, *plan, n.z[t], n.g[t], ni);
+            }
+        }
+    });
+}
+
+// ---- reductions and optimizers --------------------------------------------------------------
+int cpde_inspect_gradients(cpde_net* net) {
+    return guarded([&] {
+        Device& d = *net->dev;
+        d.reserve_grads(net->layers - 1);
+        for (int t = 0; t + 1 < net->layers; ++t)
+            launch_grad_stats(d, net->state[net->active[t]][t], net->param_count(t), t);
+    });
+}
+
+int cpde_scalars_download(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
+                          cpde_gradient_stats* gradient_out) {
+    return guarded([&] {
+        require(costs <= dev->cost_capacity && layers <= dev->grad_capacity, "scalar slots out of range");
+        if (costs)
+            HIP_CHECK(hipMemcpyAsync(dev->host_costs, dev->cost_totals, sizeof(CostStats) * costs,
+                                     hipMemcpyDeviceToHost, dev->stream));
+        if (layers)
+            HIP_CHECK(hipMemcpyAsync(dev->host_grads, dev->grad_totals, sizeof(GradStats) * layers,
+                                     hipMemcpyDeviceToHost, dev->stream));
+        HIP_CHECK(hipStreamSynchronize(dev->stream));
+        if (costs && cost_out) std::memcpy(cost_out, dev->host_costs, sizeof(CostStats) * costs);
+        if (layers && gradient_out) std::memcpy(gradient_out, dev->host_grads, sizeof(GradStats) * layers);
+    });
+}
+
+int cpde_rprop(cpde_net* net) {
+    return guarded([&] { launch_rprop(*net->dev, *net); });
+}
+
+int cpde_adam(cpde_net* net, int step, float lr) {
+    return guarded([&] {
+        require(step >= 1, "Adam step must be positive");
+        launch_adam(*net->dev, *net, step, lr);
+    });
+}
+
+int cpde_set_steps(cpde_net* net, float value) {
+    return guarded([&] { launch_set_steps(*net->dev, *net, value); });
+}
+
+int cpde_restore_steps(cpde_net* net, float floor_value) {
+    return guarded([&] { launch_restore_steps(*net->dev, *net, floor_value); });
+}
+
+int cpde_zero_gradient(cpde_net* net) {
+    return guarded([&] {
+        for (int t = 0; t + 1 < net->layers; ++t)
+            launch_fill(*net->dev, net->state[net->active[t]][t], net->param_count(t), 0.0f);
+    });
+}
+
+int cpde_reset_optimizer(cpde_net* net) {
+    return guarded([&] {
+        for (int t = 0; t + 1 < net->layers; ++t) {
+            net->active[t] = 1;
+            for (int b = 1; b < 4; ++b) launch_fill(*net->dev, net->state[b][t], net->param_count(t), 0.0f);
+        }
+    });
+}
+
+// ---- expression programs (hipRTC) ----------------------------------------------------------
+int cpde_program_compile(cpde_device* dev, const char* source, cpde_program** out, char* log, size_t log_capacity) {
+    return guarded([&] {
+        require(source && out, "null argument");
+        hiprtcProgram prog;
+        if (hiprtcCreateProgram(&prog, source, "cpde_expression.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+            throw compile_error("hiprtcCreateProgram failed");
+        hipDeviceProp_t prop;
+        HIP_CHECK(hipGetDeviceProperties(&prop, dev->ordinal));
+        std::string arch = std::string("--offload-arch=") + prop.gcnArchName;
+        const char* options[] = {arch.c_str(), "-O3", "-std=c++17"};
+        const hiprtcResult result = hiprtcCompileProgram(prog, 3, options);
+        size_t size = 0;
+        hiprtcGetProgramLogSize(prog, &size);
+        std::string text(size, '\0');
+        if (size) hiprtcGetProgramLog(prog, &text[0]);
+        while (!text.empty() && text.back() == '\0') text.pop_back();
+        if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
+        if (result != HIPRTC_SUCCESS) {
+            hiprtcDestroyProgram(&prog);
+            throw compile_error("expression compile failed: " + text);
+        }
+        size_t code_size = 0;
+        hiprtcGetCodeSize(prog, &code_size);
+        std::vector<char> code(code_size);
+        hiprtcGetCode(prog, code.data());
+        hiprtcDestroyProgram(&prog);
+        auto p = std::make_unique<cpde_program>();
+        p->dev = dev;
+        p->log = text;
+        HIP_CHECK(hipModuleLoadData(&p->module, code.data()));
+        HIP_CHECK(hipModuleGetFunction(&p->function, p->module, "expression"));
+        *out = p.release();
+    });
+}
+
+int cpde_program_destroy(cpde_program* program) {
+    return guarded([&] {
+        if (!program) return;
+        (void)hipStreamSynchronize(program->dev->stream);
+        if (program->module) (void)hipModuleUnload(program->module);
+        delete program;
+    });
+}
+
+int cpde_cost_expression(cpde_plan* plan, cpde_program* program, const double* fields,
+                         const double* quadrature_weights, int samples, int offset, int valid,
+                         const double* multiplier, void* scratch, int cost_index, int collect, int gradient) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
+        require(!gradient || plan->backward, "plan has no adjoint storage");
+        const float* y = n.z[n.layers - 1];
+        float* g = gradient ? n.g[n.layers - 1] : nullptr;
+        double* loss = static_cast<double*>(scratch);
+        int* bad = reinterpret_cast<int*>(loss + plan->width);
+        int outputs = n.neurons.back(), rows = plan->rows, width = plan->width;
+        int col = collect, grd = gradient;
+        void* args[] = {&y, &g, &fields, &quadrature_weights, &loss, &bad, &outputs, &rows, &samples, &width,
+                        &offset, &valid, &multiplier, &col, &grd};
+        const int blocks = std::max(1, std::min(kMaxCostBlocks, (width + kCostThreads - 1) / kCostThreads));
+        HIP_CHECK(hipModuleLaunchKernel(program->function, blocks, 1, 1, kCostThreads, 1, 1, 0, d.stream, args,
+                                        nullptr));
+        launch_sample_reduce(d, loss, bad, valid, offset, cost_index);
+    });
+}
+
+int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int count, int root, int leaves,
+                       double* values, double* adjoints, double* multipliers, int* active, cpde_graph_summary* summary,
+                       int gradient) {
+    return guarded([&] {
+        require(leaves <= dev->cost_capacity, "graph leaves exceed cost slots");
+        launch_graph(*dev, nodes, count, root, leaves, values, adjoints, multipliers, active, summary, gradient != 0);
+    });
+}
+
+int cpde_mark(cpde_device* dev, int slot) {
+    return guarded([&] {
+        require(slot >= 0 && slot < 8, "invalid event slot");
+        HIP_CHECK(hipEventRecord(dev->marks[slot], dev->stream));
+    });
+}
+
+int cpde_elapsed(cpde_device* dev, int from_slot, int to_slot, float* ms) {
+    return guarded([&] {
+        require(from_slot >= 0 && from_slot < 8 && to_slot >= 0 && to_slot < 8, "invalid event slot");
+        HIP_CHECK(hipEventSynchronize(dev->marks[to_slot]));
+        HIP_CHECK(hipEventElapsedTime(ms, dev->marks[from_slot], dev->marks[to_slot]));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,157 @@
+// Internal declarations shared by the device library's translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/cpde_hip.h"
+
+namespace cpde {
+
+// Raised for invalid arguments; the C ABI maps it to CPDE_EINVAL.
+struct invalid : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+// Raised for HIP runtime failures; mapped to CPDE_EDEVICE.
+struct device_error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+struct compile_error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+void set_error(const std::string& message);
+void check_hip(hipError_t status, const char* what, const char* file, int line);
+#define HIP_CHECK(expr) ::cpde::check_hip((expr), #expr, __FILE__, __LINE__)
+inline void require(bool ok, const char* message) {
+    if (!ok) throw invalid(message);
+}
+
+constexpr int kMaxOrder = 6;
+constexpr int kMaxRows = 255;      // row indices are stored in 8 bits in the term tables
+constexpr int kMaxTransitions = 32;  // per fused optimizer launch
+constexpr int kCostThreads = 256;
+constexpr int kMaxCostBlocks = 1024;
+
+// Device-side mirrors of the public reduction structs.
+struct CostStats {
+    double value;
+    int bad_sample, bad_component;
+};
+struct GradStats {
+    double squared_norm, max_abs;
+    unsigned long long nonfinite;
+    int first, pad_;
+};
+static_assert(sizeof(CostStats) == sizeof(cpde_cost_stats), "cost stats layout");
+static_assert(sizeof(GradStats) == sizeof(cpde_gradient_stats), "gradient stats layout");
+
+// Composition term tables for one schema (built on the host, see tables.cpp).
+//   forward:   for row r >= 1 at fwd_offset[r]: order k, then for m = 1..k a count
+//              c_m followed by c_m records {coefficient bits, packed block rows};
+//              block rows are 8-bit, packed little-endian into two ints.
+//   adjoint:   for row i at pair_offset[i]: count, then records {j, dn, coefficient}.
+struct Tables {
+    int rows = 0, variables = 0;
+    std::vector<int> table;        // rows x (variables+1)
+    std::vector<int> words;        // forward section then adjoint section
+    std::vector<int> fwd_offset;   // per row
+    std::vector<int> pair_offset;  // per row
+    int forward_terms = 0, pair_terms = 0, max_order = 0;
+};
+Tables build_tables(int rows, int variables, const int* table);
+
+struct Device;
+
+struct Net {
+    Device* dev = nullptr;
+    int layers = 0;
+    std::vector<int> neurons, linear;
+    // Per transition t: four state buffers of n_{t+1} x (n_t+1) floats.
+    std::vector<float*> state[4];
+    std::vector<int> active;  // 1 or 2 per transition
+    // Stack arena shared by every plan of the network (contexts are views,
+    // the reference's layer banks, cuda/cpde_engine.cuh:661-693).
+    std::vector<float*> z, y, g;      // per layer
+    std::vector<size_t> capacity;     // floats per layer buffer
+    uint64_t generation = 0;
+    // split-K partial buffer for the weight-gradient contraction
+    float* partials = nullptr;
+    size_t partial_capacity = 0;
+    int param_count(int t) const { return neurons[t + 1] * (neurons[t] + 1); }
+};
+
+struct Plan {
+    Net* net = nullptr;
+    int rows = 0, variables = 0, width = 0, backward = 0;
+    Tables tables;
+    int* dev_tables = nullptr;  // device copy of tables.words, then tables.fwd_offset
+    int* dev_rows = nullptr;    // device row map of the last activate/output
+    std::vector<int> host_rows;
+    size_t columns() const { return size_t(rows) * size_t(width); }
+};
+
+struct Program {
+    Device* dev = nullptr;
+    hipModule_t module = nullptr;
+    hipFunction_t function = nullptr;
+    std::string log;
+};
+
+struct Device {
+    int ordinal = 0;
+    int compute_units = 0;
+    hipStream_t stream = nullptr;
+    // reduction workspace (cuda/reduction_kernels.cuh:101-178)
+    CostStats* cost_blocks = nullptr;   // kMaxCostBlocks
+    CostStats* cost_totals = nullptr;   // cost_capacity
+    GradStats* grad_blocks = nullptr;   // kMaxCostBlocks
+    GradStats* grad_totals = nullptr;   // grad_capacity
+    CostStats* host_costs = nullptr;
+    GradStats* host_grads = nullptr;
+    int cost_capacity = 0, grad_capacity = 0;
+    hipEvent_t marks[8] = {};
+    void reserve_costs(int costs);
+    void reserve_grads(int layers);
+};
+
+// ---- kernel launchers (kernels.hip) -------------------------------------------------
+void launch_activate(Device& d, float* x, const float* data, int data_width, int channels, const int* rows_dev,
+                     int rows, int width, int offset, int valid);
+void launch_output(Device& d, float* dest, const float* out, int dest_width, int channels, const int* rows_dev,
+                   int rows, int width, int offset, int valid);
+void launch_compose_forward(Device& d, const Plan& p, const float* z, float* y, int n);
+void launch_compose_adjoint(Device& d, const Plan& p, const float* z, float* g, int n);
+// C[M x N] = A[M x K] * B[K x N]; a_t: A stored k-contiguous (A[k + lda*m]);
+// b_t: B stored n-contiguous (B[n + ldb*k]).  bias (may be null) is added to every
+// column n with n % period == 0.
+void launch_gemm(Device& d, int M, int N, int K, const float* A, int lda, bool a_t, const float* B, int ldb, bool b_t,
+                 float* C, int ldc, const float* bias, int period);
+// Weight gradient dW[M x N] (+)= G[M x K] * Y[N x K]^T (both column-major with
+// ld M and N), deterministic split-K through the network's partial buffer.
+void launch_wgrad(Device& d, Net& net, int M, int N, int K, const float* G, const float* Y, float* dW, bool accumulate);
+// db[m] (+)= sum over points p of G[(p*R)*M + m] (value row of a [point][row][M] stack).
+void launch_bias_grad(Device& d, int M, int width, int R, const float* G, float* db, bool accumulate);
+void launch_matching(Device& d, const Plan& p, const float* y, float* g, const float* target, int target_width,
+                     const int* target_rows, const float* weights, int weight_samples, int offset, int valid,
+                     int cost_index, bool collect, bool gradient);
+void launch_polynomial(Device& d, const Plan& p, const float* y, float* g, const cpde_poly_term* terms, int term_count,
+                       const float* coefficients, const float* rhs, const float* weights, int equations, int samples,
+                       int offset, int valid, int cost_index, bool collect, bool gradient);
+void launch_sample_reduce(Device& d, const double* values, const int* bad, int valid, int offset, int cost_index);
+void launch_scale_adjoint(Device& d, const Plan& p, float* g, const double* multiplier);
+void launch_costs_begin(Device& d, int costs);
+void launch_grad_stats(Device& d, const float* g, int count, int slot);
+void launch_fill(Device& d, float* p, size_t count, float value);
+void launch_rprop(Device& d, Net& net);
+void launch_adam(Device& d, Net& net, int step, float lr);
+void launch_set_steps(Device& d, Net& net, float value);
+void launch_restore_steps(Device& d, Net& net, float floor_value);
+void launch_graph(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,
+                  double* adjoints, double* multipliers, int* active, cpde_graph_summary* summary, bool gradient);
+
+}  // namespace cpde

@@ -1,0 +1,886 @@
+// gfx950 kernels of the cPDE hot path.
+//
+// Stacks are [point][row][neuron] (neuron fastest): one GEMM column is one
+// (point,row) pair, so a point's derivative rows are adjacent columns.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+
+#include "common.hpp"
+
+namespace cpde {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// ------------------------------------------------------------------------------------------
+// sigma^{(k)}(z), k = 1..7, from q = 1/(1+e^z): the reference's recurrences
+// (cuda/derivative_kernels_v4.cu:1-10, 462-468; KNOWN_ISSUES F04 keeps the tails).
+__device__ __forceinline__ void sigma_derivatives(float z, float* s) {
+    const float q = 1.0f / (1.0f + expf(z));
+    s[1] = q * (1.0f - q);
+    s[2] = -s[1] * (1.0f - 2.0f * q);
+    s[3] = s[1] * (1.0f - 6.0f * s[1]);
+    s[4] = s[2] * (1.0f - 12.0f * s[1]);
+    s[5] = s[1] - (5.0f * s[2]) * (6.0f * s[2]);
+    s[6] = s[2] + 5.0f * (s[4] - s[2]) * (1.0f - 6.0f * s[1]);
+    s[7] = (5.0f * s[1]) * (0.2f - (8.4f * s[1]) * (3.0f - 4.0f * (5.0f * s[1] + 5.0f * s[3])));
+}
+
+// Sum over a row's multiset-partition terms: sum_m s[m+shift] * M_m, with
+// M_m = sum_terms coefficient * prod(block rows).  `col` is this lane's private
+// LDS column (stride B floats per row); `pos` walks the uniform term table.
+template <int B, int SHIFT>
+__device__ __forceinline__ float partition_sum(const float* col, const int* __restrict__ words, int& pos,
+                                               const float* s) {
+    const int k = words[pos++];
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 1; m <= kMaxOrder; ++m) {
+        if (m <= k) {
+            const int count = words[pos++];
+            float M = 0.0f;
+            for (int q = 0; q < count; ++q) {
+                const float c = __int_as_float(words[pos]);
+                const unsigned w0 = unsigned(words[pos + 1]), w1 = unsigned(words[pos + 2]);
+                pos += 3;
+                float prod = col[(w0 & 255u) * B];
+                if (m > 1) prod *= col[((w0 >> 8) & 255u) * B];
+                if (m > 2) prod *= col[((w0 >> 16) & 255u) * B];
+                if (m > 3) prod *= col[(w0 >> 24) * B];
+                if (m > 4) prod *= col[(w1 & 255u) * B];
+                if (m > 5) prod *= col[((w1 >> 8) & 255u) * B];
+                M = fmaf(c, prod, M);
+            }
+            acc = (m == 1) ? s[1 + SHIFT] * M : fmaf(s[m + SHIFT], M, acc);
+        }
+    }
+    return acc;
+}
+
+// Forward composition y = d^alpha sigma(z) for every row of one (point, neuron)
+// per lane (replaces d0..d6, cuda/derivative_kernels_v4.cu:382-745, and the
+// per-row launch loop network::D, cuda/cpde_engine.cuh:852-866).
+template <int B>
+__global__ __launch_bounds__(B) void compose_forward_kernel(const float* __restrict__ z, float* __restrict__ y, int R,
+                                                            int n, int elements, const int* __restrict__ words) {
+    extern __shared__ float lds[];
+    const int t = threadIdx.x;
+    const int e = blockIdx.x * B + t;
+    const bool live = e < elements;
+    const int p = live ? e / n : 0, i = live ? e - p * n : 0;
+    const size_t base = size_t(p) * R * n + i;
+    float* col = lds + t;
+    for (int r = 0; r < R; ++r) col[r * B] = live ? z[base + size_t(r) * n] : 0.0f;
+    float s[8];
+    const float z0 = col[0];
+    sigma_derivatives(z0, s);
+    if (live) y[base] = 1.0f / (1.0f + expf(-z0));
+    int pos = 0;
+    for (int r = 1; r < R; ++r) {
+        const float v = partition_sum<B, 0>(col, words, pos, s);
+        if (live) y[base + size_t(r) * n] = v;
+    }
+}
+
+// Adjoint composition (replaces back_step + DPlus/d1p..d6p,
+// cuda/derivative_kernels_v4.cu:12-380):
+//   g_z[i] = sigma'(z) g_y[i] + sum_{j>i, alpha_j>=alpha_i} C(alpha_j,alpha_i) g_y[j] D[alpha_j-alpha_i]
+// with D[beta] = d^beta sigma'(z) evaluated once per row (it depends only on the
+// difference row), computed in place over the z column in descending row order.
+template <int B>
+__global__ __launch_bounds__(B) void compose_adjoint_kernel(const float* __restrict__ z, float* __restrict__ g, int R,
+                                                            int n, int elements, const int* __restrict__ words,
+                                                            const int* __restrict__ fwd_offset, int pair_begin) {
+    extern __shared__ float lds[];
+    const int t = threadIdx.x;
+    const int e = blockIdx.x * B + t;
+    const bool live = e < elements;
+    const int p = live ? e / n : 0, i = live ? e - p * n : 0;
+    const size_t base = size_t(p) * R * n + i;
+    float* zc = lds + t;
+    float* gc = lds + size_t(R) * B + t;
+    for (int r = 0; r < R; ++r) {
+        zc[r * B] = live ? z[base + size_t(r) * n] : 0.0f;
+        gc[r * B] = live ? g[base + size_t(r) * n] : 0.0f;
+    }
+    float s[8];
+    sigma_derivatives(zc[0], s);
+    for (int r = R - 1; r >= 1; --r) {
+        int pos = fwd_offset[r];
+        const float d = partition_sum<B, 1>(zc, words, pos, s);
+        zc[r * B] = d;
+    }
+    int pos = pair_begin;
+    for (int a = 0; a < R; ++a) {
+        const int count = words[pos++];
+        float acc = s[1] * gc[a * B];
+        for (int q = 0; q < count; ++q) {
+            const int j = words[pos], dn = words[pos + 1];
+            const float c = __int_as_float(words[pos + 2]);
+            pos += 3;
+            acc = acc + (c * gc[j * B]) * zc[dn * B];
+        }
+        if (live) g[base + size_t(a) * n] = acc;
+    }
+}
+
+static int compose_block(int R, int arrays) {
+    // Largest block (256/128/64) whose private columns fit in 64 KB of LDS.
+    for (int b = 256; b >= 64; b /= 2)
+        if (size_t(arrays) * R * b * sizeof(float) <= 65536) return b;
+    return 64;
+}
+
+void launch_compose_forward(Device& d, const Plan& p, const float* z, float* y, int n) {
+    const int R = p.rows, elements = p.width * n;
+    const int b = compose_block(R, 1);
+    const size_t lds = size_t(R) * b * sizeof(float);
+    const int grid = (elements + b - 1) / b;
+    if (b == 256)
+        hipLaunchKernelGGL(compose_forward_kernel<256>, grid, 256, lds, d.stream, z, y, R, n, elements, p.dev_tables);
+    else if (b == 128)
+        hipLaunchKernelGGL(compose_forward_kernel<128>, grid, 128, lds, d.stream, z, y, R, n, elements, p.dev_tables);
+    else
+        hipLaunchKernelGGL(compose_forward_kernel<64>, grid, 64, lds, d.stream, z, y, R, n, elements, p.dev_tables);
+    HIP_CHECK(hipGetLastError());
+}
+
+void launch_compose_adjoint(Device& d, const Plan& p, const float* z, float* g, int n) {
+    const int R = p.rows, elements = p.width * n;
+    const int b = compose_block(R, 2);
+    const size_t lds = 2 * size_t(R) * b * sizeof(float);
+    const int grid = (elements + b - 1) / b;
+    const int* offsets = p.dev_tables + p.tables.words.size();
+    const int pair_begin = p.tables.pair_offset[0];
+    if (b == 256)
+        hipLaunchKernelGGL(compose_adjoint_kernel<256>, grid, 256, lds, d.stream, z, g, R, n, elements, p.dev_tables,
+                           offsets, pair_begin);
+    else if (b == 128)
+        hipLaunchKernelGGL(compose_adjoint_kernel<128>, grid, 128, lds, d.stream, z, g, R, n, elements, p.dev_tables,
+                           offsets, pair_begin);
+    else
+        hipLaunchKernelGGL(compose_adjoint_kernel<64>, grid, 64, lds, d.stream, z, g, R, n, elements, p.dev_tables,
+                           offsets, pair_begin);
+    HIP_CHECK(hipGetLastError());
+}
+
+// ------------------------------------------------------------------------------------------
+// FP32 MFMA GEMM: C[M x N] = A[M x K] * B[K x N] on v_mfma_f32_32x32x2_f32 (true
+// fp32, no reduced-precision shortcut).  256 lanes = WM x WN waves; each wave owns
+// a (BM/WM) x (BN/WN) tile made of 32x32 MFMA blocks.  Tiles of A and B pass
+// through LDS in K chunks of BK.  Split-K: blockIdx.z takes K range
+// [z*k_split, (z+1)*k_split) and writes its partial product to C + z*ldc*N.
+constexpr int BK = 16;
+
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(256) void gemm_kernel(int M, int N, int K, const float* __restrict__ A, int lda, int a_t,
+                                                   const float* __restrict__ Bm, int ldb, int b_t, float* __restrict__ C,
+                                                   int ldc, const float* __restrict__ bias, int period, int k_split) {
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int IM = TM / 32, IN = TN / 32;
+    __shared__ float As[BK][BM + 1];
+    __shared__ float Bs[BK][BN + 1];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave % WM, wn = wave / WM;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    int kbegin = 0, kend = K;
+    if (k_split > 0) {
+        kbegin = blockIdx.z * k_split;
+        kend = min(K, kbegin + k_split);
+        C += size_t(blockIdx.z) * ldc * N;
+    }
+    floatx16 acc[IM][IN];
+#pragma unroll
+    for (int a = 0; a < IM; ++a)
+#pragma unroll
+        for (int b = 0; b < IN; ++b)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+
+    for (int k0 = kbegin; k0 < kend; k0 += BK) {
+        // A tile -> As[k][m]
+#pragma unroll
+        for (int idx = t; idx < BM * BK; idx += 256) {
+            int m, k;
+            if (a_t) { k = idx % BK; m = idx / BK; }
+            else { m = idx % BM; k = idx / BM; }
+            const int gm = m0 + m, gk = k0 + k;
+            float v = 0.0f;
+            if (gm < M && gk < kend) v = a_t ? A[gk + size_t(lda) * gm] : A[gm + size_t(lda) * gk];
+            As[k][m] = v;
+        }
+        // B tile -> Bs[k][n]
+#pragma unroll
+        for (int idx = t; idx < BN * BK; idx += 256) {
+            int n, k;
+            if (b_t) { n = idx % BN; k = idx / BN; }
+            else { k = idx % BK; n = idx / BK; }
+            const int gn = n0 + n, gk = k0 + k;
+            float v = 0.0f;
+            if (gn < N && gk < kend) v = b_t ? Bm[gn + size_t(ldb) * gk] : Bm[gk + size_t(ldb) * gn];
+            Bs[k][n] = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            const int kr = kk + (lane >> 5), lc = lane & 31;
+            float av[IM], bv[IN];
+#pragma unroll
+            for (int a = 0; a < IM; ++a) av[a] = As[kr][wm * TM + a * 32 + lc];
+#pragma unroll
+            for (int b = 0; b < IN; ++b) bv[b] = Bs[kr][wn * TN + b * 32 + lc];
+#pragma unroll
+            for (int a = 0; a < IM; ++a)
+#pragma unroll
+                for (int b = 0; b < IN; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    // Accumulator layout of a 32x32 block: lane l, register v holds
+    // row 8*(v/4) + 4*(l/32) + v%4, column l%32.
+#pragma unroll
+    for (int a = 0; a < IM; ++a)
+#pragma unroll
+        for (int b = 0; b < IN; ++b) {
+            const int gn = n0 + wn * TN + b * 32 + (lane & 31);
+            if (gn >= N) continue;
+            const bool add_bias = bias != nullptr && (gn % period) == 0;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int gm = m0 + wm * TM + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (gm < M) C[gm + size_t(ldc) * gn] = acc[a][b][v] + (add_bias ? bias[gm] : 0.0f);
+            }
+        }
+}
+
+static void gemm_dispatch(Device& d, int M, int N, int K, const float* A, int lda, bool a_t, const float* B, int ldb,
+                          bool b_t, float* C, int ldc, const float* bias, int period, int splits, int k_split) {
+    if (M <= 32) {
+        dim3 grid((M + 31) / 32, (N + 127) / 128, splits);
+        hipLaunchKernelGGL((gemm_kernel<32, 128, 1, 4>), grid, 256, 0, d.stream, M, N, K, A, lda, int(a_t), B, ldb,
+                           int(b_t), C, ldc, bias, period, k_split);
+    } else {
+        dim3 grid((M + 127) / 128, (N + 63) / 64, splits);
+        hipLaunchKernelGGL((gemm_kernel<128, 64, 4, 1>), grid, 256, 0, d.stream, M, N, K, A, lda, int(a_t), B, ldb,
+                           int(b_t), C, ldc, bias, period, k_split);
+    }
+    HIP_CHECK(hipGetLastError());
+}
+
+void launch_gemm(Device& d, int M, int N, int K, const float* A, int lda, bool a_t, const float* B, int ldb, bool b_t,
+                 float* C, int ldc, const float* bias, int period) {
+    if (M <= 0 || N <= 0) return;
+    gemm_dispatch(d, M, N, K, A, lda, a_t, B, ldb, b_t, C, ldc, bias, period > 0 ? period : 1, 1, 0);
+}
+
+// Fixed-order sum of split-K partials: out[i] = sum_s P[s][i] (+ out[i]).
+__global__ void split_reduce_kernel(const float* __restrict__ P, int splits, size_t count, float* __restrict__ out,
+                                    int accumulate) {
+    for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < count; i += size_t(gridDim.x) * blockDim.x) {
+        float s = 0.0f;
+        for (int z = 0; z < splits; ++z) s += P[size_t(z) * count + i];
+        out[i] = accumulate ? out[i] + s : s;
+    }
+}
+
+void launch_wgrad(Device& d, Net& net, int M, int N, int K, const float* G, const float* Y, float* dW,
+                  bool accumulate) {
+    const int BMx = M <= 32 ? 32 : 128, BNx = M <= 32 ? 128 : 64;
+    const int tiles = ((M + BMx - 1) / BMx) * ((N + BNx - 1) / BNx);
+    int splits = std::max(1, (2 * d.compute_units + tiles - 1) / tiles);
+    splits = std::min(splits, std::max(1, K / 64));
+    int k_split = (K + splits - 1) / splits;
+    k_split = (k_split + BK - 1) / BK * BK;
+    splits = (K + k_split - 1) / k_split;
+    const size_t need = size_t(splits) * M * N;
+    if (need > net.partial_capacity) {
+        HIP_CHECK(hipStreamSynchronize(d.stream));
+        if (net.partials) HIP_CHECK(hipFree(net.partials));
+        net.partials = nullptr;
+        HIP_CHECK(hipMalloc(&net.partials, need * sizeof(float)));
+        net.partial_capacity = need;
+    }
+    // dW = G * Y^T: A = G (M x K, ld M), B(k, n) = Y[n + N*k] (n-contiguous).
+    gemm_dispatch(d, M, N, K, G, M, false, Y, N, true, net.partials, M, nullptr, 1, splits, k_split);
+    const size_t count = size_t(M) * N;
+    const int blocks = int(std::min<size_t>((count + 255) / 256, 1024));
+    hipLaunchKernelGGL(split_reduce_kernel, blocks, 256, 0, d.stream, net.partials, splits, count, dW,
+                       int(accumulate));
+    HIP_CHECK(hipGetLastError());
+}
+
+// db[m] (+)= sum_p G[(p*R)*M + m]: one block per 64 outputs; lanes stride the
+// points and a fixed tree combines them.
+__global__ __launch_bounds__(256) void bias_grad_kernel(int M, int width, int R, const float* __restrict__ G,
+                                                        float* __restrict__ db, int accumulate) {
+    __shared__ float part[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m = blockIdx.x * 64 + lane;
+    float s = 0.0f;
+    if (m < M)
+        for (int p = wave; p < width; p += 4) s += G[size_t(p) * R * M + m];
+    part[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && m < M) {
+        const float total = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+        db[m] = accumulate ? db[m] + total : total;
+    }
+}
+
+void launch_bias_grad(Device& d, int M, int width, int R, const float* G, float* db, bool accumulate) {
+    hipLaunchKernelGGL(bias_grad_kernel, (M + 63) / 64, 256, 0, d.stream, M, width, R, G, db, int(accumulate));
+    HIP_CHECK(hipGetLastError());
+}
+
+// ------------------------------------------------------------------------------------------
+// Activation of a chunk (Server::activate, cuda/cpde_server.cu:158-170) and the
+// evaluation copy-out (:180): wire layout [row][sample][channel] <-> stack.
+__global__ void activate_kernel(float* __restrict__ x, const float* __restrict__ data, int data_width, int channels,
+                                const int* __restrict__ rows, int R, int width, int offset, int valid) {
+    const size_t total = size_t(width) * R * channels;
+    for (size_t e = blockIdx.x * size_t(blockDim.x) + threadIdx.x; e < total; e += size_t(gridDim.x) * blockDim.x) {
+        const int c = int(e % channels);
+        const size_t pr = e / channels;
+        const int r = int(pr % R), p = int(pr / R);
+        x[e] = p < valid ? data[(size_t(rows[r]) * data_width + offset + p) * channels + c] : 0.0f;
+    }
+}
+
+void launch_activate(Device& d, float* x, const float* data, int data_width, int channels, const int* rows_dev,
+                     int rows, int width, int offset, int valid) {
+    const size_t total = size_t(width) * rows * channels;
+    const int blocks = int(std::min<size_t>((total + 255) / 256, 4096));
+    hipLaunchKernelGGL(activate_kernel, blocks, 256, 0, d.stream, x, data, data_width, channels, rows_dev, rows, width,
+                       offset, valid);
+    HIP_CHECK(hipGetLastError());
+}
+
+__global__ void output_kernel(float* __restrict__ dest, const float* __restrict__ out, int dest_width, int channels,
+                              const int* __restrict__ rows, int R, int offset, int valid) {
+    const size_t total = size_t(valid) * R * channels;
+    for (size_t e = blockIdx.x * size_t(blockDim.x) + threadIdx.x; e < total; e += size_t(gridDim.x) * blockDim.x) {
+        const int c = int(e % channels);
+        const size_t pr = e / channels;
+        const int r = int(pr % R), p = int(pr / R);
+        dest[(size_t(rows[r]) * dest_width + offset + p) * channels + c] = out[e];
+    }
+}
+
+void launch_output(Device& d, float* dest, const float* out, int dest_width, int channels, const int* rows_dev,
+                   int rows, int width, int offset, int valid) {
+    (void)width;
+    const size_t total = size_t(valid) * rows * channels;
+    if (!total) return;
+    const int blocks = int(std::min<size_t>((total + 255) / 256, 4096));
+    hipLaunchKernelGGL(output_kernel, blocks, 256, 0, d.stream, dest, out, dest_width, channels, rows_dev, rows, offset,
+                       valid);
+    HIP_CHECK(hipGetLastError());
+}
+
+// ------------------------------------------------------------------------------------------
+// Deterministic reductions.  Cost statistics combine as a signed double sum plus
+// the lexicographically smallest (sample, component) bad location
+// (cuda/reduction_kernels.cuh:36-46); partials are reduced in a fixed order.
+__device__ __forceinline__ CostStats combine(CostStats a, const CostStats& b) {
+    a.value += b.value;
+    if (b.bad_sample < a.bad_sample || (b.bad_sample == a.bad_sample && b.bad_component < a.bad_component)) {
+        a.bad_sample = b.bad_sample;
+        a.bad_component = b.bad_component;
+    }
+    return a;
+}
+__device__ __forceinline__ CostStats empty_cost() { return CostStats{0.0, INT_MAX, INT_MAX}; }
+__device__ __forceinline__ void mark_bad(CostStats& s, int sample, int component) {
+    s = combine(s, CostStats{0.0, sample, component});
+}
+
+// Block-wide fixed-order reduction: wave shuffles, then the 4 wave results in order.
+__device__ CostStats block_reduce_cost(CostStats v) {
+    __shared__ CostStats waves[kCostThreads / 64];
+    for (int off = 32; off > 0; off >>= 1) {
+        CostStats o;
+        o.value = __shfl_down(v.value, off, 64);
+        o.bad_sample = __shfl_down(v.bad_sample, off, 64);
+        o.bad_component = __shfl_down(v.bad_component, off, 64);
+        v = combine(v, o);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) waves[wave] = v;
+    __syncthreads();
+    CostStats r = empty_cost();
+    if (threadIdx.x == 0)
+        for (int w = 0; w < int(blockDim.x >> 6); ++w) r = combine(r, waves[w]);
+    return r;
+}
+
+__global__ __launch_bounds__(kCostThreads) void cost_finish_kernel(const CostStats* __restrict__ blocks, int count,
+                                                                   CostStats* __restrict__ total) {
+    CostStats v = empty_cost();
+    for (int i = threadIdx.x; i < count; i += blockDim.x) v = combine(v, blocks[i]);
+    v = block_reduce_cost(v);
+    if (threadIdx.x == 0) *total = combine(*total, v);
+}
+
+static int cost_blocks_for(int count) { return std::max(1, std::min(kMaxCostBlocks, (count + kCostThreads - 1) / kCostThreads)); }
+
+static void finish_cost(Device& d, int blocks, int cost_index) {
+    hipLaunchKernelGGL(cost_finish_kernel, 1, kCostThreads, 0, d.stream, d.cost_blocks, blocks,
+                       d.cost_totals + cost_index);
+    HIP_CHECK(hipGetLastError());
+}
+
+__global__ void clear_costs_kernel(CostStats* c, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += blockDim.x * gridDim.x) c[i] = empty_cost();
+}
+
+void launch_costs_begin(Device& d, int costs) {
+    d.reserve_costs(costs);
+    hipLaunchKernelGGL(clear_costs_kernel, 1, 256, 0, d.stream, d.cost_totals, costs);
+    HIP_CHECK(hipGetLastError());
+}
+
+// Array-matching squared loss (cuda/cost_kernels.cuh:6-35) on the output stack
+// y [point][row][outputs]; g receives dE/dy.  One lane per point.
+__global__ __launch_bounds__(kCostThreads) void matching_kernel(
+    const float* __restrict__ y, float* __restrict__ g, const float* __restrict__ target, int target_width,
+    const int* __restrict__ target_rows, const float* __restrict__ weights, int weight_samples, int R, int outputs,
+    int width, int valid, int offset, int collect, int gradient, CostStats* __restrict__ partials) {
+    CostStats local = empty_cost();
+    for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < width; p += blockDim.x * gridDim.x) {
+        float value = 0.0f;
+        for (int d = 0; d < R; ++d)
+            for (int o = 0; o < outputs; ++o) {
+                const size_t i = (size_t(p) * R + d) * outputs + o;
+                float gi = 0.0f;
+                if (p < valid) {
+                    const int wp = weight_samples == 1 ? 0 : offset + p;
+                    const float w = weights[(size_t(d) * weight_samples + wp) * outputs + o];
+                    if (w != 0.0f) {
+                        const float r = y[i] - target[(size_t(target_rows[d]) * target_width + offset + p) * outputs + o];
+                        value += w * r * r;
+                        gi = 2.0f * w * r;
+                    }
+                }
+                if (gradient) {
+                    g[i] = gi;
+                    if (p < valid && !isfinite(gi)) mark_bad(local, offset + p, d * outputs + o);
+                }
+            }
+        if (!isfinite(value)) mark_bad(local, offset + p, -1);
+        if (collect) local.value += double(value);
+    }
+    local = block_reduce_cost(local);
+    if (threadIdx.x == 0) partials[blockIdx.x] = local;
+}
+
+void launch_matching(Device& d, const Plan& p, const float* y, float* g, const float* target, int target_width,
+                     const int* target_rows, const float* weights, int weight_samples, int offset, int valid,
+                     int cost_index, bool collect, bool gradient) {
+    const int outputs = p.net->neurons.back();
+    const int blocks = cost_blocks_for(p.width);
+    hipLaunchKernelGGL(matching_kernel, blocks, kCostThreads, 0, d.stream, y, g, target, target_width, target_rows,
+                       weights, weight_samples, p.rows, outputs, p.width, valid, offset, int(collect), int(gradient),
+                       d.cost_blocks);
+    HIP_CHECK(hipGetLastError());
+    finish_cost(d, blocks, cost_index);
+}
+
+// Sparse linear/quadratic residuals (cuda/cost_kernels.cuh:37-90); component
+// index = row*outputs + output.
+__device__ __forceinline__ size_t component_at(int index, int outputs, int R, int p) {
+    return (size_t(p) * R + index / outputs) * outputs + index % outputs;
+}
+
+__global__ __launch_bounds__(kCostThreads) void polynomial_kernel(
+    const float* __restrict__ y, float* __restrict__ g, const cpde_poly_term* __restrict__ terms, int term_count,
+    const float* __restrict__ coefficients, const float* __restrict__ rhs, const float* __restrict__ weights,
+    int equations, int samples, int R, int outputs, int width, int valid, int offset, int collect, int gradient,
+    CostStats* __restrict__ partials) {
+    CostStats local = empty_cost();
+    for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < width; p += blockDim.x * gridDim.x) {
+        if (gradient)
+            for (int k = 0; k < R * outputs; ++k) g[size_t(p) * R * outputs + k] = 0.0f;
+        float total = 0.0f;
+        if (p < valid)
+            for (int e = 0; e < equations; ++e) {
+                const int sample = offset + p;
+                const float w = weights[size_t(e) * samples + sample];
+                if (w == 0.0f) continue;
+                float r = -rhs[size_t(e) * samples + sample];
+                for (int t = 0; t < term_count; ++t) {
+                    if (terms[t].equation != e) continue;
+                    const float c = coefficients[size_t(t) * samples + sample];
+                    if (c == 0.0f) continue;
+                    const float a = y[component_at(terms[t].a, outputs, R, p)];
+                    r += c * a * (terms[t].b < 0 ? 1.0f : y[component_at(terms[t].b, outputs, R, p)]);
+                }
+                total += w * r * r;
+                const float scale = 2.0f * w * r;
+                if (gradient)
+                    for (int t = 0; t < term_count; ++t) {
+                        if (terms[t].equation != e) continue;
+                        const float c = coefficients[size_t(t) * samples + sample];
+                        if (c == 0.0f) continue;
+                        if (terms[t].b < 0) {
+                            g[component_at(terms[t].a, outputs, R, p)] += scale * c;
+                        } else {
+                            g[component_at(terms[t].a, outputs, R, p)] +=
+                                scale * c * y[component_at(terms[t].b, outputs, R, p)];
+                            g[component_at(terms[t].b, outputs, R, p)] +=
+                                scale * c * y[component_at(terms[t].a, outputs, R, p)];
+                        }
+                    }
+            }
+        if (!isfinite(total)) mark_bad(local, offset + p, -1);
+        if (collect) local.value += double(total);
+        if (gradient && p < valid)
+            for (int k = 0; k < R * outputs; ++k)
+                if (!isfinite(g[size_t(p) * R * outputs + k])) mark_bad(local, offset + p, k);
+    }
+    local = block_reduce_cost(local);
+    if (threadIdx.x == 0) partials[blockIdx.x] = local;
+}
+
+void launch_polynomial(Device& d, const Plan& p, const float* y, float* g, const cpde_poly_term* terms, int term_count,
+                       const float* coefficients, const float* rhs, const float* weights, int equations, int samples,
+                       int offset, int valid, int cost_index, bool collect, bool gradient) {
+    const int outputs = p.net->neurons.back();
+    const int blocks = cost_blocks_for(p.width);
+    hipLaunchKernelGGL(polynomial_kernel, blocks, kCostThreads, 0, d.stream, y, g, terms, term_count, coefficients, rhs,
+                       weights, equations, samples, p.rows, outputs, p.width, valid, offset, int(collect),
+                       int(gradient), d.cost_blocks);
+    HIP_CHECK(hipGetLastError());
+    finish_cost(d, blocks, cost_index);
+}
+
+// Per-sample expression densities -> cost slot (cost_graph::sample_blocks,
+// cuda/cost_graph.cuh:35-43).  bad[p] == -2 means clean.
+__global__ __launch_bounds__(kCostThreads) void sample_blocks_kernel(const double* __restrict__ values,
+                                                                     const int* __restrict__ bad, int valid, int offset,
+                                                                     CostStats* __restrict__ partials) {
+    CostStats local = empty_cost();
+    for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < valid; p += blockDim.x * gridDim.x) {
+        local.value += values[p];
+        if (bad[p] != -2) mark_bad(local, offset + p, bad[p]);
+    }
+    local = block_reduce_cost(local);
+    if (threadIdx.x == 0) partials[blockIdx.x] = local;
+}
+
+void launch_sample_reduce(Device& d, const double* values, const int* bad, int valid, int offset, int cost_index) {
+    const int blocks = cost_blocks_for(valid);
+    hipLaunchKernelGGL(sample_blocks_kernel, blocks, kCostThreads, 0, d.stream, values, bad, valid, offset,
+                       d.cost_blocks);
+    HIP_CHECK(hipGetLastError());
+    finish_cost(d, blocks, cost_index);
+}
+
+__global__ void scale_adjoint_kernel(float* __restrict__ g, size_t count, const double* __restrict__ multiplier) {
+    const double m = *multiplier;
+    for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < count; i += size_t(gridDim.x) * blockDim.x)
+        g[i] = m == 0 ? 0.0f : float(g[i] * m);
+}
+
+void launch_scale_adjoint(Device& d, const Plan& p, float* g, const double* multiplier) {
+    const size_t count = p.columns() * p.net->neurons.back();
+    const int blocks = int(std::min<size_t>((count + 255) / 256, 1024));
+    hipLaunchKernelGGL(scale_adjoint_kernel, blocks, 256, 0, d.stream, g, count, multiplier);
+    HIP_CHECK(hipGetLastError());
+}
+
+// Gradient statistics (cuda/reduction_kernels.cuh:81-98): promote before squaring.
+__device__ __forceinline__ GradStats combine_grad(GradStats a, const GradStats& b) {
+    a.squared_norm += b.squared_norm;
+    if (b.max_abs > a.max_abs) a.max_abs = b.max_abs;
+    a.nonfinite += b.nonfinite;
+    if (b.first < a.first) a.first = b.first;
+    return a;
+}
+
+__device__ GradStats block_reduce_grad(GradStats v) {
+    __shared__ GradStats waves[4];
+    for (int off = 32; off > 0; off >>= 1) {
+        GradStats o;
+        o.squared_norm = __shfl_down(v.squared_norm, off, 64);
+        o.max_abs = __shfl_down(v.max_abs, off, 64);
+        o.nonfinite = __shfl_down(v.nonfinite, off, 64);
+        o.first = __shfl_down(v.first, off, 64);
+        v = combine_grad(v, o);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) waves[wave] = v;
+    __syncthreads();
+    GradStats r{0.0, 0.0, 0ull, INT_MAX, 0};
+    if (threadIdx.x == 0)
+        for (int w = 0; w < int(blockDim.x >> 6); ++w) r = combine_grad(r, waves[w]);
+    return r;
+}
+
+__global__ __launch_bounds__(256) void grad_blocks_kernel(const float* __restrict__ g, int count,
+                                                          GradStats* __restrict__ partials) {
+    GradStats local{0.0, 0.0, 0ull, INT_MAX, 0};
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += blockDim.x * gridDim.x) {
+        const double v = g[i];
+        if (!isfinite(v)) {
+            ++local.nonfinite;
+            if (i < local.first) local.first = i;
+        } else {
+            local.squared_norm += v * v;
+            const double mag = fabs(v);
+            if (mag > local.max_abs) local.max_abs = mag;
+        }
+    }
+    local = block_reduce_grad(local);
+    if (threadIdx.x == 0) partials[blockIdx.x] = local;
+}
+
+__global__ __launch_bounds__(256) void grad_finish_kernel(const GradStats* __restrict__ blocks, int count,
+                                                          GradStats* __restrict__ total) {
+    GradStats v{0.0, 0.0, 0ull, INT_MAX, 0};
+    for (int i = threadIdx.x; i < count; i += blockDim.x) v = combine_grad(v, blocks[i]);
+    v = block_reduce_grad(v);
+    if (threadIdx.x == 0) *total = v;
+}
+
+void launch_grad_stats(Device& d, const float* g, int count, int slot) {
+    const int blocks = cost_blocks_for(count);
+    hipLaunchKernelGGL(grad_blocks_kernel, blocks, 256, 0, d.stream, g, count, d.grad_blocks);
+    HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(grad_finish_kernel, 1, 256, 0, d.stream, d.grad_blocks, blocks, d.grad_totals + slot);
+    HIP_CHECK(hipGetLastError());
+}
+
+__global__ void fill_kernel(float* __restrict__ p, size_t count, float value) {
+    for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < count; i += size_t(gridDim.x) * blockDim.x)
+        p[i] = value;
+}
+
+void launch_fill(Device& d, float* p, size_t count, float value) {
+    if (!count) return;
+    const int blocks = int(std::min<size_t>((count + 255) / 256, 1024));
+    hipLaunchKernelGGL(fill_kernel, blocks, 256, 0, d.stream, p, count, value);
+    HIP_CHECK(hipGetLastError());
+}
+
+// ------------------------------------------------------------------------------------------
+// Optimizers: one launch covers every transition.  Each transition's buffers
+// are separate allocations; the launch carries their pointers by value.
+struct OptimizerArgs {
+    float* W[kMaxTransitions];
+    float* S[kMaxTransitions];   // RPROP step / Adam first moment
+    float* Ga[kMaxTransitions];  // active gradient
+    float* Gi[kMaxTransitions];  // inactive gradient / Adam second moment
+    int begin[kMaxTransitions + 1];
+    int transitions;
+};
+
+__device__ __forceinline__ int find_transition(const OptimizerArgs& a, int i) {
+    int t = 0;
+    while (t + 1 < a.transitions && i >= a.begin[t + 1]) ++t;
+    return t;
+}
+
+// Resile_k (cuda/derivative_kernels_v4.cu:752-778), sign tests on float products.
+__global__ void rprop_kernel(OptimizerArgs a) {
+    const int total = a.begin[a.transitions];
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += blockDim.x * gridDim.x) {
+        const int t = find_transition(a, i), j = i - a.begin[t];
+        float* W = a.W[t] + j;
+        float* step = a.S[t] + j;
+        float* ga = a.Ga[t] + j;
+        const float gi = a.Gi[t][j];
+        const float g = *ga;
+        const float prod = __fmul_rn(g, gi);
+        float s = *step;
+        if (prod > 0) s *= 1.2f;
+        const float nW = *W - copysignf(s, g);
+        if (prod < 0) {
+            *W = *W + copysignf(s, gi);
+            s *= 0.5f;
+            *ga = 0.0f;
+        } else if (g != 0.0f) {
+            if (fabsf(nW) <= 20.0f) *W = nW;
+            else {
+                s = 0.1f;
+                *ga = 0.0f;
+            }
+        }
+        *step = s;
+    }
+}
+
+// ADAM_k (cuda/derivative_kernels_v4.cu:780-799); M in S, V in the inactive buffer.
+__global__ void adam_kernel(OptimizerArgs a, float lr, float beta1, float beta2, float beta1t, float beta2t) {
+    const int total = a.begin[a.transitions];
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += blockDim.x * gridDim.x) {
+        const int t = find_transition(a, i), j = i - a.begin[t];
+        const float g = a.Ga[t][j];
+        float m = a.S[t][j], v = a.Gi[t][j];
+        m = __fadd_rn(__fmul_rn(beta1, m), __fmul_rn(1 - beta1, g));
+        v = __fadd_rn(__fmul_rn(beta2, v), __fmul_rn(__fmul_rn(1 - beta2, g), g));
+        a.S[t][j] = m;
+        a.Gi[t][j] = v;
+        const float mh = m / (1 - beta1t), vh = v / (1 - beta2t);
+        const float nW = float(double(a.W[t][j]) - double(lr * mh) / (double(sqrtf(vh)) + 1e-8));
+        if (fabsf(nW) <= 20.0f) a.W[t][j] = nW;
+    }
+}
+
+// Set_Resile_k / Reset_Resile_k (cuda/derivative_kernels_v4.cu:801-832).
+__global__ void steps_kernel(OptimizerArgs a, float value, int floor_mode) {
+    const int total = a.begin[a.transitions];
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += blockDim.x * gridDim.x) {
+        const int t = find_transition(a, i), j = i - a.begin[t];
+        if (!floor_mode || a.S[t][j] < value) {
+            a.S[t][j] = value;
+            a.Ga[t][j] = 0.0f;
+            a.Gi[t][j] = 0.0f;
+        }
+    }
+}
+
+template <class F>
+static void for_transition_groups(Net& net, F launch) {
+    const int T = net.layers - 1;
+    for (int first = 0; first < T; first += kMaxTransitions) {
+        OptimizerArgs a{};
+        a.transitions = std::min(kMaxTransitions, T - first);
+        a.begin[0] = 0;
+        for (int k = 0; k < a.transitions; ++k) {
+            const int t = first + k;
+            const int act = net.active[t], inact = act == 1 ? 2 : 1;
+            a.W[k] = net.state[0][t];
+            a.S[k] = net.state[3][t];
+            a.Ga[k] = net.state[act][t];
+            a.Gi[k] = net.state[inact][t];
+            a.begin[k + 1] = a.begin[k] + net.param_count(t);
+        }
+        const int blocks = std::max(1, std::min(1024, (a.begin[a.transitions] + 255) / 256));
+        launch(a, blocks);
+    }
+}
+
+void launch_rprop(Device& d, Net& net) {
+    for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
+        hipLaunchKernelGGL(rprop_kernel, blocks, 256, 0, d.stream, a);
+        HIP_CHECK(hipGetLastError());
+    });
+    for (auto& act : net.active) act = act == 1 ? 2 : 1;
+}
+
+void launch_adam(Device& d, Net& net, int step, float lr) {
+    const float b1 = 0.9f, b2 = 0.999f;
+    const float b1t = std::pow(b1, float(step)), b2t = std::pow(b2, float(step));
+    for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
+        hipLaunchKernelGGL(adam_kernel, blocks, 256, 0, d.stream, a, lr, b1, b2, b1t, b2t);
+        HIP_CHECK(hipGetLastError());
+    });
+}
+
+void launch_set_steps(Device& d, Net& net, float value) {
+    for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
+        hipLaunchKernelGGL(steps_kernel, blocks, 256, 0, d.stream, a, value, 0);
+        HIP_CHECK(hipGetLastError());
+    });
+}
+
+void launch_restore_steps(Device& d, Net& net, float floor_value) {
+    for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
+        hipLaunchKernelGGL(steps_kernel, blocks, 256, 0, d.stream, a, floor_value, 1);
+        HIP_CHECK(hipGetLastError());
+    });
+}
+
+// ------------------------------------------------------------------------------------------
+// Scalar cost graph on one lane (cost_graph::execute, cuda/cost_graph.cuh:6-27;
+// opcode semantics cuda/scalar_ops.cuh:5-26).
+enum { kConstant, kLeaf, kField, kAdd, kSub, kMul, kDiv, kPower, kNeg, kExp, kLog, kSqrt, kSin, kCos, kTanh, kAttach };
+
+__device__ double scalar_value(int op, double a, double b, double p) {
+    switch (op) {
+    case kConstant: return p;
+    case kAdd: return a + b;
+    case kSub: return a - b;
+    case kMul: return a * b;
+    case kDiv: return b == 0 ? NAN : a / b;
+    case kPower: return ((a < 0 && floor(p) != p) || (a == 0 && p < 0)) ? NAN : pow(a, p);
+    case kNeg: return -a;
+    case kExp: return exp(a);
+    case kLog: return a > 0 ? log(a) : NAN;
+    case kSqrt: return a >= 0 ? sqrt(a) : NAN;
+    case kSin: return sin(a);
+    case kCos: return cos(a);
+    case kTanh: return tanh(a);
+    case kAttach: return a;
+    default: return NAN;
+    }
+}
+
+__device__ void scalar_partials(int op, double a, double b, double v, double p, double& da, double& db) {
+    da = db = 0;
+    switch (op) {
+    case kAdd:
+    case kAttach: da = db = 1; break;
+    case kSub: da = 1; db = -1; break;
+    case kMul: da = b; db = a; break;
+    case kDiv: da = 1 / b; db = -v / b; break;
+    case kPower: da = p == 0 ? 0 : (p == 1 ? 1 : p * pow(a, p - 1)); break;
+    case kNeg: da = -1; break;
+    case kExp: da = v; break;
+    case kLog: da = 1 / a; break;
+    case kSqrt: da = .5 / v; break;
+    case kSin: da = cos(a); break;
+    case kCos: da = -sin(a); break;
+    case kTanh: da = 1 - v * v; break;
+    default: break;
+    }
+}
+
+__global__ void graph_kernel(const cpde_scalar_node* __restrict__ nodes, int count, int root,
+                             const CostStats* __restrict__ integrals, int leaves, double* values, double* adjoints,
+                             double* multipliers, int* active, cpde_graph_summary* summary, int gradient) {
+    if (blockIdx.x || threadIdx.x) return;
+    summary->bad_node = -1;
+    summary->value = 0;
+    for (int i = 0; i < leaves; ++i) multipliers[i] = 0;
+    for (int i = 0; i < count; ++i) {
+        const cpde_scalar_node n = nodes[i];
+        adjoints[i] = 0;
+        active[i] = n.op == kLeaf;
+        if (n.op == kLeaf) values[i] = integrals[n.a].value;
+        else {
+            values[i] = scalar_value(n.op, n.a < 0 ? 0 : values[n.a], n.b < 0 ? 0 : values[n.b], n.parameter);
+            if (n.op > 2) active[i] = active[n.a] || ((n.op <= kDiv || n.op == kAttach) && active[n.b]);
+        }
+        if (!isfinite(values[i]) && summary->bad_node < 0) summary->bad_node = i;
+    }
+    summary->value = values[root];
+    if (!gradient || summary->bad_node >= 0) return;
+    adjoints[root] = 1;
+    for (int i = count - 1; i >= 0; --i) {
+        const cpde_scalar_node n = nodes[i];
+        const double seed = adjoints[i];
+        if (seed == 0 || !active[i]) continue;
+        if (n.op == kLeaf) multipliers[n.a] += seed;
+        else if (n.op > 2) {
+            double a, b;
+            scalar_partials(n.op, values[n.a], n.b < 0 ? 0 : values[n.b], values[i], n.parameter, a, b);
+            if (active[n.a]) adjoints[n.a] += seed * a;
+            if ((n.op <= kDiv || n.op == kAttach) && active[n.b]) adjoints[n.b] += seed * b;
+        }
+        if (!isfinite(seed) && summary->bad_node < 0) summary->bad_node = i;
+    }
+    for (int i = 0; i < leaves; ++i)
+        if (!isfinite(multipliers[i])) summary->bad_node = root;
+}
+
+void launch_graph(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,
+                  double* adjoints, double* multipliers, int* active, cpde_graph_summary* summary, bool gradient) {
+    hipLaunchKernelGGL(graph_kernel, 1, 1, 0, d.stream, nodes, count, root, d.cost_totals, leaves, values, adjoints,
+                       multipliers, active, summary, int(gradient));
+    HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace cpde

@@ -1,0 +1,304 @@
+"""Synthetic workloads: derivative schemas, input stacks, targets and weights.
+
+Schemas follow the reference's ``table`` ordering: every sub-multi-index of a
+requested derivative is included and rows sort by (order, count tuple)
+(cpde/quadrature.py:16-38, closure semantics cpde/_prepare.py:84-90).
+
+Input stacks put coordinates in the value row, unit vectors in the first-order
+rows and zeros above (scripts/benchmark_fourier_performance.py:47-50).
+
+The named workloads are:
+  * ``fourier_fit``: 2->128^4->1 on a 27x27 grid in [0,1]^2, a seeded Fourier sum
+    target with analytic derivatives, Xavier-uniform weights (seed 3407), matching
+    weights 1/var per row; order 2 and order 6 variants;
+  * ``poisson_disk``: 2->64^3->1, 64 Gauss-Legendre radii x 64 angles interior
+    quadrature plus 256 boundary points, residual u_xx+u_yy+f;
+  * ``fourier_3d``: 3->128^5->1 on a 32^3 grid, all mixed partials through order 4;
+  * ``fourier_large``: 2->256^4->1 on a 512x512 grid, order 6, chunked;
+  * ``reference_benchmark(order)``: the reference's published Fourier benchmark
+    workload (scripts/benchmark_fourier_performance.py:20-38 and the Python
+    initialiser cpde/api.py:277-280), used to pin the published losses.
+"""
+from __future__ import annotations
+
+import itertools
+import math
+
+import numpy as np
+
+
+# ----------------------------------------------------------------------------- schemas
+def full_schema(variables, order):
+    """All multi-indices of total order <= ``order`` in ``variables`` variables,
+    rows (order, counts...) sorted by (order, counts)."""
+    counts = [c for c in itertools.product(range(order + 1), repeat=variables) if sum(c) <= order]
+    counts.sort(key=lambda c: (sum(c), c))
+    return np.array([(sum(c), *c) for c in counts], np.int32)
+
+
+def closed_schema(variables, requested):
+    """Closure of explicit count tuples (value row always included)."""
+    keys = {(0,) * variables}
+    for key in requested:
+        keys.update(itertools.product(*(range(c + 1) for c in key)))
+    rows = sorted(keys, key=lambda c: (sum(c), c))
+    return np.array([(sum(c), *c) for c in rows], np.int32)
+
+
+def input_stack(points, schema):
+    """(rows, channels=variables, points) stack for an identity input layer."""
+    pts = np.asarray(points, np.float64)
+    n, v = pts.shape
+    a = np.zeros((len(schema), v, n), np.float32)
+    for r, row in enumerate(schema):
+        if row[0] == 0:
+            a[r] = pts.T
+        elif row[0] == 1:
+            a[r] = np.asarray(row[1:], np.float32)[:, None]
+    return a
+
+
+# ----------------------------------------------------------------------------- weights
+def xavier_weights(neurons, seed=3407):
+    """Column-major n_out x (n_in+1) blocks, Xavier-uniform weights, zero biases."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for n_in, n_out in zip(neurons, neurons[1:]):
+        bound = math.sqrt(6.0 / (n_in + n_out))
+        w = rng.uniform(-bound, bound, n_out * n_in)
+        out.append(np.concatenate((w, np.zeros(n_out))).astype(np.float32))
+    return out
+
+
+def reference_init(neurons, seed):
+    """The reference Python initialiser: U(+-2/sqrt(fan_in)) weights column-major,
+    then U(+-0.1) biases (cpde/api.py:277-280)."""
+    rng = np.random.default_rng(seed)
+    return [np.concatenate((rng.uniform(-2 / np.sqrt(w), 2 / np.sqrt(w), h * w),
+                            rng.uniform(-.1, .1, h))).astype(np.float32)
+            for w, h in zip(neurons, neurons[1:])]
+
+
+def linear_flags(neurons):
+    return [1] + [0] * (len(neurons) - 2) + [1]
+
+
+# ----------------------------------------------------------------------------- targets
+def fourier_modes(variables, modes, max_frequency, seed=2026):
+    rng = np.random.default_rng(seed)
+    freq = rng.integers(1, max_frequency + 1, size=(modes, variables))
+    coef = rng.standard_normal(modes)
+    phase = rng.uniform(0, 2 * np.pi, size=(modes, variables))
+    return freq, coef, phase
+
+
+def fourier_target(points, schema, freq, coef, phase):
+    """u = sum_m c_m prod_v sin(f_mv x_v + phi_mv); d^alpha multiplies by f^alpha and
+    shifts each phase by alpha_v * pi/2.  Returns (rows, points) float64."""
+    pts = np.asarray(points, np.float64)
+    out = np.zeros((len(schema), len(pts)))
+    for r, row in enumerate(schema):
+        alpha = row[1:]
+        for m in range(len(coef)):
+            term = np.full(len(pts), coef[m])
+            for v in range(pts.shape[1]):
+                term = term * freq[m, v] ** alpha[v] * np.sin(freq[m, v] * pts[:, v] + phase[m, v] + alpha[v] * np.pi / 2)
+            out[r] += term
+    return out
+
+
+def uniform_grid(n, dims):
+    axes = [np.linspace(0, 1, n)] * dims
+    mesh = np.meshgrid(*axes, indexing='ij')
+    return np.column_stack([m.ravel() for m in mesh])
+
+
+class MatchingWorkload:
+    """Everything a matching-cost run needs, in protocol layouts."""
+
+    def __init__(self, name, neurons, points, schema, target, weights, init, chunk=0):
+        self.name, self.neurons = name, list(neurons)
+        self.linear = linear_flags(neurons)
+        self.points = np.asarray(points, np.float32)
+        self.schema = schema
+        self.inputs = input_stack(self.points, schema)
+        self.target = np.asarray(target, np.float32)            # (rows, points)
+        self.row_weights = np.asarray(weights, np.float32)      # (rows,)
+        self.init = init
+        self.chunk = chunk
+
+    @property
+    def rows(self):
+        return len(self.schema)
+
+    @property
+    def size(self):
+        return len(self.points)
+
+    def flops_per_epoch(self):
+        """Algorithmic GEMM flops: forward + transposed (not the input layer) + wgrad."""
+        pairs = list(zip(self.neurons, self.neurons[1:]))
+        rp = self.rows * self.size
+        fwd = sum(a * b for a, b in pairs)
+        return 2 * rp * (fwd + sum(a * b for a, b in pairs[1:]) + fwd)
+
+    def bytes_per_epoch(self):
+        """Algorithmic HBM bytes: per hidden layer composition (read z, write y) and
+        adjoint (read z, read g_y, write g_z) = 5n floats per row-point, the output
+        cost 3*n_out, and RPROP 28 bytes per parameter."""
+        rp = self.rows * self.size
+        hidden = sum(self.neurons[1:-1])
+        params = sum(b * (a + 1) for a, b in zip(self.neurons, self.neurons[1:]))
+        return 4 * rp * (5 * hidden + 3 * self.neurons[-1]) + 28 * params
+
+    def upload(self, session, chunk=None):
+        """Creates data, target, network and cost objects; returns their ids."""
+        d = session.data(self.inputs, self.schema)
+        t = session.data(self.target[:, None, :], self.schema)
+        n = session.network(self.neurons, self.linear, self.init)
+        rows = list(range(self.rows))
+        c = session.matching_cost(n, d, t, rows, rows, self.row_weights[:, None, None], 1,
+                                  self.chunk if chunk is None else chunk)
+        return dict(data=d, target=t, net=n, cost=c)
+
+
+def fourier_fit(order=6, grid=27, neurons=(2, 128, 128, 128, 128, 1), modes=8, max_frequency=4, seed=3407):
+    schema = full_schema(2, order)
+    pts = uniform_grid(grid, 2)
+    freq, coef, phase = fourier_modes(2, modes, max_frequency)
+    target = fourier_target(pts, schema, freq, coef, phase)
+    weights = 1.0 / target.var(axis=1)
+    return MatchingWorkload(f'fourier_fit_order{order}', neurons, pts, schema, target, weights,
+                            xavier_weights(neurons, seed))
+
+
+def fourier_3d(grid=32, order=4, neurons=(3, 128, 128, 128, 128, 128, 1), modes=12, max_frequency=3, points=None):
+    schema = full_schema(3, order)
+    pts = uniform_grid(grid, 3)
+    if points is not None:
+        pts = pts[np.linspace(0, len(pts) - 1, points).astype(int)]
+    freq, coef, phase = fourier_modes(3, modes, max_frequency)
+    target = fourier_target(pts, schema, freq, coef, phase)
+    return MatchingWorkload('fourier_3d_order4', neurons, pts, schema, target, 1.0 / target.var(axis=1),
+                            xavier_weights(neurons))
+
+
+def fourier_large(grid=512, order=6, neurons=(2, 256, 256, 256, 256, 1), modes=16, chunk=65536, points=None):
+    schema = full_schema(2, order)
+    pts = uniform_grid(grid, 2)
+    if points is not None:
+        pts = pts[np.linspace(0, len(pts) - 1, points).astype(int)]
+    freq, coef, phase = fourier_modes(2, modes, 4)
+    target = fourier_target(pts, schema, freq, coef, phase)
+    return MatchingWorkload('fourier_large_order6', neurons, pts, schema, target, 1.0 / target.var(axis=1),
+                            xavier_weights(neurons), chunk=min(chunk, len(pts)))
+
+
+def reference_benchmark(order):
+    """The published benchmark workload: 27x27 grid in [-1,1]^2, 10x10 Fourier
+    coefficient grid (seed 2026), rows weighted by 1/var, reference initialiser
+    with seed 3407 (scripts/benchmark_fourier_performance.py:20-57)."""
+    neurons = [2, 128, 128, 128, 128, 1]
+    schema = closed_schema(2, [(i, order - i) for i in range(order + 1)])
+    x, y = np.meshgrid(np.linspace(-1, 1, 27), np.linspace(-1, 1, 27), indexing='ij')
+    pts = np.column_stack((x.ravel(), y.ravel())).astype(np.float32)
+    xd, yd = pts.astype(float).T
+    coef = np.random.default_rng(2026).uniform(-1, 1, (4, 10, 10))
+    target = np.zeros((len(schema), len(pts)))
+    for row, (_, dx, dy) in enumerate(schema):
+        for n in range(1, 11):
+            for k in range(1, 11):
+                a, b, c, d = coef[:, n - 1, k - 1] * n ** int(dx) * k ** int(dy) / (n * k)
+                sx, cx = np.sin(n * xd + dx * np.pi / 2), np.cos(n * xd + dx * np.pi / 2)
+                sy, cy = np.sin(k * yd + dy * np.pi / 2), np.cos(k * yd + dy * np.pi / 2)
+                target[row] += a * sx * sy + b * sx * cy + c * cx * sy + d * cx * cy
+    weights = (1 / target.std(axis=1) ** 2).astype(np.float32)
+    return MatchingWorkload(f'reference_fourier_order{order}', neurons, pts, schema, target.astype(np.float32),
+                            weights, reference_init(neurons, 3407))
+
+
+# Published losses at initial weights for reference_benchmark(order), RTX 3090 CUDA
+# build (docs/benchmarks/fourier-rtx3090.json:159,189,219,249,279,309,339).
+PUBLISHED_LOSSES = [1519.6657229734592, 2989.1356939971447, 5187.967334091663, 8111.595301151276,
+                    11767.45415353775, 16145.947476387024, 21259.16511631012]
+
+
+# ----------------------------------------------------------------------------- Poisson
+def disk_quadrature(radial=64, angular=64):
+    """Interior: Gauss-Legendre radii r=(t+1)/2 with weight (w/2) r (2 pi/angular),
+    uniform angles.  Returns points (N,2) and weights (N,)."""
+    t, w = np.polynomial.legendre.leggauss(radial)
+    r = (t + 1) / 2
+    wr = w / 2 * r
+    th = 2 * np.pi * np.arange(angular) / angular
+    R, T = np.meshgrid(r, th, indexing='ij')
+    W = np.repeat(wr, angular) * (2 * np.pi / angular)
+    pts = np.column_stack(((R * np.cos(T)).ravel(), (R * np.sin(T)).ravel()))
+    return pts, W
+
+
+def circle_points(count=256):
+    th = 2 * np.pi * np.arange(count) / count
+    return np.column_stack((np.cos(th), np.sin(th))), np.full(count, 2 * np.pi / count)
+
+
+def gaussian_source(points, count=4, seed=2026):
+    rng = np.random.default_rng(seed)
+    amp = rng.standard_normal(count)
+    rad = 0.5 * np.sqrt(rng.uniform(0, 1, count))
+    ang = rng.uniform(0, 2 * np.pi, count)
+    centres = np.column_stack((rad * np.cos(ang), rad * np.sin(ang)))
+    width = rng.uniform(0.15, 0.3, count)
+    p = np.asarray(points, np.float64)
+    f = np.zeros(len(p))
+    for a, c, s in zip(amp, centres, width):
+        f += a * np.exp(-np.sum((p - c) ** 2, axis=1) / (2 * s * s))
+    return f
+
+
+class PoissonWorkload:
+    """Config: 2->64^3->1 sigmoid; interior cost (u_xx+u_yy+f)^2 with quadrature
+    weights, boundary cost u^2; the graph root is their sum."""
+
+    def __init__(self, neurons=(2, 64, 64, 64, 1), radial=64, angular=64, boundary=256, seed=3407):
+        self.neurons = list(neurons)
+        self.linear = linear_flags(neurons)
+        self.interior, self.interior_w = disk_quadrature(radial, angular)
+        self.boundary, self.boundary_w = circle_points(boundary)
+        self.f = gaussian_source(self.interior)
+        self.schema = closed_schema(2, [(2, 0), (0, 2)])   # rows: 1, y, x, yy, xx
+        self.init = xavier_weights(neurons, seed)
+
+    def row_of(self, counts):
+        for r, row in enumerate(self.schema):
+            if tuple(row[1:]) == tuple(counts):
+                return r
+        raise KeyError(counts)
+
+    def interior_ir(self):
+        """(u_xx + u_yy + f)**2: components index row*outputs + output."""
+        xx, yy = self.row_of((2, 0)), self.row_of((0, 2))
+        nodes = [(1, xx, 0), (1, yy, 0), (3, 0, 1), (2, 0, 0), (3, 2, 3), (7, 4, 0)]
+        consts = [0, 0, 0, 0, 0, 2.0]
+        return nodes, consts
+
+    @staticmethod
+    def boundary_ir():
+        return [(1, 0, 0), (7, 0, 0)], [0, 2.0]
+
+    @staticmethod
+    def graph():
+        """Root = leaf0 + leaf1."""
+        from .wire import graph_bytes
+        return graph_bytes([(1, 0, 0), (1, 1, 0), (3, 0, 1)], [0.0, 0.0, 0.0], 2)
+
+    def upload(self, session):
+        vschema = closed_schema(2, [])
+        di = session.data(input_stack(self.interior, self.schema), self.schema)
+        db = session.data(input_stack(self.boundary, vschema), vschema)
+        n = session.network(self.neurons, self.linear, self.init)
+        nodes, consts = self.interior_ir()
+        ci = session.integral_cost(n, di, nodes, consts, self.f[None, :], self.interior_w)
+        bnodes, bconsts = self.boundary_ir()
+        cb = session.integral_cost(n, db, bnodes, bconsts, np.zeros((0, len(self.boundary))), self.boundary_w)
+        return dict(interior=di, boundary=db, net=n, costs=[ci, cb])

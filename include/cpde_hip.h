@@ -1,0 +1,202 @@
+/*
+ * cpde_hip.h -- C ABI of the MI355X (gfx950) cPDE device library, libcpde_hip.so.
+ *
+ * The reference drives its kernels through an in-source operator seam: the
+ * CPDE_LAUNCH macro plus the cuBLAS/CUB/runtime subset that cpu/include/
+ * substitutes (cuda/backend_launch.hpp:1-10, cpu/include/cublas_v2.h:23-83,
+ * cpu/include/cub/device/device_reduce.cuh:1-16).  This header sits at that seam:
+ * the host server (cpde_amd/csrc/server.cpp) calls only these entry points, the
+ * way the reference's Server calls its network/Workspace methods.  Plain
+ * pointers and sizes only; every pointer documented "device" is device memory
+ * obtained from cpde_buffer_alloc (or a network/plan accessor).
+ *
+ * Error convention (the reference's: cuda/cuda_check_v1.cuh:36-47 exits on a
+ * device fault; validation errors become kind-1 frames, cuda/cpde_server.cu:22):
+ *   CPDE_OK         success
+ *   CPDE_EINVAL     invalid argument -- the host reports it and keeps all state
+ *   CPDE_EDEVICE    HIP runtime or kernel failure -- the host prints and exits
+ *   CPDE_ECOMPILE   hipRTC rejected a generated expression kernel
+ * cpde_last_error() returns the message of the calling thread's last failure.
+ *
+ * Layouts.  A stack holds, for one layer, every derivative row of every point of
+ * a chunk: [point][row][neuron], neuron fastest.  Wire data (protocol op 2) is
+ * [row][sample][channel].  A weight block is n_out x (n_in+1), column-major,
+ * bias in the last column (cuda/cpde_engine.cuh:622-639).
+ */
+#ifndef CPDE_HIP_H
+#define CPDE_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CPDE_OK 0
+#define CPDE_EINVAL 1
+#define CPDE_EDEVICE 2
+#define CPDE_ECOMPILE 4
+
+typedef struct cpde_device_s cpde_device;
+typedef struct cpde_net_s cpde_net;
+typedef struct cpde_plan_s cpde_plan;
+typedef struct cpde_program_s cpde_program;
+
+/* Per-cost reduction result: signed double sum and the first bad (sample,
+ * component); component -1 means the objective itself
+ * (cuda/reduction_kernels.cuh:28-46).  INT32_MAX marks "no bad value". */
+typedef struct {
+    double value;
+    int32_t bad_sample;
+    int32_t bad_component;
+} cpde_cost_stats;
+
+/* Per-layer gradient statistics (cuda/reduction_kernels.cuh:53-58,81-98). */
+typedef struct {
+    double squared_norm;
+    double max_abs;
+    uint64_t nonfinite_count;
+    int32_t first_nonfinite;
+    int32_t pad_;
+} cpde_gradient_stats;
+
+/* Sparse polynomial residual term (cuda/cost_kernels.cuh:37): b = -1 is linear. */
+typedef struct {
+    int32_t equation, a, b;
+} cpde_poly_term;
+
+/* Scalar graph node (cuda/scalar_ops.cuh:6). */
+typedef struct {
+    int32_t op, a, b, pad_;
+    double parameter;
+} cpde_scalar_node;
+
+/* Scalar graph result (cuda/cost_graph.cuh:6). */
+typedef struct {
+    double value;
+    int32_t bad_node;
+    int32_t pad_;
+} cpde_graph_summary;
+
+const char* cpde_last_error(void);
+
+/* ---- device, stream and buffers (replaces cudaSetDevice/cudaStreamCreate/
+ *      cudaMalloc/cudaMemcpy uses, cuda/cpde_engine.cuh:23-87, cuda/cpde_server.cu:26-33) */
+int cpde_device_open(int ordinal, cpde_device** out);
+int cpde_device_close(cpde_device* dev);
+int cpde_device_synchronize(cpde_device* dev);
+/* Name and compute-unit count of the open device. */
+int cpde_device_info(cpde_device* dev, char* name, size_t capacity, int* compute_units);
+int cpde_buffer_alloc(cpde_device* dev, size_t bytes, void** out);
+int cpde_buffer_free(cpde_device* dev, void* ptr);
+/* Synchronous copies in stream order. */
+int cpde_buffer_upload(cpde_device* dev, void* dst, const void* src, size_t bytes);
+int cpde_buffer_download(cpde_device* dev, void* dst, const void* src, size_t bytes);
+int cpde_buffer_copy(cpde_device* dev, void* dst, const void* src, size_t bytes);
+
+/* ---- network: weights and optimizer state (class weights/network,
+ *      cuda/cpde_engine.cuh:562-659,782-850; op 3 cuda/cpde_server.cu:455-473).
+ * initial[t] is the n_{t+1} x (n_t+1) block of transition t (may be NULL: zeros).
+ * Gradient buffers start at zero and the RPROP step at 0.002. */
+int cpde_net_create(cpde_device* dev, int layers, const int* neurons, const int* linear,
+                    const float* const* initial, cpde_net** out);
+int cpde_net_destroy(cpde_net* net);
+/* Device pointer and element count of state buffer b of transition t:
+ * 0 weights, 1 and 2 the gradient ping-pong pair, 3 RPROP step / Adam first moment. */
+int cpde_net_state(cpde_net* net, int transition, int buffer, float** device_ptr, int* count);
+/* The active gradient buffer (1 or 2) of a transition (weights::act_grad). */
+int cpde_net_active(cpde_net* net, int transition);
+int cpde_net_set_active(cpde_net* net, int transition, int active);
+/* Incremented whenever the network's stack arena is reallocated (all plans'
+ * stacks are then undefined until the next cpde_activate). */
+uint64_t cpde_net_generation(cpde_net* net);
+
+/* ---- plans: one derivative schema x chunk width x backward flag over a network
+ *      (class context + stack + derivative_tables, cuda/cpde_engine.cuh:391-560;
+ *      Server::prepare, cuda/cpde_server.cu:148-157).
+ * table: rows x (variables+1), row-major (order, counts...); orders sorted,
+ * value row first, order <= 6. */
+int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, int width, int backward,
+                     cpde_plan** out);
+int cpde_plan_destroy(cpde_plan* plan);
+/* Device pointer of a plan's stack: kind 0 = z (layer 0: the input), 1 = y
+ * (sigmoid activations), 2 = adjoint dE/dz.  Layout [point][row][neuron]. */
+int cpde_plan_stack(cpde_plan* plan, int layer, int kind, float** device_ptr);
+
+/* ---- hot path ---------------------------------------------------------------------- */
+/* Server::activate (cuda/cpde_server.cu:158-170): copy the chunk's rows of wire
+ * data [data_rows][data_width][channels] (device) into layer 0, rows[r] (host)
+ * selecting the data row of plan row r; lanes [valid, width) are zeroed. */
+int cpde_activate(cpde_plan* plan, const float* data, int data_width, const int* rows, int offset, int valid);
+/* network::feedforward (cuda/cpde_engine.cuh:889-913): every layer's linear step
+ * (fp32 MFMA, bias on the value row) and sigmoid composition through order 6. */
+int cpde_forward(cpde_plan* plan);
+/* Copy the output stack's valid lanes to wire layout dest [dest_rows][dest_width][n_out]
+ * (device), plan row r going to dest row rows[r] (Server::evaluate :171-183). */
+int cpde_output(cpde_plan* plan, float* dest, int dest_width, const int* rows, int offset, int valid);
+
+/* Reset cost slots [0, costs) (Workspace::begin, cuda/reduction_kernels.cuh:149-152). */
+int cpde_costs_begin(cpde_device* dev, int costs);
+/* Array-matching squared loss (cuda/cost_kernels.cuh:6-35) fused with its
+ * deterministic reduction into cost slot cost_index.  target: device wire data
+ * [target_rows_total][target_width][n_out]; target_rows, weights: device. */
+int cpde_cost_matching(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
+                       const float* weights, int weight_samples, int offset, int valid, int cost_index,
+                       int collect, int gradient);
+/* Sparse linear/quadratic residual cost (cuda/cost_kernels.cuh:37-90); all device. */
+int cpde_cost_polynomial(cpde_plan* plan, const cpde_poly_term* terms, int term_count, const float* coefficients,
+                         const float* rhs, const float* weights, int equations, int samples, int offset, int valid,
+                         int cost_index, int collect, int gradient);
+/* dE/dY *= multiplier for graph leaves (cuda/cost_graph.cuh:29-34); device scalar. */
+int cpde_scale_adjoint(cpde_plan* plan, const double* multiplier);
+/* network::backprop (cuda/cpde_engine.cuh:947-991): adjoint compositions, the
+ * transposed products and the weight+bias gradient contraction (deterministic
+ * split-K).  accumulate=0 overwrites the active gradient, 1 adds to it. */
+int cpde_backward(cpde_plan* plan, int accumulate);
+
+/* ---- reductions, validation data and optimizer ------------------------------------- */
+/* Per-transition statistics of the active gradient into slot t (inspect_gradients). */
+int cpde_inspect_gradients(cpde_net* net);
+/* Synchronous download of cost slots and gradient-statistics slots (Workspace::download). */
+int cpde_scalars_download(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
+                          cpde_gradient_stats* gradient_out);
+/* RPROP over every transition, then switch the active gradient buffer
+ * (Resile_k + switch_active, cuda/derivative_kernels_v4.cu:752-778). */
+int cpde_rprop(cpde_net* net);
+/* Adam step `step` (>= 1) with learning rate lr (ADAM_k, :780-799). */
+int cpde_adam(cpde_net* net, int step, float lr);
+/* Set every step to value and clear both histories (Set_Resile_k, :825-832). */
+int cpde_set_steps(cpde_net* net, float value);
+/* Raise steps below floor to floor, clearing that entry's histories (Reset_Resile_k). */
+int cpde_restore_steps(cpde_net* net, float floor_value);
+/* Zero the active gradient (graph passes, cuda/cpde_server.cu:278). */
+int cpde_zero_gradient(cpde_net* net);
+/* Zero gradients and steps/moments, active = 1 (Server::reset, :184-192). */
+int cpde_reset_optimizer(cpde_net* net);
+
+/* ---- scalar-expression costs: generated source compiled with hipRTC for gfx950
+ *      (cuda/expression_program.hpp:96-131 used NVRTC) and the scalar cost graph. */
+int cpde_program_compile(cpde_device* dev, const char* source, cpde_program** out, char* log, size_t log_capacity);
+int cpde_program_destroy(cpde_program* program);
+/* Per-sample expression over the plan's output stack, then its deterministic
+ * reduction into cost slot cost_index.  fields [F][samples], quadrature_weights
+ * [samples] (device, double); multiplier: device double or NULL;
+ * scratch: device, 2*width doubles' worth (values + flags). */
+int cpde_cost_expression(cpde_plan* plan, cpde_program* program, const double* fields,
+                         const double* quadrature_weights, int samples, int offset, int valid,
+                         const double* multiplier, void* scratch, int cost_index, int collect, int gradient);
+/* cost_graph::execute (cuda/cost_graph.cuh:6-27) on one lane: reads cost slots,
+ * writes values/adjoints/multipliers/active (device) and the summary (device). */
+int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int count, int root, int leaves,
+                       double* values, double* adjoints, double* multipliers, int* active,
+                       cpde_graph_summary* summary, int gradient);
+
+/* ---- timing ---------------------------------------------------------------------- */
+/* Record an event on the device stream; elapsed milliseconds between two marks. */
+int cpde_mark(cpde_device* dev, int slot);
+int cpde_elapsed(cpde_device* dev, int from_slot, int to_slot, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,25 @@
+import os
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+for p in (ROOT, ROOT / 'oracle'):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+
+def pytest_configure(config):
+    config.addinivalue_line('markers', 'gpu: needs an MI355X; drives the HIP library through its C ABI')
+    config.addinivalue_line('markers', 'slow: long CPU-side oracle run')
+
+
+@pytest.fixture(scope='session')
+def device():
+    from cpde_amd import hip
+    d = hip.Device(int(os.environ.get('CPDE_TEST_DEVICE', '0')))
+    name, cus = d.info()
+    print(f'\n[device] {name} CUs={cus}', flush=True)
+    yield d
+    d.close()

@@ -1,0 +1,133 @@
+"""Kernel-level parity of the HIP path against the oracle, through the C ABI.
+
+Tolerances (fp32 on both sides, different summation orders):
+  * linear step:            scaled error <= 2e-5 against a float64 product;
+  * composition / adjoint:  scaled error <= 1e-4 against the oracle on the same
+                            GPU-produced z (error relative to max(|x|, row rms));
+  * epoch:                  loss rel <= 1e-4, outputs and gradients rel-L2 <= 1e-3
+                            (the order-6 bar), typically ~1e-6.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from cpde_amd import hip, workloads as W
+from helpers import rel_l2, scaled_error
+
+pytestmark = pytest.mark.gpu
+
+SCHEMAS = {
+    '2var_order6': W.full_schema(2, 6),
+    '3var_order4': W.full_schema(3, 4),
+    '1var_order6': W.full_schema(1, 6),
+    'poisson_xx_yy': W.closed_schema(2, [(2, 0), (0, 2)]),
+    '2var_order2': W.full_schema(2, 2),
+    'value_only': W.full_schema(2, 0),
+}
+
+
+def random_layer(device, schema, n, points, seed, scale=0.7):
+    """One sigmoid layer fed by random full stacks: returns net, plan, data."""
+    rng = np.random.default_rng(seed)
+    V = schema.shape[1] - 1
+    R = len(schema)
+    neurons, linear = [V, n, 1], [1, 0, 1]
+    w0 = np.concatenate([rng.uniform(-1, 1, n * V), rng.uniform(-.5, .5, n)]).astype(np.float32)
+    w1 = np.concatenate([rng.uniform(-1, 1, n), [0.1]]).astype(np.float32)
+    net = hip.Net(device, neurons, linear, [w0, w1])
+    plan = hip.Plan(net, schema, points, True)
+    data = (rng.standard_normal((R, points, V)) * scale).astype(np.float32)   # [row][sample][channel]
+    buf = hip.Buffer.of(device, data)
+    plan.activate(buf, points, np.arange(R, dtype=np.int32), 0, points)
+    return net, plan, buf, data, [w0, w1]
+
+
+@pytest.mark.parametrize('name', list(SCHEMAS))
+def test_linear_step_and_composition(device, name):
+    schema = SCHEMAS[name]
+    R, V = schema.shape[0], schema.shape[1] - 1
+    n, points = 64, 37
+    print(f'[case] composition {name} R={R} n={n} points={points}', flush=True)
+    net, plan, buf, data, (w0, w1) = random_layer(device, schema, n, points, 7)
+    plan.forward()
+    device.synchronize()
+    z1 = plan.stack(1, 0)                       # (points, R, n)
+    # linear step against float64: z = W x (+ b on the value row)
+    W0 = w0[:n * V].reshape(V, n).T.astype(np.float64)
+    x = data.astype(np.float64)                 # (R, points, V)
+    want = np.einsum('iv,rpv->pri', W0, x)
+    want[:, 0, :] += w0[n * V:]
+    assert scaled_error(z1, want) < 2e-5
+    y1 = plan.stack(1, 1)
+    zref = hip.stack_to_reference(z1).reshape(R, -1)
+    yref = oracle.compose(schema, zref).reshape(R, points, n)
+    err = scaled_error(hip.stack_to_reference(y1), yref, axis=(1, 2))
+    print(f'[result] {name} composition scaled error {err:.3e}', flush=True)
+    assert err < 1e-4
+    plan.destroy(); net.destroy(); buf.free()
+
+
+@pytest.mark.parametrize('name', list(SCHEMAS))
+def test_adjoint_composition(device, name):
+    schema = SCHEMAS[name]
+    R = schema.shape[0]
+    n, points = 64, 29
+    print(f'[case] adjoint {name} R={R}', flush=True)
+    net, plan, buf, data, (w0, w1) = random_layer(device, schema, n, points, 11)
+    rng = np.random.default_rng(3)
+    target = rng.standard_normal((R, points, 1)).astype(np.float32)
+    tbuf = hip.Buffer.of(device, target)
+    trows = hip.Buffer.of(device, np.arange(R, dtype=np.int32))
+    wts = hip.Buffer.of(device, np.linspace(0.5, 1.5, R).astype(np.float32))
+    device.costs_begin(1)
+    plan.forward()
+    plan.matching(tbuf, points, trows, wts, 1, 0, points, 0)
+    plan.backward(False)
+    device.synchronize()
+    z1 = hip.stack_to_reference(plan.stack(1, 0)).reshape(R, -1)
+    g2 = plan.stack(2, 2)[:, :, 0].astype(np.float64)         # (points, R)
+    gy = np.einsum('i,pr->rpi', w1[:n].astype(np.float64), g2).reshape(R, -1).astype(np.float32)
+    gz_ref = oracle.compose_adjoint(schema, z1, gy).reshape(R, points, n)
+    gz = hip.stack_to_reference(plan.stack(1, 2))
+    err = scaled_error(gz, gz_ref, axis=(1, 2))
+    print(f'[result] {name} adjoint scaled error {err:.3e}', flush=True)
+    assert err < 1e-4
+    for b in (tbuf, trows, wts, buf):
+        b.free()
+    plan.destroy(); net.destroy()
+
+
+def small_workload(order, neurons, points, seed=5):
+    schema = W.full_schema(2, order)
+    rng = np.random.default_rng(seed)
+    pts = rng.uniform(0, 1, (points, 2))
+    freq, coef, phase = W.fourier_modes(2, 4, 3, seed)
+    target = W.fourier_target(pts, schema, freq, coef, phase)
+    return W.MatchingWorkload('small', neurons, pts, schema, target, 1.0 / target.var(axis=1),
+                              W.xavier_weights(neurons, seed))
+
+
+@pytest.mark.parametrize('order,neurons,points,chunk', [
+    (6, [2, 32, 32, 1], 50, 0),
+    (6, [2, 32, 32, 1], 50, 16),
+    (2, [2, 48, 40, 24, 1], 101, 0),
+    (4, [2, 16, 1], 64, 25),
+])
+def test_epoch_matches_oracle(device, order, neurons, points, chunk):
+    print(f'[case] epoch order={order} neurons={neurons} points={points} chunk={chunk}', flush=True)
+    wl = small_workload(order, neurons, points)
+    run = hip.MatchingRun(device, wl, chunk=chunk or None)
+    run.step()
+    device.synchronize()
+    loss = run.loss()
+    grads = run.gradients()
+    ref_loss, ref_grads, _ = oracle.matching_epoch(wl.neurons, wl.linear, wl.init, wl.schema,
+                                                   wl.inputs.transpose(0, 2, 1), wl.target[:, :, None],
+                                                   wl.row_weights[:, None, None], chunk=chunk)
+    print(f'[result] loss {loss!r} oracle {ref_loss!r}', flush=True)
+    assert abs(loss / ref_loss - 1) < 1e-4
+    for t, (g, r) in enumerate(zip(grads, ref_grads)):
+        e = rel_l2(g, r)
+        print(f'[result] transition {t} gradient rel-L2 {e:.3e}', flush=True)
+        assert e < 1e-3
+    run.close()
