@@ -1,0 +1,175 @@
+"""Benchmark of the cPDE training epoch on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+
+One step is one training epoch of a matching cost on the derivative stack:
+forward propagation of every derivative row through the network, the squared
+matching loss against the analytic Fourier derivatives, the weight gradient
+(adjoint compositions, transposed products, split-K weight contraction) and
+one RPROP update -- the work of Server::pass + network::train
+(cuda/cpde_server.cu:223-257, cuda/cpde_engine.cuh:993-1014), a superset of
+the reference's "fwd+cost+wgrad" timing scope.  Inputs, targets and weights are
+resident in HBM before the timed region starts.
+
+Prints one JSON line.  ``value`` is points x derivative rows per second for the
+whole job; ``ms_per_step`` the wall-clock milliseconds per epoch.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from cpde_amd import hip, workloads  # noqa: E402
+
+METRIC = 'ms/epoch (fwd+cost+wgrad) at order 6, 729 pts; points·derivs/s; % roofline'
+# The reference's published order-6 figure for this workload shape: 5.65 ms/epoch
+# on an RTX 3090, i.e. 729*28/5.65e-3 points*derivs/s (README.md:63).
+PUBLISHED_POINTS_DERIVS_PER_S = 729 * 28 / 5.65e-3
+PEAK_FP32_MFMA = 157.3e12   # flop/s, dense
+PEAK_HBM = 8.0e12           # bytes/s
+MFMA_KINDS = {'gemm_forward', 'gemm_transposed', 'gemm_wgrad'}
+
+WORKLOADS = {
+    'fourier_fit_order6': lambda: workloads.fourier_fit(6),
+    'fourier_fit_order2': lambda: workloads.fourier_fit(2),
+    'fourier_3d_order4': lambda: workloads.fourier_3d(),
+    'fourier_large_order6': lambda: workloads.fourier_large(),
+}
+
+
+def describe(wl, name):
+    return {
+        'workload': name,
+        'network': '→'.join(str(n) for n in wl.neurons) + ' sigmoid',
+        'points': wl.size,
+        'derivative_rows': wl.rows,
+        'chunk': wl.chunk or wl.size,
+        'step': 'forward + matching cost + weight gradient + RPROP',
+    }
+
+
+def roofline(report):
+    """Dominant kernel class by device time; achieved = its algorithmic work
+    per launch divided by its mean launch duration."""
+    kind = max(report, key=lambda k: report[k][1])
+    launches, ms, work = report[kind]
+    seconds = ms / 1e3
+    if kind in MFMA_KINDS:
+        achieved, peak, unit, bound = work / seconds / 1e12, PEAK_FP32_MFMA / 1e12, 'TFLOP/s', 'mfma'
+    else:
+        achieved, peak, unit, bound = work / seconds / 1e9, PEAK_HBM / 1e9, 'GB/s', 'hbm'
+    return {'kernel': kind, 'bound': bound, 'achieved': round(achieved, 3), 'peak': peak, 'unit': unit,
+            'frac': round(achieved / peak, 4), 'traffic': None,
+            'launches': launches, 'mean_launch_us': round(ms * 1e3 / launches, 3),
+            'work_per_launch': work / launches}
+
+
+def cpu_baseline(wl):
+    """The CPU restatement of the same epoch (oracle/, single thread), timed on
+    one full epoch of the workload."""
+    sys.path.insert(0, str(ROOT / 'oracle'))
+    import oracle
+    x = wl.inputs.transpose(0, 2, 1)
+    t0 = time.perf_counter()
+    oracle.matching_epoch(wl.neurons, wl.linear, wl.init, wl.schema, x, wl.target[:, :, None],
+                          wl.row_weights[:, None, None], chunk=wl.chunk, outputs=False)
+    W = [np.array(w, np.float32) for w in wl.init]
+    for w in W:  # one RPROP pass over the parameters, as in the timed step
+        z = np.zeros_like(w)
+        oracle.rprop(w, np.full_like(w, 0.002), z, z)
+    seconds = time.perf_counter() - t0
+    return {'value': round(wl.size * wl.rows / seconds, 1), 'unit': 'points·derivs/s', 'cores': 1,
+            'kind': 'port', 'seconds': round(seconds, 3),
+            'sample': f'one full epoch ({wl.size} points x {wl.rows} rows, {wl.name}) of the C restatement, '
+                      'fwd+cost+wgrad+RPROP, single thread'}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=500)
+    ap.add_argument('--warmup', type=int, default=50)
+    ap.add_argument('--workload', default='fourier_fit_order6', choices=sorted(WORKLOADS))
+    ap.add_argument('--trace-steps', type=int, default=20)
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py measures one GPU only: the cPDE hot path runs on a single device '
+              '(multi-GPU point sharding is a design, not a build, here); run with --gpus 1', file=sys.stderr)
+        return 2
+
+    wl = WORKLOADS[args.workload]()
+    device = hip.Device(0)
+    name, cus = device.info()
+    run = hip.MatchingRun(device, wl)
+
+    def step():
+        run.step(collect=True)
+        run.net.rprop()
+
+    for _ in range(args.warmup):
+        step()
+    device.synchronize()
+    device.mark(0)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    device.mark(1)
+    device.synchronize()
+    wall = time.perf_counter() - t0
+    device_ms = device.elapsed(0, 1)
+    loss = run.loss()
+
+    device.trace(True)
+    for _ in range(args.trace_steps):
+        step()
+    report = device.trace_report()
+    device.trace(False)
+
+    ms = wall * 1e3 / args.steps
+    value = wl.size * wl.rows / (ms / 1e3)
+    t_roof = wl.flops_per_epoch() / PEAK_FP32_MFMA + wl.bytes_per_epoch() / PEAK_HBM
+    out = {
+        'metric': METRIC,
+        'value': round(value, 1),
+        'unit': 'points·derivs/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(ms, 5),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': round(value / PUBLISHED_POINTS_DERIVS_PER_S, 3) if args.workload == 'fourier_fit_order6'
+        else None,
+        'dtype': 'f32',
+        'data': 'synthetic (seeded Fourier-sum targets with analytic derivatives, Xavier-uniform weights)',
+        'config': describe(wl, args.workload),
+        'device': f'{name}, {cus} CUs',
+        'device_ms_per_step': round(device_ms / args.steps, 5),
+        'epoch_roofline': {'t_roof_us': round(t_roof * 1e6, 2), 'frac': round(t_roof / (ms / 1e3), 4),
+                           'gflop': wl.flops_per_epoch() / 1e9, 'gbytes': wl.bytes_per_epoch() / 1e9},
+        'loss_after_timed_steps': loss,
+        'roofline': roofline(report),
+        'kernels': {k: {'launches_per_step': v[0] / args.trace_steps, 'us_per_step': round(v[1] * 1e3 /
+                        args.trace_steps, 3)} for k, v in sorted(report.items(), key=lambda kv: -kv[1][1])},
+        'cpu_baseline': None,
+    }
+    run.close()
+    device.close()
+    if not args.no_cpu_baseline:
+        out['cpu_baseline'] = cpu_baseline(wl)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == '__main__':
+    sys.exit(main())

@@ -56,6 +56,8 @@ def build_lib():
 
 
 def build_server():
+    if not (CSRC / 'server.cpp').exists():
+        return None
     BIN_DIR.mkdir(exist_ok=True)
     tmp = SERVER.with_name('cpde_server.tmp')
     _run(['g++', '-O2', '-std=c++17', '-pthread', '-I', ROOT / 'include', '-I', '/opt/rocm/include',

@@ -28,6 +28,38 @@ void check_hip(hipError_t status, const char* what, const char* file, int line) 
     throw device_error(buf);
 }
 
+TraceScope::TraceScope(Device& dev, int kind, double work) : d(dev) {
+    if (!d.tracing) return;
+    if (d.event_pool.size() < 2 * d.pending.size() + 2) {
+        for (int i = 0; i < 64; ++i) {
+            hipEvent_t e;
+            HIP_CHECK(hipEventCreate(&e));
+            d.event_pool.push_back(e);
+        }
+    }
+    TraceRecord r{kind, work, d.event_pool[2 * d.pending.size()], d.event_pool[2 * d.pending.size() + 1]};
+    HIP_CHECK(hipEventRecord(r.start, d.stream));
+    index = int(d.pending.size());
+    d.pending.push_back(r);
+}
+
+TraceScope::~TraceScope() {
+    if (index >= 0) (void)hipEventRecord(d.pending[index].stop, d.stream);
+}
+
+void Device::fold_trace() {
+    if (pending.empty()) return;
+    HIP_CHECK(hipStreamSynchronize(stream));
+    for (const auto& r : pending) {
+        float ms = 0;
+        HIP_CHECK(hipEventElapsedTime(&ms, r.start, r.stop));
+        trace_ms[r.kind] += ms;
+        trace_work[r.kind] += r.work;
+        trace_launches[r.kind] += 1;
+    }
+    pending.clear();
+}
+
 void Device::reserve_costs(int costs) {
     require(costs >= 0, "invalid cost count");
     if (costs <= cost_capacity) return;
@@ -148,6 +180,7 @@ int cpde_device_close(cpde_device* dev) {
         if (!dev) return;
         (void)hipStreamSynchronize(dev->stream);
         for (auto& e : dev->marks) (void)hipEventDestroy(e);
+        for (auto& e : dev->event_pool) (void)hipEventDestroy(e);
         (void)hipFree(dev->cost_blocks);
         (void)hipFree(dev->grad_blocks);
         (void)hipFree(dev->cost_totals);
@@ -568,6 +601,36 @@ int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int coun
         launch_graph(*dev, nodes, count, root, leaves, values, adjoints, multipliers, active, summary, gradient != 0);
     });
 }
+
+int cpde_trace_enable(cpde_device* dev, int on) {
+    return guarded([&] {
+        dev->fold_trace();
+        dev->tracing = on != 0;
+        for (int k = 0; k < kTraceKinds; ++k) {
+            dev->trace_ms[k] = dev->trace_work[k] = 0;
+            dev->trace_launches[k] = 0;
+        }
+    });
+}
+
+int cpde_trace_read(cpde_device* dev, int kind, uint64_t* launches, double* total_ms, double* work) {
+    return guarded([&] {
+        require(kind >= 0 && kind < kTraceKinds, "invalid trace kind");
+        dev->fold_trace();
+        if (launches) *launches = dev->trace_launches[kind];
+        if (total_ms) *total_ms = dev->trace_ms[kind];
+        if (work) *work = dev->trace_work[kind];
+    });
+}
+
+const char* cpde_trace_name(int kind) {
+    static const char* names[kTraceKinds] = {"compose_forward", "compose_adjoint", "gemm_forward", "gemm_transposed",
+                                             "gemm_wgrad",      "split_reduce",    "bias_grad",    "activate",
+                                             "cost",            "reduce",          "optimizer",    "other"};
+    return kind >= 0 && kind < kTraceKinds ? names[kind] : "";
+}
+
+int cpde_trace_kinds(void) { return kTraceKinds; }
 
 int cpde_mark(cpde_device* dev, int slot) {
     return guarded([&] {

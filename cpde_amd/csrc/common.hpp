@@ -102,6 +102,19 @@ struct Program {
     std::string log;
 };
 
+// Per-launch device timing (HIP events on the library's stream), grouped by
+// kernel class.  `work` is the launch's algorithmic work: bytes for the
+// HBM-bound classes, flops for the matrix-core classes.
+enum TraceKind {
+    kTraceComposeForward, kTraceComposeAdjoint, kTraceGemm, kTraceGemmTransposed, kTraceWgrad, kTraceSplitReduce,
+    kTraceBiasGrad, kTraceActivate, kTraceCost, kTraceReduce, kTraceOptimizer, kTraceOther, kTraceKinds
+};
+struct TraceRecord {
+    int kind;
+    double work;
+    hipEvent_t start, stop;
+};
+
 struct Device {
     int ordinal = 0;
     int compute_units = 0;
@@ -115,8 +128,23 @@ struct Device {
     GradStats* host_grads = nullptr;
     int cost_capacity = 0, grad_capacity = 0;
     hipEvent_t marks[8] = {};
+    // tracing
+    bool tracing = false;
+    std::vector<hipEvent_t> event_pool;
+    std::vector<TraceRecord> pending;
+    double trace_ms[kTraceKinds] = {}, trace_work[kTraceKinds] = {};
+    uint64_t trace_launches[kTraceKinds] = {};
+    void fold_trace();
     void reserve_costs(int costs);
     void reserve_grads(int layers);
+};
+
+// Brackets one launch with events when tracing is on.
+struct TraceScope {
+    Device& d;
+    int index = -1;
+    TraceScope(Device& dev, int kind, double work);
+    ~TraceScope();
 };
 
 // ---- kernel launchers (kernels.hip) -------------------------------------------------

@@ -137,6 +137,7 @@ void launch_compose_forward(Device& d, const Plan& p, const float* z, float* y, 
     const int b = compose_block(R, 1);
     const size_t lds = size_t(R) * b * sizeof(float);
     const int grid = (elements + b - 1) / b;
+    TraceScope trace(d, kTraceComposeForward, 8.0 * double(elements) * R);  // read z, write y
     if (b == 256)
         hipLaunchKernelGGL(compose_forward_kernel<256>, grid, 256, lds, d.stream, z, y, R, n, elements, p.dev_tables);
     else if (b == 128)
@@ -152,6 +153,7 @@ void launch_compose_adjoint(Device& d, const Plan& p, const float* z, float* g, 
     const size_t lds = 2 * size_t(R) * b * sizeof(float);
     const int grid = (elements + b - 1) / b;
     const int* offsets = p.dev_tables + p.tables.words.size();
+    TraceScope trace(d, kTraceComposeAdjoint, 12.0 * double(elements) * R);  // read z and g_y, write g_z
     const int pair_begin = p.tables.pair_offset[0];
     if (b == 256)
         hipLaunchKernelGGL(compose_adjoint_kernel<256>, grid, 256, lds, d.stream, z, g, R, n, elements, p.dev_tables,
@@ -272,6 +274,7 @@ static void gemm_dispatch(Device& d, int M, int N, int K, const float* A, int ld
 void launch_gemm(Device& d, int M, int N, int K, const float* A, int lda, bool a_t, const float* B, int ldb, bool b_t,
                  float* C, int ldc, const float* bias, int period) {
     if (M <= 0 || N <= 0) return;
+    TraceScope trace(d, a_t ? kTraceGemmTransposed : kTraceGemm, 2.0 * M * double(N) * K);
     gemm_dispatch(d, M, N, K, A, lda, a_t, B, ldb, b_t, C, ldc, bias, period > 0 ? period : 1, 1, 0);
 }
 
@@ -303,9 +306,13 @@ void launch_wgrad(Device& d, Net& net, int M, int N, int K, const float* G, cons
         net.partial_capacity = need;
     }
     // dW = G * Y^T: A = G (M x K, ld M), B(k, n) = Y[n + N*k] (n-contiguous).
-    gemm_dispatch(d, M, N, K, G, M, false, Y, N, true, net.partials, M, nullptr, 1, splits, k_split);
+    {
+        TraceScope trace(d, kTraceWgrad, 2.0 * M * double(N) * K);
+        gemm_dispatch(d, M, N, K, G, M, false, Y, N, true, net.partials, M, nullptr, 1, splits, k_split);
+    }
     const size_t count = size_t(M) * N;
     const int blocks = int(std::min<size_t>((count + 255) / 256, 1024));
+    TraceScope trace(d, kTraceSplitReduce, 4.0 * double(count) * (splits + (accumulate ? 2 : 1)));
     hipLaunchKernelGGL(split_reduce_kernel, blocks, 256, 0, d.stream, net.partials, splits, count, dW,
                        int(accumulate));
     HIP_CHECK(hipGetLastError());
@@ -330,6 +337,7 @@ __global__ __launch_bounds__(256) void bias_grad_kernel(int M, int width, int R,
 }
 
 void launch_bias_grad(Device& d, int M, int width, int R, const float* G, float* db, bool accumulate) {
+    TraceScope trace(d, kTraceBiasGrad, 4.0 * (double(width) * M + M));
     hipLaunchKernelGGL(bias_grad_kernel, (M + 63) / 64, 256, 0, d.stream, M, width, R, G, db, int(accumulate));
     HIP_CHECK(hipGetLastError());
 }
@@ -352,6 +360,7 @@ void launch_activate(Device& d, float* x, const float* data, int data_width, int
                      int rows, int width, int offset, int valid) {
     const size_t total = size_t(width) * rows * channels;
     const int blocks = int(std::min<size_t>((total + 255) / 256, 4096));
+    TraceScope trace(d, kTraceActivate, 8.0 * double(total));
     hipLaunchKernelGGL(activate_kernel, blocks, 256, 0, d.stream, x, data, data_width, channels, rows_dev, rows, width,
                        offset, valid);
     HIP_CHECK(hipGetLastError());
@@ -426,6 +435,7 @@ __global__ __launch_bounds__(kCostThreads) void cost_finish_kernel(const CostSta
 static int cost_blocks_for(int count) { return std::max(1, std::min(kMaxCostBlocks, (count + kCostThreads - 1) / kCostThreads)); }
 
 static void finish_cost(Device& d, int blocks, int cost_index) {
+    TraceScope trace(d, kTraceReduce, double(sizeof(CostStats)) * (blocks + 2));
     hipLaunchKernelGGL(cost_finish_kernel, 1, kCostThreads, 0, d.stream, d.cost_blocks, blocks,
                        d.cost_totals + cost_index);
     HIP_CHECK(hipGetLastError());
@@ -480,10 +490,14 @@ void launch_matching(Device& d, const Plan& p, const float* y, float* g, const f
                      int cost_index, bool collect, bool gradient) {
     const int outputs = p.net->neurons.back();
     const int blocks = cost_blocks_for(p.width);
+    {
+    // y and target read, g written
+    TraceScope trace(d, kTraceCost, 12.0 * double(p.columns()) * outputs);
     hipLaunchKernelGGL(matching_kernel, blocks, kCostThreads, 0, d.stream, y, g, target, target_width, target_rows,
                        weights, weight_samples, p.rows, outputs, p.width, valid, offset, int(collect), int(gradient),
                        d.cost_blocks);
     HIP_CHECK(hipGetLastError());
+    }
     finish_cost(d, blocks, cost_index);
 }
 
@@ -764,6 +778,7 @@ static void for_transition_groups(Net& net, F launch) {
 
 void launch_rprop(Device& d, Net& net) {
     for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
+        TraceScope trace(d, kTraceOptimizer, 28.0 * a.begin[a.transitions]);  // 4 reads, 3 writes per entry
         hipLaunchKernelGGL(rprop_kernel, blocks, 256, 0, d.stream, a);
         HIP_CHECK(hipGetLastError());
     });

@@ -77,6 +77,11 @@ SIGNATURES = {
     'cpde_program_destroy': (i32, [vp]),
     'cpde_cost_expression': (i32, [vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, i32]),
     'cpde_graph_execute': (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, i32]),
+    'cpde_trace_enable': (i32, [vp, i32]),
+    'cpde_trace_read': (i32, [vp, i32, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_double),
+                              ctypes.POINTER(ctypes.c_double)]),
+    'cpde_trace_name': (ctypes.c_char_p, [i32]),
+    'cpde_trace_kinds': (i32, []),
     'cpde_mark': (i32, [vp, i32]),
     'cpde_elapsed': (i32, [vp, i32, i32, ctypes.POINTER(f32)]),
 }
@@ -186,6 +191,20 @@ class Device:
         ms = f32()
         check(load().cpde_elapsed(self.handle, a, b, ctypes.byref(ms)))
         return ms.value
+
+    def trace(self, on):
+        check(load().cpde_trace_enable(self.handle, int(on)))
+
+    def trace_report(self):
+        """{kernel class: (launches, total device ms, total algorithmic work)}."""
+        out = {}
+        lib = load()
+        for k in range(lib.cpde_trace_kinds()):
+            n, ms, work = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_double()
+            check(lib.cpde_trace_read(self.handle, k, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(work)))
+            if n.value:
+                out[lib.cpde_trace_name(k).decode()] = (n.value, ms.value, work.value)
+        return out
 
     def close(self):
         if self.handle:
@@ -326,15 +345,20 @@ class MatchingRun:
         self.target_rows = Buffer.of(device, np.arange(wl.rows, dtype=np.int32))
         self.weights = Buffer.of(device, np.ascontiguousarray(wl.row_weights, np.float32))
         self.rows = np.arange(wl.rows, dtype=np.int32)
+        self._loaded = None
         device.costs_begin(1)
 
     def step(self, collect=True):
-        """forward + cost + backward over every chunk (Server::pass)."""
+        """forward + cost + backward over every chunk (Server::pass).  As in
+        Server::activate (cuda/cpde_server.cu:163) the input copy is skipped when
+        the loaded chunk is unchanged."""
         self.device.costs_begin(1)
         first = True
         for offset in range(0, self.samples, self.width):
             valid = min(self.width, self.samples - offset)
-            self.plan.activate(self.data, self.samples, self.rows, offset, valid)
+            if self._loaded != (offset, valid):
+                self.plan.activate(self.data, self.samples, self.rows, offset, valid)
+                self._loaded = (offset, valid)
             self.plan.forward()
             self.plan.matching(self.target, self.samples, self.target_rows, self.weights, 1, offset, valid, 0,
                                collect, True)

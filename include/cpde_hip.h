@@ -192,6 +192,16 @@ int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int coun
                        cpde_graph_summary* summary, int gradient);
 
 /* ---- timing ---------------------------------------------------------------------- */
+/* Kernel tracing (no counterpart in the reference, which has no built-in
+ * profiling): while enabled, every launch is bracketed by HIP events on the
+ * device stream and accounted to its kernel class.  Enabling (or disabling)
+ * clears the totals.  cpde_trace_read synchronizes and returns a class's
+ * launch count, summed device milliseconds and summed algorithmic work
+ * (bytes for HBM-bound classes, flops for the matrix-core classes). */
+int cpde_trace_enable(cpde_device* dev, int on);
+int cpde_trace_read(cpde_device* dev, int kind, uint64_t* launches, double* total_ms, double* work);
+const char* cpde_trace_name(int kind);
+int cpde_trace_kinds(void);
 /* Record an event on the device stream; elapsed milliseconds between two marks. */
 int cpde_mark(cpde_device* dev, int slot);
 int cpde_elapsed(cpde_device* dev, int from_slot, int to_slot, float* ms);

@@ -1,0 +1,125 @@
+"""Pins the oracle against golden vectors written by the reference CPU server
+(tests/golden/make_golden.py) and against the reference's published losses.
+CPU only; no GPU and no reference tree needed."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from cpde_amd import workloads as W
+from helpers import rel_l2
+
+GOLDEN = Path(__file__).resolve().parent / 'golden'
+
+
+def checksum(a):
+    a = np.asarray(a, np.float64).ravel()
+    return np.array([a.size, a.sum(), (a * a).sum(), (a * np.arange(a.size) / max(a.size, 1)).sum()])
+
+
+def probes(count, seed=2718):
+    return np.random.default_rng(seed).standard_normal((64, count))
+
+
+def load(name):
+    """A golden record; records of generated workloads get their inputs rebuilt
+    by the workload generator and checked against the stored checksums."""
+    path = GOLDEN / f'{name}.npz'
+    if not path.exists():
+        pytest.skip(f'{path.name} not generated')
+    g = dict(np.load(path, allow_pickle=False))
+    if 'generator' in g:
+        import ast
+        wl = getattr(W, str(g['generator']))(**ast.literal_eval(str(g['generator_args'])))
+        got = np.stack([checksum(wl.points), checksum(wl.target), checksum(wl.row_weights),
+                        checksum(np.concatenate(wl.init))])
+        assert np.allclose(got, g['checksums'], rtol=1e-12, atol=0), 'workload generator drifted'
+        g.update(schema=wl.schema, points=wl.points, target=wl.target, row_weights=wl.row_weights)
+        for t, w in enumerate(wl.init):
+            g[f'init{t}'] = w
+    return g
+
+
+def check_gradient(g, t, grad, tol):
+    if f'grad{t}' in g:
+        assert rel_l2(grad, g[f'grad{t}']) < tol, t
+    else:
+        p = probes(grad.size) @ np.asarray(grad, np.float64)
+        assert np.linalg.norm(p - g[f'grad{t}_probes']) < tol * np.linalg.norm(g[f'grad{t}_probes']), t
+        assert abs(np.linalg.norm(np.asarray(grad, np.float64)) / g[f'grad{t}_norm'] - 1) < tol, t
+
+
+def transitions(g):
+    return len(g['neurons']) - 1
+
+
+def epoch(g, chunk=None):
+    T = transitions(g)
+    init = [g[f'init{t}'] for t in range(T)]
+    schema = g['schema']
+    inputs = W.input_stack(g['points'], schema)
+    c = int(g['chunk']) if chunk is None else chunk
+    return oracle.matching_epoch(g['neurons'], g['linear'], init, schema, inputs.transpose(0, 2, 1),
+                                 g['target'][:, :, None], g['row_weights'][:, None, None], chunk=c)
+
+
+MATCHING = ['tiny_order6', 'tiny_3var_order4', 'fourier_order2', 'fourier3d_reduced', 'large_reduced']
+
+
+@pytest.mark.parametrize('name', MATCHING)
+def test_epoch_against_reference_server(name):
+    g = load(name)
+    loss, grads, outputs = epoch(g)
+    assert abs(loss / g['loss'] - 1) < 1e-5
+    for t, grad in enumerate(grads):
+        check_gradient(g, t, grad, 1e-5)
+    if 'outputs' in g:
+        assert rel_l2(outputs, g['outputs']) < 1e-6
+
+
+@pytest.mark.slow
+def test_order6_epoch_against_reference_server():
+    g = load('fourier_order6')
+    loss, grads, outputs = epoch(g)
+    assert abs(loss / g['loss'] - 1) < 1e-5
+    for t, grad in enumerate(grads):
+        check_gradient(g, t, grad, 1e-5)
+    for r in range(outputs.shape[0]):
+        assert rel_l2(outputs[r], g['outputs'][r]) < 1e-5, r
+
+
+def test_chunked_epoch_matches_reference_chunks():
+    g = load('tiny_order6')
+    loss, grads, _ = epoch(g, chunk=7)
+    assert abs(loss / g['chunk7_loss'] - 1) < 1e-5
+    for t, grad in enumerate(grads):
+        assert rel_l2(grad, g[f'chunk7_grad{t}']) < 1e-5
+
+
+@pytest.mark.parametrize('name', ['tiny_order6', 'tiny_3var_order4'])
+def test_first_rprop_step_matches_reference(name):
+    """From a fresh optimizer state the reference's one-epoch update is
+    w - copysign(0.002, g) wherever g != 0: the oracle, fed the reference's own
+    gradient, must reproduce its weights and steps bit for bit."""
+    g = load(name)
+    for t in range(transitions(g)):
+        w = g[f'init{t}']
+        grad = g[f'grad{t}']
+        W_, S, ga, gi = oracle.rprop(w, np.full_like(w, 0.002), grad, np.zeros_like(w))
+        np.testing.assert_array_equal(W_, g[f'after{t}'])
+        np.testing.assert_array_equal(S, g[f'step{t}'])
+        assert int(g[f'active{t}']) == 2
+
+
+def test_published_losses():
+    """The reference's Fourier benchmark workload at initial weights, orders 0..6:
+    the reference CPU server, and the oracle, against the published CUDA losses
+    (docs/benchmarks/fourier-rtx3090.json)."""
+    g = load('published')
+    assert np.allclose(g['published_losses'], W.PUBLISHED_LOSSES, rtol=2e-8)
+    for order in (0, 3):
+        wl = W.reference_benchmark(order)
+        loss, _, _ = oracle.matching_epoch(wl.neurons, wl.linear, wl.init, wl.schema, wl.inputs.transpose(0, 2, 1),
+                                           wl.target[:, :, None], wl.row_weights[:, None, None], outputs=False)
+        assert abs(loss / W.PUBLISHED_LOSSES[order] - 1) < 1e-6, order
