@@ -44,10 +44,17 @@ def build_lib():
     LIB_DIR.mkdir(exist_ok=True)
     obj_dir = PKG / '_build'
     obj_dir.mkdir(exist_ok=True)
+    # the layer-fused kernel templates are compiled at run time (hipRTC, per
+    # schema); embed their text into the library
+    text = (CSRC / 'fused.hip.in').read_text()
+    assert ')CPDE_SRC"' not in text
+    embedded = obj_dir / 'fused_source.cpp'
+    embedded.write_text('namespace cpde {\nextern const char* const kFusedSource;\n'
+                        'const char* const kFusedSource = R"CPDE_SRC(' + text + ')CPDE_SRC";\n}\n')
     objs = []
-    for src in ['kernels.hip', 'api.hip', 'tables.cpp']:
-        obj = obj_dir / (src + '.o')
-        _run([hipcc(), *HIP_FLAGS, '-I', ROOT / 'include', '-c', CSRC / src, '-o', obj])
+    for src in [CSRC / 'kernels.hip', CSRC / 'api.hip', CSRC / 'tables.cpp', CSRC / 'jit.cpp', embedded]:
+        obj = obj_dir / (src.name + '.o')
+        _run([hipcc(), *HIP_FLAGS, '-I', ROOT / 'include', '-c', src, '-o', obj])
         objs.append(obj)
     tmp = LIB.with_suffix('.so.tmp')
     _run([hipcc(), *HIP_FLAGS, '-shared', '-o', tmp, *objs, '-lhiprtc'])
@@ -66,10 +73,28 @@ def build_server():
     return SERVER
 
 
+def warm_jit():
+    """Compile the schema-specialised kernels of the benchmark workloads into
+    the code-object cache (cpde_amd/jit_cache), so that a fresh process on the
+    GPU finds them without compiling."""
+    from . import hip, workloads as W
+    cache = PKG / 'jit_cache'
+    if cache.exists():
+        shutil.rmtree(cache)
+    hip.load(LIB)
+    for table, neurons in [(W.full_schema(2, 6), [2, 128, 128, 128, 128, 1]),
+                           (W.full_schema(2, 2), [2, 128, 128, 128, 128, 1]),
+                           (W.full_schema(3, 4), [3, 128, 128, 128, 128, 128, 1]),
+                           (W.full_schema(2, 6), [2, 256, 256, 256, 256, 1]),
+                           (W.closed_schema(2, [(2, 0), (0, 2)]), [2, 64, 64, 64, 1])]:
+        hip.jit_prepare(table, neurons, ARCH)
+
+
 def main(argv):
     what = argv[1] if len(argv) > 1 else 'all'
     if what in ('all', 'lib'):
         build_lib()
+        warm_jit()
     if what in ('all', 'server'):
         build_server()
 

@@ -145,6 +145,183 @@ static const int* plan_rows(Plan& p, const int* rows) {
     return p.dev_rows;
 }
 
+FusedModule::~FusedModule() {
+    if (module) (void)hipModuleUnload(module);
+}
+
+static int env_int(const char* name, int fallback) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : fallback;
+}
+
+// The layer-fused path covers sigmoid hidden layers between a linear input
+// layer with few channels and a linear output layer with few outputs; other
+// architectures use the table-driven kernels.  CPDE_FUSED=0 forces the latter.
+static bool fused_eligible(const Net& n, const Plan& p) {
+    if (!env_int("CPDE_FUSED", 1)) return false;
+    const int L = n.layers;
+    if (L < 3 || L - 1 > kMaxTransitions || p.rows > 64 || n.neurons[0] > 16) return false;
+    for (int l = 1; l + 1 < L; ++l)
+        if (n.linear[l] || n.neurons[l] > 256) return false;
+    return n.neurons[L - 1] <= 8 && n.neurons[L - 1] <= n.neurons[L - 2];
+}
+
+static std::string device_arch(int ordinal) {
+    hipDeviceProp_t prop;
+    HIP_CHECK(hipGetDeviceProperties(&prop, ordinal));
+    std::string arch = prop.gcnArchName;
+    const size_t colon = arch.find(':');
+    return colon == std::string::npos ? arch : arch.substr(0, colon);
+}
+
+static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const std::vector<int>& neurons) {
+    const int ppb = std::max(1, env_int("CPDE_FUSED_POINTS", 2));
+    const std::string src = fused_source(t, neurons, ppb);
+    for (auto& kv : d.fused_modules)
+        if (kv.first == src) return kv.second;
+    std::string log;
+    const std::vector<char> code = compile_module(src, device_arch(d.ordinal), &log);
+    auto m = std::make_shared<FusedModule>();
+    m->points_per_block = ppb;
+    HIP_CHECK(hipModuleLoadData(&m->module, code.data()));
+    HIP_CHECK(hipModuleGetFunction(&m->input_layer, m->module, "input_layer_k"));
+    HIP_CHECK(hipModuleGetFunction(&m->output_backward, m->module, "output_backward_k"));
+    const int L = int(neurons.size());
+    m->hidden_forward.assign(L, nullptr);
+    m->hidden_backward.assign(L, nullptr);
+    for (int k = 1; k + 2 < L; ++k) {
+        HIP_CHECK(hipModuleGetFunction(&m->hidden_forward[k], m->module, ("hidden_forward_" + std::to_string(k)).c_str()));
+        HIP_CHECK(
+            hipModuleGetFunction(&m->hidden_backward[k], m->module, ("hidden_backward_" + std::to_string(k)).c_str()));
+    }
+    d.fused_modules.emplace_back(src, m);
+    return m;
+}
+
+static void launch_module(Device& d, hipFunction_t f, unsigned gx, unsigned gy, void** args) {
+    HIP_CHECK(hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, d.stream, args, nullptr));
+}
+
+static void fused_forward(Plan& p) {
+    Net& n = *p.net;
+    Device& d = *n.dev;
+    FusedModule& fm = *p.fused;
+    const int L = n.layers, R = p.rows;
+    int width = p.width;
+    const double cols = double(p.columns());
+    {
+        const float* W = n.state[0][0];
+        const float* X = n.z[0];
+        float* Z = n.z[1];
+        float* Y = n.y[1];
+        void* args[] = {&W, &X, &Z, &Y, &width};
+        TraceScope trace(d, kTraceFusedInput, 4.0 * cols * (n.neurons[0] + 2 * n.neurons[1]));
+        launch_module(d, fm.input_layer, unsigned((size_t(width) * n.neurons[1] + 255) / 256), 1, args);
+    }
+    for (int t = 1; t + 2 < L; ++t) {
+        const float* W = n.state[0][t];
+        const float* Yin = n.y[t];
+        float* Z = n.z[t + 1];
+        float* Y = n.y[t + 1];
+        void* args[] = {&W, &Yin, &Z, &Y, &width};
+        TraceScope trace(d, kTraceFusedForward, 2.0 * n.neurons[t] * n.neurons[t + 1] * cols);
+        launch_module(d, fm.hidden_forward[t], unsigned((n.neurons[t + 1] + 63) / 64),
+                      unsigned((width + fm.points_per_block - 1) / fm.points_per_block), args);
+    }
+    launch_output_forward(d, n.state[0][L - 2], n.y[L - 2], n.z[L - 1], n.neurons[L - 2], n.neurons[L - 1], R,
+                          int(p.columns()));
+}
+
+// Grouped weight gradient of every transition (dW_t = G_{t+1} Y_t^T plus the
+// bias), split over the columns; splits are shared out in proportion to each
+// transition's (tile-padded) work so the launch holds about two blocks per CU.
+static void weight_gradients(Plan& p, bool accumulate) {
+    Net& n = *p.net;
+    Device& d = *n.dev;
+    const int L = n.layers, T = L - 1, K = int(p.columns());
+    WgradArgs wa{};
+    ReduceArgs ra{};
+    wa.transitions = T;
+    wa.K = K;
+    wa.R = p.rows;
+    double total_tiles = 0, flops = 0;
+    for (int t = 0; t < T; ++t) total_tiles += ((n.neurons[t + 1] + 63) / 64) * ((n.neurons[t] + 63) / 64);
+    size_t offset = 0;
+    std::vector<size_t> part_offset(T);
+    std::vector<int> splits(T);
+    wa.block_begin[0] = 0;
+    for (int t = 0; t < T; ++t) {
+        const int M = n.neurons[t + 1], N = n.neurons[t];
+        const int tiles = ((M + 63) / 64) * ((N + 63) / 64);
+        int s = int(2.0 * d.compute_units / total_tiles + 0.5);
+        s = std::max(1, std::min(s, std::max(1, K / 64)));
+        int chunk = (K + s - 1) / s;
+        chunk = (chunk + 15) / 16 * 16;
+        s = (K + chunk - 1) / chunk;
+        splits[t] = s;
+        wa.M[t] = M;
+        wa.N[t] = N;
+        wa.kchunk[t] = chunk;
+        wa.block_begin[t + 1] = wa.block_begin[t] + tiles * s;
+        wa.G[t] = n.g[t + 1];
+        wa.Y[t] = n.linear[t] ? n.z[t] : n.y[t];
+        part_offset[t] = offset;
+        offset += size_t(s) * M * (N + 1);
+        flops += 2.0 * M * N * double(K);
+    }
+    if (offset > n.partial_capacity) {
+        HIP_CHECK(hipStreamSynchronize(d.stream));
+        if (n.partials) HIP_CHECK(hipFree(n.partials));
+        n.partials = nullptr;
+        HIP_CHECK(hipMalloc(&n.partials, offset * sizeof(float)));
+        n.partial_capacity = offset;
+    }
+    for (int t = 0; t < T; ++t) wa.partial[t] = n.partials + part_offset[t];
+    launch_wgrad_grouped(d, wa, flops);
+    ra.transitions = T;
+    ra.accumulate = accumulate ? 1 : 0;
+    ra.begin[0] = 0;
+    for (int t = 0; t < T; ++t) {
+        ra.partial[t] = wa.partial[t];
+        ra.grad[t] = n.state[n.active[t]][t];
+        ra.M[t] = n.neurons[t + 1];
+        ra.N[t] = n.neurons[t];
+        ra.splits[t] = splits[t];
+        ra.begin[t + 1] = ra.begin[t] + n.neurons[t + 1] * (n.neurons[t] + 1);
+    }
+    launch_reduce_grouped(d, ra);
+}
+
+static void fused_backward(Plan& p, bool accumulate) {
+    Net& n = *p.net;
+    Device& d = *n.dev;
+    FusedModule& fm = *p.fused;
+    const int L = n.layers;
+    int width = p.width;
+    const double cols = double(p.columns());
+    {
+        const int NIo = n.neurons[L - 2], NOo = n.neurons[L - 1];
+        const float* W = n.state[0][L - 2];
+        const float* G = n.g[L - 1];
+        const float* Zl = n.z[L - 2];
+        float* Gl = n.g[L - 2];
+        void* args[] = {&W, &G, &Zl, &Gl, &width};
+        TraceScope trace(d, kTraceFusedOutput, 4.0 * cols * (3.0 * NIo + NOo));
+        launch_module(d, fm.output_backward, unsigned((size_t(width) * NIo + 255) / 256), 1, args);
+    }
+    for (int t = L - 3; t >= 1; --t) {
+        const float* W = n.state[0][t];
+        const float* Gnext = n.g[t + 1];
+        const float* Zl = n.z[t];
+        float* Gl = n.g[t];
+        void* args[] = {&W, &Gnext, &Zl, &Gl, &width};
+        TraceScope trace(d, kTraceFusedBackward, 2.0 * n.neurons[t] * n.neurons[t + 1] * cols);
+        launch_module(d, fm.hidden_backward[t], unsigned((n.neurons[t] + 63) / 64),
+                      unsigned((width + fm.points_per_block - 1) / fm.points_per_block), args);
+    }
+    weight_gradients(p, accumulate);
+}
+
 }  // namespace cpde
 
 using namespace cpde;
@@ -343,6 +520,7 @@ int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, i
         HIP_CHECK(hipMemcpyAsync(p->dev_tables, blob.data(), blob.size() * sizeof(int), hipMemcpyHostToDevice,
                                  net->dev->stream));
         reserve_arena(*net, *p);
+        if (fused_eligible(*net, *p)) p->fused = load_fused(*net->dev, p->tables, net->neurons);
         HIP_CHECK(hipStreamSynchronize(net->dev->stream));
         *out = p.release();
     });
@@ -385,6 +563,10 @@ int cpde_forward(cpde_plan* plan) {
     return guarded([&] {
         Net& n = *plan->net;
         Device& d = *n.dev;
+        if (plan->fused) {
+            fused_forward(*plan);
+            return;
+        }
         const int cols = int(plan->columns());
         for (int t = 0; t + 1 < n.layers; ++t) {
             const int ni = n.neurons[t], no = n.neurons[t + 1];
@@ -450,17 +632,19 @@ int cpde_backward(cpde_plan* plan, int accumulate) {
         Net& n = *plan->net;
         Device& d = *n.dev;
         require(plan->backward, "plan has no adjoint storage");
-        const int cols = int(plan->columns());
-        for (int t = n.layers - 2; t >= 0; --t) {
-            const int ni = n.neurons[t], no = n.neurons[t + 1];
-            float* grad = n.state[n.active[t]][t];
-            launch_wgrad(d, n, no, ni, cols, n.g[t + 1], activations(n, t), grad, accumulate != 0);
-            launch_bias_grad(d, no, plan->width, plan->rows, n.g[t + 1], grad + size_t(no) * ni, accumulate != 0);
-            if (t > 0) {
-                launch_gemm(d, ni, cols, no, n.state[0][t], no, true, n.g[t + 1], no, false, n.g[t], ni, nullptr, 1);
-                if (!n.linear[t]) launch_compose_adjoint(d, *plan, n.z[t], n.g[t], ni);
-            }
+        if (plan->fused) {
+            fused_backward(*plan, accumulate != 0);
+            return;
         }
+        // dE/dz of every layer (transposed products, in-place adjoint
+        // compositions), then all weight gradients in one grouped launch
+        const int cols = int(plan->columns());
+        for (int t = n.layers - 2; t >= 1; --t) {
+            const int ni = n.neurons[t], no = n.neurons[t + 1];
+            launch_gemm(d, ni, cols, no, n.state[0][t], no, true, n.g[t + 1], no, false, n.g[t], ni, nullptr, 1);
+            if (!n.linear[t]) launch_compose_adjoint(d, *plan, n.z[t], n.g[t], ni);
+        }
+        weight_gradients(*plan, accumulate != 0);
     });
 }
 
@@ -624,13 +808,32 @@ int cpde_trace_read(cpde_device* dev, int kind, uint64_t* launches, double* tota
 }
 
 const char* cpde_trace_name(int kind) {
-    static const char* names[kTraceKinds] = {"compose_forward", "compose_adjoint", "gemm_forward", "gemm_transposed",
-                                             "gemm_wgrad",      "split_reduce",    "bias_grad",    "activate",
-                                             "cost",            "reduce",          "optimizer",    "other"};
+    static const char* names[kTraceKinds] = {
+        "compose_forward", "compose_adjoint", "gemm_forward",   "gemm_transposed", "gemm_wgrad",
+        "split_reduce",    "bias_grad",       "activate",       "cost",            "reduce",
+        "optimizer",       "other",           "fused_input",    "fused_forward",   "fused_backward",
+        "fused_output_backward"};
     return kind >= 0 && kind < kTraceKinds ? names[kind] : "";
 }
 
 int cpde_trace_kinds(void) { return kTraceKinds; }
+
+int cpde_jit_prepare(int rows, int variables, const int* table, int layers, const int* neurons, const char* arch,
+                     char* log, size_t log_capacity) {
+    return guarded([&] {
+        require(table && neurons && arch && layers >= 3, "invalid argument");
+        const Tables t = build_tables(rows, variables, table);
+        const int ppb = std::max(1, env_int("CPDE_FUSED_POINTS", 2));
+        std::string text;
+        try {
+            compile_module(fused_source(t, std::vector<int>(neurons, neurons + layers), ppb), arch, &text);
+        } catch (...) {
+            if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
+            throw;
+        }
+        if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
+    });
+}
 
 int cpde_mark(cpde_device* dev, int slot) {
     return guarded([&] {

@@ -66,6 +66,7 @@ struct Tables {
 Tables build_tables(int rows, int variables, const int* table);
 
 struct Device;
+struct FusedModule;
 
 struct Net {
     Device* dev = nullptr;
@@ -92,6 +93,7 @@ struct Plan {
     int* dev_tables = nullptr;  // device copy of tables.words, then tables.fwd_offset
     int* dev_rows = nullptr;    // device row map of the last activate/output
     std::vector<int> host_rows;
+    std::shared_ptr<FusedModule> fused;  // null: table-driven kernels
     size_t columns() const { return size_t(rows) * size_t(width); }
 };
 
@@ -107,7 +109,8 @@ struct Program {
 // HBM-bound classes, flops for the matrix-core classes.
 enum TraceKind {
     kTraceComposeForward, kTraceComposeAdjoint, kTraceGemm, kTraceGemmTransposed, kTraceWgrad, kTraceSplitReduce,
-    kTraceBiasGrad, kTraceActivate, kTraceCost, kTraceReduce, kTraceOptimizer, kTraceOther, kTraceKinds
+    kTraceBiasGrad, kTraceActivate, kTraceCost, kTraceReduce, kTraceOptimizer, kTraceOther, kTraceFusedInput,
+    kTraceFusedForward, kTraceFusedBackward, kTraceFusedOutput, kTraceKinds
 };
 struct TraceRecord {
     int kind;
@@ -135,9 +138,40 @@ struct Device {
     double trace_ms[kTraceKinds] = {}, trace_work[kTraceKinds] = {};
     uint64_t trace_launches[kTraceKinds] = {};
     void fold_trace();
+    // fused modules compiled on this device, by source text
+    std::vector<std::pair<std::string, std::shared_ptr<FusedModule>>> fused_modules;
     void reserve_costs(int costs);
     void reserve_grads(int layers);
 };
+
+// Grouped weight-gradient launch (one entry per transition).
+struct WgradArgs {
+    const float* G[kMaxTransitions];
+    const float* Y[kMaxTransitions];
+    float* partial[kMaxTransitions];
+    int M[kMaxTransitions], N[kMaxTransitions], kchunk[kMaxTransitions];
+    int block_begin[kMaxTransitions + 1];
+    int transitions, K, R;
+};
+struct ReduceArgs {
+    const float* partial[kMaxTransitions];
+    float* grad[kMaxTransitions];
+    int M[kMaxTransitions], N[kMaxTransitions], splits[kMaxTransitions];
+    int begin[kMaxTransitions + 1];
+    int transitions, accumulate;
+};
+
+// Schema-specialised layer-fused kernels of one plan (jit.cpp, fused.hip.in).
+struct FusedModule {
+    hipModule_t module = nullptr;
+    hipFunction_t input_layer = nullptr, output_backward = nullptr;
+    std::vector<hipFunction_t> hidden_forward, hidden_backward;  // per transition (index t)
+    int points_per_block = 2;
+    ~FusedModule();
+};
+std::string compose_source(const Tables& t);
+std::string fused_source(const Tables& t, const std::vector<int>& neurons, int points_per_block);
+std::vector<char> compile_module(const std::string& source, const std::string& arch, std::string* log);
 
 // Brackets one launch with events when tracing is on.
 struct TraceScope {
@@ -159,11 +193,6 @@ void launch_compose_adjoint(Device& d, const Plan& p, const float* z, float* g, 
 // column n with n % period == 0.
 void launch_gemm(Device& d, int M, int N, int K, const float* A, int lda, bool a_t, const float* B, int ldb, bool b_t,
                  float* C, int ldc, const float* bias, int period);
-// Weight gradient dW[M x N] (+)= G[M x K] * Y[N x K]^T (both column-major with
-// ld M and N), deterministic split-K through the network's partial buffer.
-void launch_wgrad(Device& d, Net& net, int M, int N, int K, const float* G, const float* Y, float* dW, bool accumulate);
-// db[m] (+)= sum over points p of G[(p*R)*M + m] (value row of a [point][row][M] stack).
-void launch_bias_grad(Device& d, int M, int width, int R, const float* G, float* db, bool accumulate);
 void launch_matching(Device& d, const Plan& p, const float* y, float* g, const float* target, int target_width,
                      const int* target_rows, const float* weights, int weight_samples, int offset, int valid,
                      int cost_index, bool collect, bool gradient);
@@ -175,6 +204,9 @@ void launch_scale_adjoint(Device& d, const Plan& p, float* g, const double* mult
 void launch_costs_begin(Device& d, int costs);
 void launch_grad_stats(Device& d, const float* g, int count, int slot);
 void launch_fill(Device& d, float* p, size_t count, float value);
+void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, int NI, int NO, int R, int columns);
+void launch_wgrad_grouped(Device& d, const WgradArgs& a, double flops);
+void launch_reduce_grouped(Device& d, const ReduceArgs& a);
 void launch_rprop(Device& d, Net& net);
 void launch_adam(Device& d, Net& net, int step, float lr);
 void launch_set_steps(Device& d, Net& net, float value);

@@ -1,0 +1,280 @@
+// Schema-specialised kernels: source generation and hipRTC compilation.
+//
+// For a derivative schema the sigmoid composition (replacing the reference's
+// hand-written d1..d6 / d1p..d6p, cuda/derivative_kernels_v4.cu:12-745) is
+// emitted as straight-line register code: every multiset-partition term with
+// its integer coefficient, every product of stack rows computed once (products
+// are built from shared prefixes), every adjoint pair (cuda/cpde_engine.cuh:476-498)
+// unrolled.  The generated functions are prepended to the layer-fused kernel
+// templates (fused.hip.in) and the module is compiled for the device's
+// architecture with hipRTC -- the way the reference compiles its expression
+// costs with NVRTC (cuda/expression_program.hpp:96-131).
+//
+// Compiled code objects are cached on disk, keyed by a hash of the source and
+// the options: $CPDE_JIT_CACHE, else <library directory>/../jit_cache.
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <mutex>
+#include <sstream>
+
+#include "common.hpp"
+
+namespace cpde {
+
+extern const char* const kFusedSource;  // fused.hip.in, embedded at build time
+
+namespace {
+
+float word_float(int w) {
+    float f;
+    std::memcpy(&f, &w, sizeof f);
+    return f;
+}
+
+std::string flit(float f) {
+    char buf[48];
+    std::snprintf(buf, sizeof buf, "%.9gf", double(f));
+    std::string s(buf);
+    if (s.find_first_of(".eEn") == std::string::npos) s.insert(s.size() - 1, ".0");
+    return s;
+}
+
+struct Products {
+    std::ostringstream& out;
+    std::map<std::vector<int>, std::string> names;
+    std::string get(const std::vector<int>& rows) {
+        if (rows.size() == 1) return "z[" + std::to_string(rows[0]) + "]";
+        auto it = names.find(rows);
+        if (it != names.end()) return it->second;
+        std::vector<int> prefix(rows.begin(), rows.end() - 1);
+        const std::string a = get(prefix);
+        std::string name = "p";
+        for (int r : rows) name += "_" + std::to_string(r);
+        out << "    const float " << name << " = " << a << " * z[" << rows.back() << "];\n";
+        names[rows] = name;
+        return name;
+    }
+};
+
+// The sigma derivatives from q = 1/(1+e^z) (cuda/derivative_kernels_v4.cu:462-468).
+void emit_sigma(std::ostringstream& o, int highest) {
+    o << "    const float q = 1.0f / (1.0f + expf(z[0]));\n";
+    o << "    const float s1 = q * (1.0f - q);\n";
+    if (highest >= 2) o << "    const float s2 = -s1 * (1.0f - 2.0f * q);\n";
+    if (highest >= 3) o << "    const float s3 = s1 * (1.0f - 6.0f * s1);\n";
+    if (highest >= 4) o << "    const float s4 = s2 * (1.0f - 12.0f * s1);\n";
+    if (highest >= 5) o << "    const float s5 = s1 - (5.0f * s2) * (6.0f * s2);\n";
+    if (highest >= 6) o << "    const float s6 = s2 + 5.0f * (s4 - s2) * (1.0f - 6.0f * s1);\n";
+    if (highest >= 7)
+        o << "    const float s7 = (5.0f * s1) * (0.2f - (8.4f * s1) * (3.0f - 4.0f * (5.0f * s1 + 5.0f * s3)));\n";
+}
+
+// sum_m s_{m+shift} M_m for row r, M_m = sum_terms c * prod(block rows).
+std::string emit_partition_sum(std::ostringstream& o, Products& P, const Tables& t, int r, int shift,
+                               const std::string& name) {
+    int pos = t.fwd_offset[r];
+    const int k = t.words[pos++];
+    std::string acc;
+    for (int m = 1; m <= k; ++m) {
+        const int count = t.words[pos++];
+        std::string M = "0.0f";
+        for (int q = 0; q < count; ++q) {
+            const float c = word_float(t.words[pos]);
+            const unsigned w0 = unsigned(t.words[pos + 1]), w1 = unsigned(t.words[pos + 2]);
+            pos += 3;
+            std::vector<int> rows;
+            for (int b = 0; b < m; ++b) rows.push_back(int(((b < 4 ? w0 >> (8 * b) : w1 >> (8 * (b - 4)))) & 255u));
+            const std::string prod = P.get(rows);
+            if (q == 0 && c == 1.0f)
+                M = prod;
+            else if (q == 0)
+                M = flit(c) + " * " + prod;
+            else
+                M = "fmaf(" + flit(c) + ", " + prod + ", " + M + ")";
+            if (q + 1 < count && M.size() > 200) {  // keep expressions short
+                const std::string tmp = name + "_m" + std::to_string(m) + "_" + std::to_string(q);
+                o << "    const float " << tmp << " = " << M << ";\n";
+                M = tmp;
+            }
+        }
+        const std::string s = "s" + std::to_string(m + shift);
+        acc = m == 1 ? s + " * " + M : "fmaf(" + s + ", " + M + ", " + acc + ")";
+        const std::string tmp = name + "_a" + std::to_string(m);
+        o << "    const float " << tmp << " = " << acc << ";\n";
+        acc = tmp;
+    }
+    return acc;
+}
+
+}  // namespace
+
+std::string compose_source(const Tables& t) {
+    std::ostringstream o;
+    o << "#define CPDE_R " << t.rows << "\n";
+    // forward
+    o << "__device__ __forceinline__ void compose_forward(const float* __restrict__ z, float* __restrict__ y) {\n";
+    emit_sigma(o, std::max(1, t.max_order));
+    o << "    y[0] = 1.0f / (1.0f + expf(-z[0]));\n";
+    {
+        Products P{o, {}};
+        for (int r = 1; r < t.rows; ++r) {
+            const std::string v = emit_partition_sum(o, P, t, r, 0, "f" + std::to_string(r));
+            o << "    y[" << r << "] = " << v << ";\n";
+        }
+    }
+    o << "}\n";
+    // adjoint
+    o << "__device__ __forceinline__ void compose_adjoint(const float* __restrict__ z, const float* __restrict__ gy,"
+         " float* __restrict__ gz) {\n";
+    emit_sigma(o, t.max_order + 1);
+    {
+        std::vector<char> needed(t.rows, 0);
+        for (int i = 0; i < t.rows; ++i) {
+            int pos = t.pair_offset[i];
+            const int count = t.words[pos++];
+            for (int q = 0; q < count; ++q, pos += 3) needed[t.words[pos + 1]] = 1;
+        }
+        Products P{o, {}};
+        for (int r = 1; r < t.rows; ++r) {
+            if (!needed[r]) continue;
+            const std::string v = emit_partition_sum(o, P, t, r, 1, "d" + std::to_string(r));
+            o << "    const float D" << r << " = " << v << ";\n";
+        }
+        for (int i = 0; i < t.rows; ++i) {
+            int pos = t.pair_offset[i];
+            const int count = t.words[pos++];
+            o << "    { float acc = s1 * gy[" << i << "];\n";
+            for (int q = 0; q < count; ++q, pos += 3) {
+                const int j = t.words[pos], dn = t.words[pos + 1];
+                require(dn > 0, "adjoint pair refers to the value row");
+                const float c = word_float(t.words[pos + 2]);
+                o << "      acc = acc + (" << flit(c) << " * gy[" << j << "]) * D" << dn << ";\n";
+            }
+            o << "      gz[" << i << "] = acc; }\n";
+        }
+    }
+    o << "}\n";
+    return o.str();
+}
+
+namespace {
+
+uint64_t fnv1a(const std::string& s, uint64_t h = 1469598103934665603ull) {
+    for (unsigned char c : s) {
+        h ^= c;
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+std::string cache_dir() {
+    if (const char* env = std::getenv("CPDE_JIT_CACHE")) return env;
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void*>(&fnv1a), &info) && info.dli_fname) {
+        std::string lib(info.dli_fname);
+        const size_t slash = lib.rfind('/');
+        if (slash != std::string::npos) return lib.substr(0, slash) + "/../jit_cache";
+    }
+    return "";
+}
+
+bool read_file(const std::string& path, std::vector<char>& out) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return false;
+    out.assign(std::istreambuf_iterator<char>(f), std::istreambuf_iterator<char>());
+    return !out.empty();
+}
+
+void write_file(const std::string& path, const std::vector<char>& data) {
+    const std::string tmp = path + ".tmp" + std::to_string(getpid());
+    {
+        std::ofstream f(tmp, std::ios::binary);
+        if (!f) return;
+        f.write(data.data(), std::streamsize(data.size()));
+        if (!f) return;
+    }
+    std::rename(tmp.c_str(), path.c_str());
+}
+
+std::mutex compile_mutex;
+
+}  // namespace
+
+// Compiles (or fetches from the cache) the code object of `source` for `arch`.
+std::vector<char> compile_module(const std::string& source, const std::string& arch, std::string* log) {
+    const std::string arch_opt = "--offload-arch=" + arch;
+    const char* options[] = {arch_opt.c_str(), "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+                             "-packed-fp32-ops"};
+    const int noptions = int(sizeof options / sizeof options[0]);
+    std::string key_text = source;
+    for (auto* opt : options) key_text += std::string("\n") + opt;
+    char name[64];
+    std::snprintf(name, sizeof name, "cpde_%016llx.co", (unsigned long long)fnv1a(key_text));
+    const std::string dir = cache_dir();
+    const std::string path = dir.empty() ? "" : dir + "/" + name;
+    std::vector<char> code;
+    std::lock_guard<std::mutex> lock(compile_mutex);
+    if (const char* dump = std::getenv("CPDE_JIT_DUMP")) {  // source of the last module, for inspection
+        std::ofstream f(dump);
+        f << source;
+    }
+    if (!path.empty() && read_file(path, code)) return code;
+    hiprtcProgram prog;
+    if (hiprtcCreateProgram(&prog, source.c_str(), "cpde_fused.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+        throw compile_error("hiprtcCreateProgram failed");
+    const hiprtcResult result = hiprtcCompileProgram(prog, noptions, options);
+    size_t size = 0;
+    hiprtcGetProgramLogSize(prog, &size);
+    std::string text(size, '\0');
+    if (size) hiprtcGetProgramLog(prog, &text[0]);
+    while (!text.empty() && text.back() == '\0') text.pop_back();
+    if (log) *log = text;
+    if (result != HIPRTC_SUCCESS) {
+        hiprtcDestroyProgram(&prog);
+        throw compile_error("fused kernel compile failed: " + text.substr(0, 4000));
+    }
+    size_t code_size = 0;
+    hiprtcGetCodeSize(prog, &code_size);
+    code.resize(code_size);
+    hiprtcGetCode(prog, code.data());
+    hiprtcDestroyProgram(&prog);
+    if (!path.empty()) {
+        mkdir(dir.c_str(), 0755);
+        write_file(path, code);
+    }
+    return code;
+}
+
+// Full source of the fused module for a schema and architecture.
+std::string fused_source(const Tables& t, const std::vector<int>& neurons, int points_per_block) {
+    std::ostringstream o;
+    o << "// generated: cPDE layer-fused kernels\n#define CPDE_POINTS " << points_per_block << "\n";
+    o << compose_source(t);
+    o << kFusedSource;
+    const int L = int(neurons.size());
+    o << "\nextern \"C\" __global__ __launch_bounds__(256) void input_layer_k(const float* W, const float* X, float* Z,"
+         " float* Y, int points) { input_layer<"
+      << neurons[0] << ", " << neurons[1] << ">(W, X, Z, Y, points); }\n";
+    for (int t = 1; t + 2 < L; ++t) {
+        o << "extern \"C\" __global__ __launch_bounds__(256) void hidden_forward_" << t
+          << "(const float* W, const float* Yin, float* Z, float* Yout, int points) { hidden_forward<" << neurons[t]
+          << ", " << neurons[t + 1] << ">(W, Yin, Z, Yout, points); }\n";
+        o << "extern \"C\" __global__ __launch_bounds__(256) void hidden_backward_" << t
+          << "(const float* W, const float* Gnext, const float* Zl, float* Gl, int points) { hidden_backward<"
+          << neurons[t] << ", " << neurons[t + 1] << ">(W, Gnext, Zl, Gl, points); }\n";
+    }
+    o << "extern \"C\" __global__ __launch_bounds__(256) void output_backward_k(const float* W, const float* G,"
+         " const float* Zl, float* Gl, int points) { output_backward<"
+      << neurons[L - 2] << ", " << neurons[L - 1] << ">(W, G, Zl, Gl, points); }\n";
+    return o.str();
+}
+
+}  // namespace cpde

@@ -278,67 +278,159 @@ void launch_gemm(Device& d, int M, int N, int K, const float* A, int lda, bool a
     gemm_dispatch(d, M, N, K, A, lda, a_t, B, ldb, b_t, C, ldc, bias, period > 0 ? period : 1, 1, 0);
 }
 
-// Fixed-order sum of split-K partials: out[i] = sum_s P[s][i] (+ out[i]).
-__global__ void split_reduce_kernel(const float* __restrict__ P, int splits, size_t count, float* __restrict__ out,
-                                    int accumulate) {
-    for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < count; i += size_t(gridDim.x) * blockDim.x) {
-        float s = 0.0f;
-        for (int z = 0; z < splits; ++z) s += P[size_t(z) * count + i];
-        out[i] = accumulate ? out[i] + s : s;
+// ------------------------------------------------------------------------------------------
+// Output transition with few outputs: z[col][o] = sum_i W[o + NO*i] y[col][i]
+// (+ bias on value-row columns).  One wave per column, lanes stride the inputs,
+// fixed-order wave reduction.
+__global__ __launch_bounds__(256) void output_forward_kernel(const float* __restrict__ W, const float* __restrict__ Y,
+                                                             float* __restrict__ Z, int NI, int NO, int R,
+                                                             int columns) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int col = blockIdx.x * 4 + wave; col < columns; col += gridDim.x * 4) {
+        const float* y = Y + size_t(col) * NI;
+        for (int o = 0; o < NO; ++o) {
+            float s = 0.0f;
+            for (int i = lane; i < NI; i += 64) s = fmaf(W[o + NO * i], y[i], s);
+            for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+            if (lane == 0) Z[size_t(col) * NO + o] = s + ((col % R) == 0 ? W[o + NO * NI] : 0.0f);
+        }
     }
 }
 
-void launch_wgrad(Device& d, Net& net, int M, int N, int K, const float* G, const float* Y, float* dW,
-                  bool accumulate) {
-    const int BMx = M <= 32 ? 32 : 128, BNx = M <= 32 ? 128 : 64;
-    const int tiles = ((M + BMx - 1) / BMx) * ((N + BNx - 1) / BNx);
-    int splits = std::max(1, (2 * d.compute_units + tiles - 1) / tiles);
-    splits = std::min(splits, std::max(1, K / 64));
-    int k_split = (K + splits - 1) / splits;
-    k_split = (k_split + BK - 1) / BK * BK;
-    splits = (K + k_split - 1) / k_split;
-    const size_t need = size_t(splits) * M * N;
-    if (need > net.partial_capacity) {
-        HIP_CHECK(hipStreamSynchronize(d.stream));
-        if (net.partials) HIP_CHECK(hipFree(net.partials));
-        net.partials = nullptr;
-        HIP_CHECK(hipMalloc(&net.partials, need * sizeof(float)));
-        net.partial_capacity = need;
-    }
-    // dW = G * Y^T: A = G (M x K, ld M), B(k, n) = Y[n + N*k] (n-contiguous).
-    {
-        TraceScope trace(d, kTraceWgrad, 2.0 * M * double(N) * K);
-        gemm_dispatch(d, M, N, K, G, M, false, Y, N, true, net.partials, M, nullptr, 1, splits, k_split);
-    }
-    const size_t count = size_t(M) * N;
-    const int blocks = int(std::min<size_t>((count + 255) / 256, 1024));
-    TraceScope trace(d, kTraceSplitReduce, 4.0 * double(count) * (splits + (accumulate ? 2 : 1)));
-    hipLaunchKernelGGL(split_reduce_kernel, blocks, 256, 0, d.stream, net.partials, splits, count, dW,
-                       int(accumulate));
+void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, int NI, int NO, int R, int columns) {
+    TraceScope trace(d, kTraceGemm, 2.0 * NI * NO * double(columns));
+    const int blocks = std::max(1, std::min(4096, (columns + 3) / 4));
+    hipLaunchKernelGGL(output_forward_kernel, blocks, 256, 0, d.stream, W, Y, Z, NI, NO, R, columns);
     HIP_CHECK(hipGetLastError());
 }
 
-// db[m] (+)= sum_p G[(p*R)*M + m]: one block per 64 outputs; lanes stride the
-// points and a fixed tree combines them.
-__global__ __launch_bounds__(256) void bias_grad_kernel(int M, int width, int R, const float* __restrict__ G,
-                                                        float* __restrict__ db, int accumulate) {
-    __shared__ float part[4][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int m = blockIdx.x * 64 + lane;
-    float s = 0.0f;
-    if (m < M)
-        for (int p = wave; p < width; p += 4) s += G[size_t(p) * R * M + m];
-    part[wave][lane] = s;
-    __syncthreads();
-    if (wave == 0 && m < M) {
-        const float total = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
-        db[m] = accumulate ? db[m] + total : total;
+// Weight gradients of several transitions in one launch: dW_t = G_t Y_t^T over
+// K = R*width columns, split over K into fixed ranges.  Block = one 64x64 tile
+// of one split of one transition; wave = 32x32 sub-tile on MFMA, operands read
+// straight from the stacks (lanes of a half-wave read 32 consecutive floats of
+// one column).  The tile's split partial is stored row-major [m][N+1]; the
+// blocks of tile column 0 also sum the bias gradient (value-row columns) into
+// entry N.  Partials are reduced in split order by reduce_grouped_kernel, so
+// the result does not depend on scheduling.
+__global__ __launch_bounds__(256) void wgrad_grouped_kernel(WgradArgs a) {
+    int t = 0;
+    while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
+    const int M = a.M[t], N = a.N[t], K = a.K;
+    const int tiles_m = (M + 63) / 64, tiles_n = (N + 63) / 64;
+    const int local = int(blockIdx.x) - a.block_begin[t];
+    const int tile = local % (tiles_m * tiles_n), split = local / (tiles_m * tiles_n);
+    const int m0 = (tile % tiles_m) * 64, n0 = (tile / tiles_m) * 64;
+    const int kbegin = split * a.kchunk[t], kend = min(K, kbegin + a.kchunk[t]);
+    const float* __restrict__ G = a.G[t];
+    const float* __restrict__ Y = a.Y[t];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5;
+    const int m = m0 + 32 * (wave & 1) + (lane & 31), n = n0 + 32 * (wave >> 1) + (lane & 31);
+    const bool mv = m < M, nv = n < N;
+    floatx16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    // register double buffering: the next 16 columns are in flight while the
+    // current 16 feed the matrix cores
+    int k = kbegin;
+    float a0[8], b0[8], a1[8], b1[8];
+    auto fetch = [&](float* av, float* bv, int k0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const size_t kk = size_t(k0 + 2 * j + h);
+            av[j] = mv ? G[kk * M + m] : 0.0f;
+            bv[j] = nv ? Y[kk * N + n] : 0.0f;
+        }
+    };
+    auto mma = [&](const float* av, const float* bv) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j], bv[j], acc, 0, 0, 0);
+    };
+    if (k + 16 <= kend) {
+        fetch(a0, b0, k);
+        for (; k + 32 <= kend; k += 32) {
+            fetch(a1, b1, k + 16);
+            mma(a0, b0);
+            if (k + 48 <= kend) fetch(a0, b0, k + 32);
+            mma(a1, b1);
+        }
+        if (k + 16 <= kend) {
+            mma(a0, b0);
+            k += 16;
+        }
+    }
+    for (; k < kend; k += 2) {
+        const int kk = k + h;
+        const float av = (mv && kk < kend) ? G[size_t(kk) * M + m] : 0.0f;
+        const float bv = (nv && kk < kend) ? Y[size_t(kk) * N + n] : 0.0f;
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+    }
+    float* P = a.partial[t] + size_t(split) * M * (N + 1);
+    const int ncol = n0 + 32 * (wave >> 1) + (lane & 31);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int mrow = m0 + 32 * (wave & 1) + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (mrow < M && ncol < N) P[size_t(mrow) * (N + 1) + ncol] = acc[v];
+    }
+    if (n0 == 0 && threadIdx.x < 64) {
+        for (int mm = m0 + int(threadIdx.x); mm < min(M, m0 + 64); mm += 64) {
+            float b = 0.0f;
+            const int first = (kbegin + a.R - 1) / a.R * a.R;
+            for (int c = first; c < kend; c += a.R) b += G[size_t(c) * M + mm];
+            P[size_t(mm) * (N + 1) + N] = b;
+        }
     }
 }
 
-void launch_bias_grad(Device& d, int M, int width, int R, const float* G, float* db, bool accumulate) {
-    TraceScope trace(d, kTraceBiasGrad, 4.0 * (double(width) * M + M));
-    hipLaunchKernelGGL(bias_grad_kernel, (M + 63) / 64, 256, 0, d.stream, M, width, R, G, db, int(accumulate));
+// grad_t[m + M*n] (+)= sum over splits of partial_t[s][m][n], n = N being the
+// bias.  Block = 64 consecutive entries x 4 waves; wave w sums splits
+// s = w, w+4, ... in order, then the four wave sums are added in wave order:
+// a fixed summation order whatever the scheduling.
+__global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
+    __shared__ float part[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int e = blockIdx.x * 64 + lane;
+    const int total = a.begin[a.transitions];
+    float s = 0.0f;
+    int t = 0, j = 0;
+    if (e < total) {
+        while (t + 1 < a.transitions && e >= a.begin[t + 1]) ++t;
+        j = e - a.begin[t];
+        const size_t stride = size_t(a.M[t]) * (a.N[t] + 1);
+        const float* P = a.partial[t] + j;
+        const int S = a.splits[t];
+        float s0 = 0.0f, s1 = 0.0f;
+        int q = wave;
+        for (; q + 4 < S; q += 8) {
+            s0 += P[q * stride];
+            s1 += P[(q + 4) * stride];
+        }
+        if (q < S) s0 += P[q * stride];
+        s = s0 + s1;
+    }
+    part[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && e < total) {
+        const float sum = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+        const int M = a.M[t], N1 = a.N[t] + 1;
+        const int mrow = j / N1, n = j - mrow * N1;
+        float* g = a.grad[t] + mrow + size_t(M) * n;
+        *g = a.accumulate ? *g + sum : sum;
+    }
+}
+
+void launch_wgrad_grouped(Device& d, const WgradArgs& a, double flops) {
+    TraceScope trace(d, kTraceWgrad, flops);
+    hipLaunchKernelGGL(wgrad_grouped_kernel, a.block_begin[a.transitions], 256, 0, d.stream, a);
+    HIP_CHECK(hipGetLastError());
+}
+
+void launch_reduce_grouped(Device& d, const ReduceArgs& a) {
+    double bytes = 0;
+    for (int t = 0; t < a.transitions; ++t)
+        bytes += 4.0 * (a.begin[t + 1] - a.begin[t]) * (a.splits[t] + (a.accumulate ? 2 : 1));
+    TraceScope trace(d, kTraceSplitReduce, bytes);
+    const int total = a.begin[a.transitions];
+    hipLaunchKernelGGL(reduce_grouped_kernel, (total + 63) / 64, 256, 0, d.stream, a);
     HIP_CHECK(hipGetLastError());
 }
 

@@ -77,6 +77,7 @@ SIGNATURES = {
     'cpde_program_destroy': (i32, [vp]),
     'cpde_cost_expression': (i32, [vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, i32]),
     'cpde_graph_execute': (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, i32]),
+    'cpde_jit_prepare': (i32, [i32, i32, vp, i32, vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     'cpde_trace_enable': (i32, [vp, i32]),
     'cpde_trace_read': (i32, [vp, i32, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_double),
                               ctypes.POINTER(ctypes.c_double)]),
@@ -316,6 +317,19 @@ class Plan:
         if self.handle:
             check(load().cpde_plan_destroy(self.handle))
             self.handle = None
+
+
+def jit_prepare(table, neurons, arch='gfx950'):
+    """Compile the fused kernels of (schema, architecture) into the code-object
+    cache; no device needed.  Returns the compiler log."""
+    t = np.ascontiguousarray(table, np.int32)
+    n = np.ascontiguousarray(neurons, np.int32)
+    log = ctypes.create_string_buffer(1 << 16)
+    code = load().cpde_jit_prepare(t.shape[0], t.shape[1] - 1, _ptr(t), len(n), _ptr(n), arch.encode(), log,
+                                   len(log))
+    if code != OK:
+        raise CpdeError(code, load().cpde_last_error().decode('utf-8', 'replace') + log.value.decode())
+    return log.value.decode()
 
 
 def wire_to_stack(a):

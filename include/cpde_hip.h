@@ -191,6 +191,13 @@ int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int coun
                        double* values, double* adjoints, double* multipliers, int* active,
                        cpde_graph_summary* summary, int gradient);
 
+/* Compile the schema-specialised layer-fused kernels of (schema, architecture)
+ * for a GPU architecture (e.g. "gfx950") into the on-disk code-object cache,
+ * without a device.  The reference's analogue is its per-expression NVRTC
+ * compile (cuda/expression_program.hpp:104-121), done lazily at first use. */
+int cpde_jit_prepare(int rows, int variables, const int* table, int layers, const int* neurons, const char* arch,
+                     char* log, size_t log_capacity);
+
 /* ---- timing ---------------------------------------------------------------------- */
 /* Kernel tracing (no counterpart in the reference, which has no built-in
  * profiling): while enabled, every launch is bracketed by HIP events on the

@@ -23,3 +23,11 @@ def device():
     print(f'\n[device] {name} CUs={cus}', flush=True)
     yield d
     d.close()
+
+
+@pytest.fixture(params=['fused', 'table'])
+def path(request, monkeypatch):
+    """Which kernel family a plan uses: the schema-specialised layer-fused
+    kernels or the table-driven ones (chosen at plan creation)."""
+    monkeypatch.setenv('CPDE_FUSED', '1' if request.param == 'fused' else '0')
+    return request.param

@@ -1,0 +1,88 @@
+"""Parity of the HIP epoch with the reference CPU server's golden vectors,
+through the C ABI, on the layer-fused (schema-specialised) kernels and on the
+table-driven kernels.
+
+Bars (order 6): loss relative error <= 1e-4; every
+derivative output row and every weight gradient relative L2 <= 1e-3.  RPROP:
+after one update from a fresh optimizer state, every weight whose reference
+gradient exceeds 1e-3 of the largest must be bit-identical to the reference's.
+"""
+import numpy as np
+import pytest
+
+from cpde_amd import hip
+from helpers import check_gradient, golden_workload, load_golden, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+CASES = ['tiny_order6', 'tiny_3var_order4', 'fourier_order2', 'fourier_order6', 'fourier3d_reduced',
+         'large_reduced']
+
+
+def outputs_of(device, run, wl):
+    """Forward every chunk and gather the output stack in wire layout."""
+    R, n_out = wl.rows, wl.neurons[-1]
+    dest = hip.Buffer(device, R * wl.size * n_out * 4)
+    rows = np.arange(R, dtype=np.int32)
+    for offset in range(0, wl.size, run.width):
+        valid = min(run.width, wl.size - offset)
+        run.plan.activate(run.data, wl.size, rows, offset, valid)
+        run.plan.forward()
+        run.plan.output(dest, wl.size, rows, offset, valid)
+    run._loaded = None
+    out = dest.download(np.float32, R * wl.size * n_out).reshape(R, wl.size, n_out)
+    dest.free()
+    return out
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_epoch_against_reference_server(device, path, name):
+    g = load_golden(name)
+    wl = golden_workload(g)
+    print(f'[case] {name} path={path} neurons={wl.neurons} R={wl.rows} P={wl.size} chunk={wl.chunk}', flush=True)
+    run = hip.MatchingRun(device, wl)
+    assert (run.plan.handle is not None)
+    run.step()
+    device.synchronize()
+    loss = run.loss()
+    rel = abs(loss / g['loss'] - 1)
+    print(f'[result] loss {loss!r} reference {float(g["loss"])!r} rel {rel:.2e}', flush=True)
+    assert rel < 1e-4
+    for t, grad in enumerate(run.gradients()):
+        err = check_gradient(g, t, grad, 1e-3)
+        print(f'[result] transition {t} gradient rel-L2 {err:.2e}', flush=True)
+    out = outputs_of(device, run, wl)
+    worst = max(rel_l2(out[r], g['outputs'][r]) for r in range(wl.rows))
+    print(f'[result] worst output row rel-L2 {worst:.2e}', flush=True)
+    assert worst < 1e-3
+    run.close()
+
+
+@pytest.mark.parametrize('name', ['tiny_order6', 'tiny_3var_order4'])
+def test_first_rprop_step_against_reference_server(device, path, name):
+    g = load_golden(name)
+    wl = golden_workload(g)
+    run = hip.MatchingRun(device, wl)
+    run.step()
+    run.net.rprop()
+    device.synchronize()
+    for t in range(len(wl.neurons) - 1):
+        ref_g = g[f'grad{t}']
+        sure = np.abs(ref_g) > 1e-3 * np.abs(ref_g).max()
+        after = run.net.state(t, 0)
+        np.testing.assert_array_equal(after[sure], g[f'after{t}'][sure])
+        np.testing.assert_array_equal(run.net.state(t, 3)[sure], g[f'step{t}'][sure])
+        assert run.net.active(t) == int(g[f'active{t}'])
+    run.close()
+
+
+def test_chunked_epoch_against_reference_server(device, path):
+    g = load_golden('tiny_order6')
+    wl = golden_workload(g)
+    run = hip.MatchingRun(device, wl, chunk=7)
+    run.step()
+    device.synchronize()
+    assert abs(run.loss() / g['chunk7_loss'] - 1) < 1e-4
+    for t, grad in enumerate(run.gradients()):
+        assert rel_l2(grad, g[f'chunk7_grad{t}']) < 1e-3
+    run.close()

@@ -43,7 +43,7 @@ def random_layer(device, schema, n, points, seed, scale=0.7):
 
 
 @pytest.mark.parametrize('name', list(SCHEMAS))
-def test_linear_step_and_composition(device, name):
+def test_linear_step_and_composition(device, path, name):
     schema = SCHEMAS[name]
     R, V = schema.shape[0], schema.shape[1] - 1
     n, points = 64, 37
@@ -68,7 +68,7 @@ def test_linear_step_and_composition(device, name):
 
 
 @pytest.mark.parametrize('name', list(SCHEMAS))
-def test_adjoint_composition(device, name):
+def test_adjoint_composition(device, path, name):
     schema = SCHEMAS[name]
     R = schema.shape[0]
     n, points = 64, 29
@@ -113,8 +113,8 @@ def small_workload(order, neurons, points, seed=5):
     (2, [2, 48, 40, 24, 1], 101, 0),
     (4, [2, 16, 1], 64, 25),
 ])
-def test_epoch_matches_oracle(device, order, neurons, points, chunk):
-    print(f'[case] epoch order={order} neurons={neurons} points={points} chunk={chunk}', flush=True)
+def test_epoch_matches_oracle(device, path, order, neurons, points, chunk):
+    print(f'[case] epoch path={path} order={order} neurons={neurons} points={points} chunk={chunk}', flush=True)
     wl = small_workload(order, neurons, points)
     run = hip.MatchingRun(device, wl, chunk=chunk or None)
     run.step()

@@ -1,54 +1,12 @@
 """Pins the oracle against golden vectors written by the reference CPU server
 (tests/golden/make_golden.py) and against the reference's published losses.
 CPU only; no GPU and no reference tree needed."""
-from pathlib import Path
-
 import numpy as np
 import pytest
 
 import oracle
 from cpde_amd import workloads as W
-from helpers import rel_l2
-
-GOLDEN = Path(__file__).resolve().parent / 'golden'
-
-
-def checksum(a):
-    a = np.asarray(a, np.float64).ravel()
-    return np.array([a.size, a.sum(), (a * a).sum(), (a * np.arange(a.size) / max(a.size, 1)).sum()])
-
-
-def probes(count, seed=2718):
-    return np.random.default_rng(seed).standard_normal((64, count))
-
-
-def load(name):
-    """A golden record; records of generated workloads get their inputs rebuilt
-    by the workload generator and checked against the stored checksums."""
-    path = GOLDEN / f'{name}.npz'
-    if not path.exists():
-        pytest.skip(f'{path.name} not generated')
-    g = dict(np.load(path, allow_pickle=False))
-    if 'generator' in g:
-        import ast
-        wl = getattr(W, str(g['generator']))(**ast.literal_eval(str(g['generator_args'])))
-        got = np.stack([checksum(wl.points), checksum(wl.target), checksum(wl.row_weights),
-                        checksum(np.concatenate(wl.init))])
-        assert np.allclose(got, g['checksums'], rtol=1e-12, atol=0), 'workload generator drifted'
-        g.update(schema=wl.schema, points=wl.points, target=wl.target, row_weights=wl.row_weights)
-        for t, w in enumerate(wl.init):
-            g[f'init{t}'] = w
-    return g
-
-
-def check_gradient(g, t, grad, tol):
-    if f'grad{t}' in g:
-        assert rel_l2(grad, g[f'grad{t}']) < tol, t
-    else:
-        p = probes(grad.size) @ np.asarray(grad, np.float64)
-        assert np.linalg.norm(p - g[f'grad{t}_probes']) < tol * np.linalg.norm(g[f'grad{t}_probes']), t
-        assert abs(np.linalg.norm(np.asarray(grad, np.float64)) / g[f'grad{t}_norm'] - 1) < tol, t
-
+from helpers import check_gradient, load_golden as load, rel_l2
 
 def transitions(g):
     return len(g['neurons']) - 1
