@@ -36,7 +36,8 @@ METRIC = 'ms/epoch (fwd+cost+wgrad) at order 6, 729 pts; points·derivs/s; % roo
 PUBLISHED_POINTS_DERIVS_PER_S = 729 * 28 / 5.65e-3
 PEAK_FP32_MFMA = 157.3e12   # flop/s, dense
 PEAK_HBM = 8.0e12           # bytes/s
-MFMA_KINDS = {'gemm_forward', 'gemm_transposed', 'gemm_wgrad', 'fused_forward', 'fused_backward'}
+MFMA_KINDS = {'gemm_forward', 'gemm_transposed', 'gemm_wgrad', 'fused_forward', 'fused_backward', 'network_forward',
+              'network_backward'}
 
 WORKLOADS = {
     'fourier_fit_order6': lambda: workloads.fourier_fit(6),

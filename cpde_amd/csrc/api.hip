@@ -174,16 +174,31 @@ static std::string device_arch(int ordinal) {
     return colon == std::string::npos ? arch : arch.substr(0, colon);
 }
 
+// Host mirror of the network-fused kernels' argument block (fused.hip.in).
+struct NetArgsHost {
+    const float* W[32];
+    float* Z[33];
+    float* Y[33];
+    float* G[33];
+    const float* X;
+};
+
+static int fused_points() { return std::max(1, env_int("CPDE_FUSED_POINTS", 2)); }
+static int net_points() { return std::max(1, env_int("CPDE_NET_POINTS", 1)); }
+
 static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const std::vector<int>& neurons) {
-    const int ppb = std::max(1, env_int("CPDE_FUSED_POINTS", 2));
-    const std::string src = fused_source(t, neurons, ppb);
+    const int ppb = fused_points(), nppb = net_points();
+    const std::string src = fused_source(t, neurons, ppb, nppb);
     for (auto& kv : d.fused_modules)
         if (kv.first == src) return kv.second;
     std::string log;
     const std::vector<char> code = compile_module(src, device_arch(d.ordinal), &log);
     auto m = std::make_shared<FusedModule>();
     m->points_per_block = ppb;
+    m->net_points_per_block = nppb;
     HIP_CHECK(hipModuleLoadData(&m->module, code.data()));
+    HIP_CHECK(hipModuleGetFunction(&m->network_forward, m->module, "network_forward_k"));
+    HIP_CHECK(hipModuleGetFunction(&m->network_backward, m->module, "network_backward_k"));
     HIP_CHECK(hipModuleGetFunction(&m->input_layer, m->module, "input_layer_k"));
     HIP_CHECK(hipModuleGetFunction(&m->output_backward, m->module, "output_backward_k"));
     const int L = int(neurons.size());
@@ -202,6 +217,21 @@ static void launch_module(Device& d, hipFunction_t f, unsigned gx, unsigned gy, 
     HIP_CHECK(hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, d.stream, args, nullptr));
 }
 
+static NetArgsHost net_args(Net& n) {
+    NetArgsHost a{};
+    for (int t = 0; t + 1 < n.layers; ++t) a.W[t] = n.state[0][t];
+    for (int l = 0; l < n.layers; ++l) {
+        a.Z[l] = n.z[l];
+        a.Y[l] = n.y[l];
+        a.G[l] = n.g[l];
+    }
+    a.X = n.z[0];
+    return a;
+}
+
+// Mode of the fused path: CPDE_FUSED=2 (default) network-fused, 1 layer-fused.
+static bool network_mode() { return env_int("CPDE_FUSED", 2) >= 2; }
+
 static void fused_forward(Plan& p) {
     Net& n = *p.net;
     Device& d = *n.dev;
@@ -209,6 +239,16 @@ static void fused_forward(Plan& p) {
     const int L = n.layers, R = p.rows;
     int width = p.width;
     const double cols = double(p.columns());
+    if (p.network) {
+        NetArgsHost a = net_args(n);
+        void* args[] = {&a, &width};
+        double flops = 0;
+        for (int t = 0; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
+        TraceScope trace(d, kTraceNetworkForward, flops);
+        launch_module(d, fm.network_forward, unsigned((width + fm.net_points_per_block - 1) / fm.net_points_per_block),
+                      1, args);
+        return;
+    }
     {
         const float* W = n.state[0][0];
         const float* X = n.z[0];
@@ -299,6 +339,19 @@ static void fused_backward(Plan& p, bool accumulate) {
     const int L = n.layers;
     int width = p.width;
     const double cols = double(p.columns());
+    if (p.network) {
+        NetArgsHost a = net_args(n);
+        void* args[] = {&a, &width};
+        double flops = 0;
+        for (int t = 1; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
+        {
+            TraceScope trace(d, kTraceNetworkBackward, flops);
+            launch_module(d, fm.network_backward,
+                          unsigned((width + fm.net_points_per_block - 1) / fm.net_points_per_block), 1, args);
+        }
+        weight_gradients(p, accumulate);
+        return;
+    }
     {
         const int NIo = n.neurons[L - 2], NOo = n.neurons[L - 1];
         const float* W = n.state[0][L - 2];
@@ -520,7 +573,10 @@ int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, i
         HIP_CHECK(hipMemcpyAsync(p->dev_tables, blob.data(), blob.size() * sizeof(int), hipMemcpyHostToDevice,
                                  net->dev->stream));
         reserve_arena(*net, *p);
-        if (fused_eligible(*net, *p)) p->fused = load_fused(*net->dev, p->tables, net->neurons);
+        if (fused_eligible(*net, *p)) {
+            p->fused = load_fused(*net->dev, p->tables, net->neurons);
+            p->network = network_mode();
+        }
         HIP_CHECK(hipStreamSynchronize(net->dev->stream));
         *out = p.release();
     });
@@ -812,7 +868,7 @@ const char* cpde_trace_name(int kind) {
         "compose_forward", "compose_adjoint", "gemm_forward",   "gemm_transposed", "gemm_wgrad",
         "split_reduce",    "bias_grad",       "activate",       "cost",            "reduce",
         "optimizer",       "other",           "fused_input",    "fused_forward",   "fused_backward",
-        "fused_output_backward"};
+        "fused_output_backward", "network_forward", "network_backward"};
     return kind >= 0 && kind < kTraceKinds ? names[kind] : "";
 }
 
@@ -823,10 +879,10 @@ int cpde_jit_prepare(int rows, int variables, const int* table, int layers, cons
     return guarded([&] {
         require(table && neurons && arch && layers >= 3, "invalid argument");
         const Tables t = build_tables(rows, variables, table);
-        const int ppb = std::max(1, env_int("CPDE_FUSED_POINTS", 2));
         std::string text;
         try {
-            compile_module(fused_source(t, std::vector<int>(neurons, neurons + layers), ppb), arch, &text);
+            compile_module(fused_source(t, std::vector<int>(neurons, neurons + layers), fused_points(), net_points()),
+                           arch, &text);
         } catch (...) {
             if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
             throw;

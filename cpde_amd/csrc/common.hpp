@@ -94,6 +94,7 @@ struct Plan {
     int* dev_rows = nullptr;    // device row map of the last activate/output
     std::vector<int> host_rows;
     std::shared_ptr<FusedModule> fused;  // null: table-driven kernels
+    bool network = false;                // fused: one network-wide kernel per pass
     size_t columns() const { return size_t(rows) * size_t(width); }
 };
 
@@ -110,7 +111,8 @@ struct Program {
 enum TraceKind {
     kTraceComposeForward, kTraceComposeAdjoint, kTraceGemm, kTraceGemmTransposed, kTraceWgrad, kTraceSplitReduce,
     kTraceBiasGrad, kTraceActivate, kTraceCost, kTraceReduce, kTraceOptimizer, kTraceOther, kTraceFusedInput,
-    kTraceFusedForward, kTraceFusedBackward, kTraceFusedOutput, kTraceKinds
+    kTraceFusedForward, kTraceFusedBackward, kTraceFusedOutput, kTraceNetworkForward, kTraceNetworkBackward,
+    kTraceKinds
 };
 struct TraceRecord {
     int kind;
@@ -166,11 +168,13 @@ struct FusedModule {
     hipModule_t module = nullptr;
     hipFunction_t input_layer = nullptr, output_backward = nullptr;
     std::vector<hipFunction_t> hidden_forward, hidden_backward;  // per transition (index t)
-    int points_per_block = 2;
+    hipFunction_t network_forward = nullptr, network_backward = nullptr;
+    int points_per_block = 2, net_points_per_block = 1;
     ~FusedModule();
 };
 std::string compose_source(const Tables& t);
-std::string fused_source(const Tables& t, const std::vector<int>& neurons, int points_per_block);
+std::string fused_source(const Tables& t, const std::vector<int>& neurons, int points_per_block,
+                         int net_points_per_block);
 std::vector<char> compile_module(const std::string& source, const std::string& arch, std::string* log);
 
 // Brackets one launch with events when tracing is on.

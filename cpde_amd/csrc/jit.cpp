@@ -254,12 +254,35 @@ std::vector<char> compile_module(const std::string& source, const std::string& a
 }
 
 // Full source of the fused module for a schema and architecture.
-std::string fused_source(const Tables& t, const std::vector<int>& neurons, int points_per_block) {
+std::string fused_source(const Tables& t, const std::vector<int>& neurons, int points_per_block,
+                         int net_points_per_block) {
     std::ostringstream o;
+    const int L = int(neurons.size());
+    int widest = 0;
+    for (int l = 1; l + 1 < L; ++l) widest = std::max(widest, neurons[l]);
     o << "// generated: cPDE layer-fused kernels\n#define CPDE_POINTS " << points_per_block << "\n";
+    o << "#define CPDE_NET_POINTS " << net_points_per_block << "\n";
+    o << "#define CPDE_STRIDE " << ((widest + 7) / 8 * 8 + 4) << "\n";
     o << compose_source(t);
     o << kFusedSource;
-    const int L = int(neurons.size());
+    // network-fused forward and backward, one call per layer with its widths
+    o << "\nextern \"C\" __global__ __launch_bounds__(256, 2) void network_forward_k(NetArgs a, int points) {\n"
+         "    __shared__ __attribute__((aligned(16))) float buf[kNNC * kS];\n"
+         "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
+         "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, buf, p0, npts);\n"
+         "    zero_pad(buf, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
+         "    __syncthreads();\n";
+    for (int t = 1; t + 2 < L; ++t)
+        o << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", buf, p0, npts);\n";
+    o << "    net_output<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2 << ", buf, p0, npts);\n}\n";
+    o << "extern \"C\" __global__ __launch_bounds__(256, 2) void network_backward_k(NetArgs a, int points) {\n"
+         "    __shared__ __attribute__((aligned(16))) float buf[kNNC * kS];\n"
+         "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
+         "    net_output_backward<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2
+      << ", buf, p0, npts);\n";
+    for (int t = L - 3; t >= 1; --t)
+        o << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", buf, p0, npts);\n";
+    o << "}\n";
     o << "\nextern \"C\" __global__ __launch_bounds__(256) void input_layer_k(const float* W, const float* X, float* Z,"
          " float* Y, int points) { input_layer<"
       << neurons[0] << ", " << neurons[1] << ">(W, X, Z, Y, points); }\n";

@@ -25,9 +25,10 @@ def device():
     d.close()
 
 
-@pytest.fixture(params=['fused', 'table'])
+@pytest.fixture(params=['network', 'layer', 'table'])
 def path(request, monkeypatch):
-    """Which kernel family a plan uses: the schema-specialised layer-fused
-    kernels or the table-driven ones (chosen at plan creation)."""
-    monkeypatch.setenv('CPDE_FUSED', '1' if request.param == 'fused' else '0')
+    """Which kernel family a plan uses (chosen at plan creation): the
+    schema-specialised network-fused or layer-fused kernels, or the
+    table-driven ones."""
+    monkeypatch.setenv('CPDE_FUSED', {'network': '2', 'layer': '1', 'table': '0'}[request.param])
     return request.param
