@@ -181,21 +181,31 @@ struct NetArgsHost {
     float* Y[33];
     float* G[33];
     const float* X;
+    float* partial_in;
+    float* partial_out;
 };
 
-static int fused_points() { return std::max(1, env_int("CPDE_FUSED_POINTS", 2)); }
-static int net_points() { return std::max(1, env_int("CPDE_NET_POINTS", 1)); }
+static FusedTuning tuning() {
+    FusedTuning t;
+    t.points_per_block = std::max(1, env_int("CPDE_FUSED_POINTS", t.points_per_block));
+    t.net_points_per_block = std::max(1, env_int("CPDE_NET_POINTS", t.net_points_per_block));
+    t.max_split = std::max(1, env_int("CPDE_NET_SPLIT", t.max_split));
+    t.max_split_adjoint = std::max(1, env_int("CPDE_NET_SPLIT_ADJOINT", t.max_split_adjoint));
+    t.forward_blocks = std::max(1, env_int("CPDE_NET_FWD_OCC", t.forward_blocks));
+    t.backward_blocks = std::max(1, env_int("CPDE_NET_BWD_OCC", t.backward_blocks));
+    return t;
+}
 
 static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const std::vector<int>& neurons) {
-    const int ppb = fused_points(), nppb = net_points();
-    const std::string src = fused_source(t, neurons, ppb, nppb);
+    const FusedTuning tune = tuning();
+    const std::string src = fused_source(t, neurons, tune);
     for (auto& kv : d.fused_modules)
         if (kv.first == src) return kv.second;
     std::string log;
     const std::vector<char> code = compile_module(src, device_arch(d.ordinal), &log);
     auto m = std::make_shared<FusedModule>();
-    m->points_per_block = ppb;
-    m->net_points_per_block = nppb;
+    m->points_per_block = tune.points_per_block;
+    m->net_points_per_block = tune.net_points_per_block;
     HIP_CHECK(hipModuleLoadData(&m->module, code.data()));
     HIP_CHECK(hipModuleGetFunction(&m->network_forward, m->module, "network_forward_k"));
     HIP_CHECK(hipModuleGetFunction(&m->network_backward, m->module, "network_backward_k"));
@@ -272,64 +282,90 @@ static void fused_forward(Plan& p) {
                           int(p.columns()));
 }
 
-// Grouped weight gradient of every transition (dW_t = G_{t+1} Y_t^T plus the
-// bias), split over the columns; splits are shared out in proportion to each
-// transition's (tile-padded) work so the launch holds about two blocks per CU.
-static void weight_gradients(Plan& p, bool accumulate) {
+// Weight gradients of every transition (dW_t = G_{t+1} Y_t^T plus the bias),
+// split over the columns.  Transitions marked `external` have their split
+// partials written by another kernel (the network-fused backward writes one
+// per block for the input and output transitions); the others are computed by
+// the grouped launch, whose matrix-core splits are shared out in proportion to
+// each transition's 128x128 tiles, about one block per CU.
+struct GradientPlan {
+    WgradArgs wa{};
+    ReduceArgs ra{};
+    std::vector<size_t> offset;
+    double flops = 0;
+    size_t total = 0;
+};
+
+static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<int>& external_splits) {
     Net& n = *p.net;
     Device& d = *n.dev;
     const int L = n.layers, T = L - 1, K = int(p.columns());
-    WgradArgs wa{};
-    ReduceArgs ra{};
-    wa.transitions = T;
-    wa.K = K;
-    wa.R = p.rows;
-    double total_tiles = 0, flops = 0;
-    for (int t = 0; t < T; ++t) total_tiles += ((n.neurons[t + 1] + 63) / 64) * ((n.neurons[t] + 63) / 64);
-    size_t offset = 0;
-    std::vector<size_t> part_offset(T);
-    std::vector<int> splits(T);
-    wa.block_begin[0] = 0;
+    GradientPlan g;
+    g.offset.assign(T, 0);
+    auto thin = [&](int t) { return n.neurons[t + 1] <= 16 || n.neurons[t] <= 16; };
+    double total_tiles = 0;
+    for (int t = 0; t < T; ++t)
+        if (!thin(t) && !external_splits[t]) total_tiles += ((n.neurons[t + 1] + 127) / 128) * ((n.neurons[t] + 127) / 128);
+    g.wa.K = K;
+    g.wa.R = p.rows;
+    g.wa.block_begin[0] = 0;
+    g.ra.accumulate = accumulate ? 1 : 0;
+    g.ra.transitions = T;
+    g.ra.begin[0] = 0;
+    g.ra.block_begin[0] = 0;
+    int w = 0;
     for (int t = 0; t < T; ++t) {
         const int M = n.neurons[t + 1], N = n.neurons[t];
-        const int tiles = ((M + 63) / 64) * ((N + 63) / 64);
-        int s = int(2.0 * d.compute_units / total_tiles + 0.5);
-        s = std::max(1, std::min(s, std::max(1, K / 64)));
-        int chunk = (K + s - 1) / s;
-        chunk = (chunk + 15) / 16 * 16;
-        s = (K + chunk - 1) / chunk;
-        splits[t] = s;
-        wa.M[t] = M;
-        wa.N[t] = N;
-        wa.kchunk[t] = chunk;
-        wa.block_begin[t + 1] = wa.block_begin[t] + tiles * s;
-        wa.G[t] = n.g[t + 1];
-        wa.Y[t] = n.linear[t] ? n.z[t] : n.y[t];
-        part_offset[t] = offset;
-        offset += size_t(s) * M * (N + 1);
-        flops += 2.0 * M * N * double(K);
+        int s = external_splits[t];
+        if (!s) {
+            const int tiles = thin(t) ? 1 : ((M + 127) / 128) * ((N + 127) / 128);
+            s = thin(t) ? 2 * d.compute_units : int(double(d.compute_units) / total_tiles + 0.5);
+            s = std::max(1, std::min(s, std::max(1, K / 64)));
+            int chunk = (K + s - 1) / s;
+            chunk = (chunk + 31) / 32 * 32;
+            s = (K + chunk - 1) / chunk;
+            g.wa.M[w] = M;
+            g.wa.N[w] = N;
+            g.wa.kchunk[w] = chunk;
+            g.wa.block_begin[w + 1] = g.wa.block_begin[w] + tiles * s;
+            g.wa.G[w] = n.g[t + 1];
+            g.wa.Y[w] = n.linear[t] ? n.z[t] : n.y[t];
+            g.flops += 2.0 * M * N * double(K);
+            ++w;
+        }
+        g.offset[t] = g.total;
+        g.total += size_t(s) * M * (N + 1);
+        g.ra.M[t] = M;
+        g.ra.N[t] = N;
+        g.ra.splits[t] = s;
+        g.ra.grad[t] = n.state[n.active[t]][t];
+        g.ra.begin[t + 1] = g.ra.begin[t] + M * (N + 1);
+        g.ra.split_minor[t] = external_splits[t] ? 1 : 0;
+        g.ra.block_begin[t + 1] = g.ra.block_begin[t] + reduce_blocks(M * (N + 1), external_splits[t] != 0);
     }
-    if (offset > n.partial_capacity) {
+    g.wa.transitions = w;
+    if (g.total > n.partial_capacity) {
         HIP_CHECK(hipStreamSynchronize(d.stream));
         if (n.partials) HIP_CHECK(hipFree(n.partials));
         n.partials = nullptr;
-        HIP_CHECK(hipMalloc(&n.partials, offset * sizeof(float)));
-        n.partial_capacity = offset;
+        HIP_CHECK(hipMalloc(&n.partials, g.total * sizeof(float)));
+        n.partial_capacity = g.total;
     }
-    for (int t = 0; t < T; ++t) wa.partial[t] = n.partials + part_offset[t];
-    launch_wgrad_grouped(d, wa, flops);
-    ra.transitions = T;
-    ra.accumulate = accumulate ? 1 : 0;
-    ra.begin[0] = 0;
+    w = 0;
     for (int t = 0; t < T; ++t) {
-        ra.partial[t] = wa.partial[t];
-        ra.grad[t] = n.state[n.active[t]][t];
-        ra.M[t] = n.neurons[t + 1];
-        ra.N[t] = n.neurons[t];
-        ra.splits[t] = splits[t];
-        ra.begin[t + 1] = ra.begin[t] + n.neurons[t + 1] * (n.neurons[t] + 1);
+        g.ra.partial[t] = n.partials + g.offset[t];
+        if (!external_splits[t]) g.wa.partial[w++] = n.partials + g.offset[t];
     }
-    launch_reduce_grouped(d, ra);
+    return g;
+}
+
+static void run_gradients(Device& d, const GradientPlan& g) {
+    if (g.wa.transitions > 0) launch_wgrad_grouped(d, g.wa, g.flops);
+    launch_reduce_grouped(d, g.ra);
+}
+
+static void weight_gradients(Plan& p, bool accumulate) {
+    run_gradients(*p.net->dev, plan_gradients(p, accumulate, std::vector<int>(p.net->layers - 1, 0)));
 }
 
 static void fused_backward(Plan& p, bool accumulate) {
@@ -340,16 +376,21 @@ static void fused_backward(Plan& p, bool accumulate) {
     int width = p.width;
     const double cols = double(p.columns());
     if (p.network) {
+        const int blocks = (width + fm.net_points_per_block - 1) / fm.net_points_per_block;
+        std::vector<int> external(L - 1, 0);
+        external[0] = external[L - 2] = blocks;
+        const GradientPlan g = plan_gradients(p, accumulate, external);
         NetArgsHost a = net_args(n);
+        a.partial_in = n.partials + g.offset[0];
+        a.partial_out = n.partials + g.offset[L - 2];
         void* args[] = {&a, &width};
         double flops = 0;
         for (int t = 1; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
         {
             TraceScope trace(d, kTraceNetworkBackward, flops);
-            launch_module(d, fm.network_backward,
-                          unsigned((width + fm.net_points_per_block - 1) / fm.net_points_per_block), 1, args);
+            launch_module(d, fm.network_backward, unsigned(blocks), 1, args);
         }
-        weight_gradients(p, accumulate);
+        run_gradients(d, g);
         return;
     }
     {
@@ -881,8 +922,7 @@ int cpde_jit_prepare(int rows, int variables, const int* table, int layers, cons
         const Tables t = build_tables(rows, variables, table);
         std::string text;
         try {
-            compile_module(fused_source(t, std::vector<int>(neurons, neurons + layers), fused_points(), net_points()),
-                           arch, &text);
+            compile_module(fused_source(t, std::vector<int>(neurons, neurons + layers), tuning()), arch, &text);
         } catch (...) {
             if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
             throw;

@@ -159,9 +159,13 @@ struct ReduceArgs {
     const float* partial[kMaxTransitions];
     float* grad[kMaxTransitions];
     int M[kMaxTransitions], N[kMaxTransitions], splits[kMaxTransitions];
-    int begin[kMaxTransitions + 1];
+    int begin[kMaxTransitions + 1];        // first entry of each transition (bytes accounting)
+    int block_begin[kMaxTransitions + 1];  // first block of each transition
+    int split_minor[kMaxTransitions];      // partial layout: 0 [split][entry], 1 [entry][split]
     int transitions, accumulate;
 };
+// Blocks reduce_grouped_kernel uses for a transition of `count` entries.
+inline int reduce_blocks(int count, bool split_minor) { return split_minor ? (count + 3) / 4 : (count + 63) / 64; }
 
 // Schema-specialised layer-fused kernels of one plan (jit.cpp, fused.hip.in).
 struct FusedModule {
@@ -172,9 +176,16 @@ struct FusedModule {
     int points_per_block = 2, net_points_per_block = 1;
     ~FusedModule();
 };
-std::string compose_source(const Tables& t);
-std::string fused_source(const Tables& t, const std::vector<int>& neurons, int points_per_block,
-                         int net_points_per_block);
+std::string compose_source(const Tables& t, const std::vector<int>& splits);
+// Launch-shape choices of the fused kernels (environment overrides in api.hip).
+struct FusedTuning {
+    int points_per_block = 2;      // layer-fused kernels
+    int net_points_per_block = 1;  // network-fused kernels
+    int max_split = 4;             // lanes per composition, at most
+    int max_split_adjoint = 1;     // lanes per adjoint composition, at most
+    int forward_blocks = 2, backward_blocks = 2;  // blocks per CU the register budget must allow
+};
+std::string fused_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning);
 std::vector<char> compile_module(const std::string& source, const std::string& arch, std::string* log);
 
 // Brackets one launch with events when tracing is on.

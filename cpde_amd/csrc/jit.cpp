@@ -116,52 +116,118 @@ std::string emit_partition_sum(std::ostringstream& o, Products& P, const Tables&
 
 }  // namespace
 
-std::string compose_source(const Tables& t) {
-    std::ostringstream o;
-    o << "#define CPDE_R " << t.rows << "\n";
-    // forward
-    o << "__device__ __forceinline__ void compose_forward(const float* __restrict__ z, float* __restrict__ y) {\n";
+namespace {
+
+int forward_terms(const Tables& t, int r) {
+    if (r == 0) return 1;
+    int pos = t.fwd_offset[r];
+    const int k = t.words[pos++];
+    int terms = 0;
+    for (int m = 1; m <= k; ++m) {
+        const int count = t.words[pos++];
+        terms += count;
+        pos += 3 * count;
+    }
+    return terms;
+}
+
+// Rows split into G groups of balanced cost (greedy, largest first).
+std::vector<int> row_groups(int rows, int G, const std::vector<int>& cost) {
+    std::vector<int> order(rows), group(rows, 0);
+    for (int r = 0; r < rows; ++r) order[r] = r;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return cost[a] > cost[b]; });
+    std::vector<long> load(G, 0);
+    for (int r : order) {
+        const int g = int(std::min_element(load.begin(), load.end()) - load.begin());
+        group[r] = g;
+        load[g] += cost[r];
+    }
+    return group;
+}
+
+// compose_forward rows where owned[r]; the others of y are left untouched.
+void emit_forward(std::ostringstream& o, const Tables& t, const std::string& name, const std::vector<char>& owned) {
+    o << "__device__ __forceinline__ void " << name << "(const float* __restrict__ z, float* __restrict__ y) {\n";
     emit_sigma(o, std::max(1, t.max_order));
-    o << "    y[0] = 1.0f / (1.0f + expf(-z[0]));\n";
-    {
-        Products P{o, {}};
-        for (int r = 1; r < t.rows; ++r) {
-            const std::string v = emit_partition_sum(o, P, t, r, 0, "f" + std::to_string(r));
-            o << "    y[" << r << "] = " << v << ";\n";
-        }
+    if (owned[0]) o << "    y[0] = 1.0f / (1.0f + expf(-z[0]));\n";
+    Products P{o, {}};
+    for (int r = 1; r < t.rows; ++r) {
+        if (!owned[r]) continue;
+        const std::string v = emit_partition_sum(o, P, t, r, 0, "f" + std::to_string(r));
+        o << "    y[" << r << "] = " << v << ";\n";
     }
     o << "}\n";
-    // adjoint
-    o << "__device__ __forceinline__ void compose_adjoint(const float* __restrict__ z, const float* __restrict__ gy,"
+}
+
+// compose_adjoint outputs gz[i] where owned[i]; the others are left untouched.
+void emit_adjoint(std::ostringstream& o, const Tables& t, const std::string& name, const std::vector<char>& owned) {
+    o << "__device__ __forceinline__ void " << name << "(const float* __restrict__ z, const float* __restrict__ gy,"
          " float* __restrict__ gz) {\n";
     emit_sigma(o, t.max_order + 1);
-    {
-        std::vector<char> needed(t.rows, 0);
-        for (int i = 0; i < t.rows; ++i) {
-            int pos = t.pair_offset[i];
-            const int count = t.words[pos++];
-            for (int q = 0; q < count; ++q, pos += 3) needed[t.words[pos + 1]] = 1;
+    std::vector<char> needed(t.rows, 0);
+    for (int i = 0; i < t.rows; ++i) {
+        if (!owned[i]) continue;
+        int pos = t.pair_offset[i];
+        const int count = t.words[pos++];
+        for (int q = 0; q < count; ++q, pos += 3) needed[t.words[pos + 1]] = 1;
+    }
+    Products P{o, {}};
+    for (int r = 1; r < t.rows; ++r) {
+        if (!needed[r]) continue;
+        const std::string v = emit_partition_sum(o, P, t, r, 1, "d" + std::to_string(r));
+        o << "    const float D" << r << " = " << v << ";\n";
+    }
+    for (int i = 0; i < t.rows; ++i) {
+        if (!owned[i]) continue;
+        int pos = t.pair_offset[i];
+        const int count = t.words[pos++];
+        o << "    { float acc = s1 * gy[" << i << "];\n";
+        for (int q = 0; q < count; ++q, pos += 3) {
+            const int j = t.words[pos], dn = t.words[pos + 1];
+            require(dn > 0, "adjoint pair refers to the value row");
+            const float c = word_float(t.words[pos + 2]);
+            o << "      acc = acc + (" << flit(c) << " * gy[" << j << "]) * D" << dn << ";\n";
         }
-        Products P{o, {}};
-        for (int r = 1; r < t.rows; ++r) {
-            if (!needed[r]) continue;
-            const std::string v = emit_partition_sum(o, P, t, r, 1, "d" + std::to_string(r));
-            o << "    const float D" << r << " = " << v << ";\n";
-        }
-        for (int i = 0; i < t.rows; ++i) {
-            int pos = t.pair_offset[i];
-            const int count = t.words[pos++];
-            o << "    { float acc = s1 * gy[" << i << "];\n";
-            for (int q = 0; q < count; ++q, pos += 3) {
-                const int j = t.words[pos], dn = t.words[pos + 1];
-                require(dn > 0, "adjoint pair refers to the value row");
-                const float c = word_float(t.words[pos + 2]);
-                o << "      acc = acc + (" << flit(c) << " * gy[" << j << "]) * D" << dn << ";\n";
-            }
-            o << "      gz[" << i << "] = acc; }\n";
-        }
+        o << "      gz[" << i << "] = acc; }\n";
     }
     o << "}\n";
+}
+
+}  // namespace
+
+// compose_forward / compose_adjoint for all rows, and for each G in `splits`
+// the G partial versions compose_forward_G<G>_<g> / compose_adjoint_G<G>_<g>
+// plus the row-to-group tables kForwardGroup<G>[R] / kAdjointGroup<G>[R].
+std::string compose_source(const Tables& t, const std::vector<int>& splits) {
+    std::ostringstream o;
+    o << "#define CPDE_R " << t.rows << "\n";
+    const std::vector<char> all(t.rows, 1);
+    emit_forward(o, t, "compose_forward", all);
+    emit_adjoint(o, t, "compose_adjoint", all);
+    std::vector<int> fcost(t.rows), acost(t.rows);
+    for (int r = 0; r < t.rows; ++r) {
+        fcost[r] = forward_terms(t, r) + 1;
+        acost[r] = t.words[t.pair_offset[r]] + 1;
+    }
+    for (int G : splits) {
+        if (G <= 1) continue;
+        const std::vector<int> fg = row_groups(t.rows, G, fcost), ag = row_groups(t.rows, G, acost);
+        for (int which = 0; which < 2; ++which) {
+            const std::vector<int>& grp = which ? ag : fg;
+            o << "constexpr unsigned char k" << (which ? "Adjoint" : "Forward") << "Group" << G << "[" << t.rows
+              << "] = {";
+            for (int r = 0; r < t.rows; ++r) o << (r ? ", " : "") << grp[r];
+            o << "};\n";
+            for (int g = 0; g < G; ++g) {
+                std::vector<char> owned(t.rows, 0);
+                for (int r = 0; r < t.rows; ++r) owned[r] = grp[r] == g;
+                const std::string name = std::string(which ? "compose_adjoint_G" : "compose_forward_G") +
+                                         std::to_string(G) + "_" + std::to_string(g);
+                if (which) emit_adjoint(o, t, name, owned);
+                else emit_forward(o, t, name, owned);
+            }
+        }
+    }
     return o.str();
 }
 
@@ -254,8 +320,8 @@ std::vector<char> compile_module(const std::string& source, const std::string& a
 }
 
 // Full source of the fused module for a schema and architecture.
-std::string fused_source(const Tables& t, const std::vector<int>& neurons, int points_per_block,
-                         int net_points_per_block) {
+std::string fused_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning) {
+    const int points_per_block = tuning.points_per_block, net_points_per_block = tuning.net_points_per_block;
     std::ostringstream o;
     const int L = int(neurons.size());
     int widest = 0;
@@ -263,25 +329,46 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, int p
     o << "// generated: cPDE layer-fused kernels\n#define CPDE_POINTS " << points_per_block << "\n";
     o << "#define CPDE_NET_POINTS " << net_points_per_block << "\n";
     o << "#define CPDE_STRIDE " << ((widest + 7) / 8 * 8 + 4) << "\n";
-    o << compose_source(t);
+    o << "#define CPDE_MAX_SPLIT " << tuning.max_split << "\n";
+    o << "#define CPDE_MAX_SPLIT_ADJOINT " << tuning.max_split_adjoint << "\n";
+    // row splits of the compositions used by the network-fused kernels
+    std::vector<int> splits;
+    for (int l = 1; l + 1 < L; ++l) {
+        const int lanes = net_points_per_block * neurons[l];
+        const int G = lanes * 4 <= 256 ? 4 : (lanes * 2 <= 256 ? 2 : 1);
+        for (int cap : {tuning.max_split, tuning.max_split_adjoint}) {
+            const int g = std::min(G, cap);
+            if (std::find(splits.begin(), splits.end(), g) == splits.end()) splits.push_back(g);
+        }
+    }
+    for (int G : splits)
+        if (G > 1) o << "#define CPDE_SPLIT" << G << " 1\n";
+    o << compose_source(t, splits);
     o << kFusedSource;
     // network-fused forward and backward, one call per layer with its widths
-    o << "\nextern \"C\" __global__ __launch_bounds__(256, 2) void network_forward_k(NetArgs a, int points) {\n"
-         "    __shared__ __attribute__((aligned(16))) float buf[kNNC * kS];\n"
+    o << "\nextern \"C\" __global__ __launch_bounds__(256, " << tuning.forward_blocks << ") void network_forward_k(NetArgs a, int points) {\n"
+         "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
+         "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n"
          "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
-         "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, buf, p0, npts);\n"
-         "    zero_pad(buf, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
+         "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
+         "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
          "    __syncthreads();\n";
     for (int t = 1; t + 2 < L; ++t)
-        o << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", buf, p0, npts);\n";
-    o << "    net_output<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2 << ", buf, p0, npts);\n}\n";
-    o << "extern \"C\" __global__ __launch_bounds__(256, 2) void network_backward_k(NetArgs a, int points) {\n"
-         "    __shared__ __attribute__((aligned(16))) float buf[kNNC * kS];\n"
+        o << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
+    o << "    net_output<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2 << ", X, p0, npts);\n}\n";
+    o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
+      << ") void network_backward_k(NetArgs a, int points) {\n"
+         "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
+         "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n"
+         "    static_assert(kNPB * " << neurons[L - 1] + 1 << " * " << neurons[L - 2]
+      << " <= kNNC * kS, \"output-gradient scratch exceeds the LDS tile\");\n"
          "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
          "    net_output_backward<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2
-      << ", buf, p0, npts);\n";
+      << ", X, T, p0, npts);\n";
     for (int t = L - 3; t >= 1; --t)
-        o << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", buf, p0, npts);\n";
+        o << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t
+          << ", X, T, p0, npts);\n";
+    o << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
     o << "}\n";
     o << "\nextern \"C\" __global__ __launch_bounds__(256) void input_layer_k(const float* W, const float* X, float* Z,"
          " float* Y, int points) { input_layer<"

@@ -305,116 +305,259 @@ void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, 
 }
 
 // Weight gradients of several transitions in one launch: dW_t = G_t Y_t^T over
-// K = R*width columns, split over K into fixed ranges.  Block = one 64x64 tile
-// of one split of one transition; wave = 32x32 sub-tile on MFMA, operands read
-// straight from the stacks (lanes of a half-wave read 32 consecutive floats of
-// one column).  The tile's split partial is stored row-major [m][N+1]; the
-// blocks of tile column 0 also sum the bias gradient (value-row columns) into
-// entry N.  Partials are reduced in split order by reduce_grouped_kernel, so
-// the result does not depend on scheduling.
-__global__ __launch_bounds__(256) void wgrad_grouped_kernel(WgradArgs a) {
-    int t = 0;
-    while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
+// K = R*width columns, split over K into fixed ranges; each block writes its
+// split's partial row-major [m][N+1] (entry N: the bias gradient, the sum over
+// value-row columns), reduced in split order by reduce_grouped_kernel so the
+// result does not depend on scheduling.  Two block roles:
+//  * matrix-core tiles (M, N > 16): a 64x64 tile, K staged through LDS in
+//    chunks of 16 columns (double-buffered, the next chunk's global loads in
+//    flight during the current chunk's MFMAs); wave = 32x32 sub-tile;
+//  * thin transitions (M or N <= 16: the input and output layers): lanes
+//    stride the wide side and accumulate the narrow side in registers.
+constexpr int kWgKC = 32;        // columns per LDS chunk
+constexpr int kWgLd = 128 + 4;   // LDS row stride of a chunk
+constexpr int kWgTile = 128;     // block tile (M x N)
+
+// Matrix-core tile of one split: 128x128 of dW, wave = 64x64 quadrant made of
+// 2x2 MFMA 32x32 blocks (per k-step: 2 A + 2 B operands feed 4 MFMAs).
+__device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local) {
+    __shared__ __attribute__((aligned(16))) float As[2][kWgKC][kWgLd];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kWgKC][kWgLd];
     const int M = a.M[t], N = a.N[t], K = a.K;
-    const int tiles_m = (M + 63) / 64, tiles_n = (N + 63) / 64;
-    const int local = int(blockIdx.x) - a.block_begin[t];
+    const int tiles_m = (M + kWgTile - 1) / kWgTile, tiles_n = (N + kWgTile - 1) / kWgTile;
     const int tile = local % (tiles_m * tiles_n), split = local / (tiles_m * tiles_n);
-    const int m0 = (tile % tiles_m) * 64, n0 = (tile / tiles_m) * 64;
+    const int m0 = (tile % tiles_m) * kWgTile, n0 = (tile / tiles_m) * kWgTile;
     const int kbegin = split * a.kchunk[t], kend = min(K, kbegin + a.kchunk[t]);
     const float* __restrict__ G = a.G[t];
     const float* __restrict__ Y = a.Y[t];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5;
-    const int m = m0 + 32 * (wave & 1) + (lane & 31), n = n0 + 32 * (wave >> 1) + (lane & 31);
-    const bool mv = m < M, nv = n < N;
-    floatx16 acc;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
-    // register double buffering: the next 16 columns are in flight while the
-    // current 16 feed the matrix cores
-    int k = kbegin;
-    float a0[8], b0[8], a1[8], b1[8];
-    auto fetch = [&](float* av, float* bv, int k0) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const size_t kk = size_t(k0 + 2 * j + h);
-            av[j] = mv ? G[kk * M + m] : 0.0f;
-            bv[j] = nv ? Y[kk * N + n] : 0.0f;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
+    // staging: thread -> 4 consecutive columns at 4*(tid%32) of rows tid/32 + 8j (j < 4)
+    const int sc = 4 * (tid & 31), sr = tid >> 5;
+    const bool vecm = (M % 4) == 0, vecn = (N % 4) == 0;
+    auto load = [&](const float* src, int ld, int c0, int cmax, bool vec, int k) -> float4 {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (k < kend) {
+            const float* p = src + size_t(k) * ld + c0 + sc;
+            if (vec && c0 + sc + 3 < cmax) v = *reinterpret_cast<const float4*>(p);
+            else {
+                if (c0 + sc + 0 < cmax) v.x = p[0];
+                if (c0 + sc + 1 < cmax) v.y = p[1];
+                if (c0 + sc + 2 < cmax) v.z = p[2];
+                if (c0 + sc + 3 < cmax) v.w = p[3];
+            }
         }
+        return v;
     };
-    auto mma = [&](const float* av, const float* bv) {
+    floatx16 acc[2][2];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j], bv[j], acc, 0, 0, 0);
-    };
-    if (k + 16 <= kend) {
-        fetch(a0, b0, k);
-        for (; k + 32 <= kend; k += 32) {
-            fetch(a1, b1, k + 16);
-            mma(a0, b0);
-            if (k + 48 <= kend) fetch(a0, b0, k + 32);
-            mma(a1, b1);
-        }
-        if (k + 16 <= kend) {
-            mma(a0, b0);
-            k += 16;
-        }
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[x][y][v] = 0.0f;
+    float bias = 0.0f;  // tile column 0 blocks: thread tid < 128 sums G[k][m0+tid] over value rows
+    const int wm = 64 * (wave & 1), wn = 64 * (wave >> 1);
+    float4 ga[4], ya[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        ga[j] = load(G, M, m0, M, vecm, kbegin + sr + 8 * j);
+        ya[j] = load(Y, N, n0, N, vecn, kbegin + sr + 8 * j);
     }
-    for (; k < kend; k += 2) {
-        const int kk = k + h;
-        const float av = (mv && kk < kend) ? G[size_t(kk) * M + m] : 0.0f;
-        const float bv = (nv && kk < kend) ? Y[size_t(kk) * N + n] : 0.0f;
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+    int buf = 0;
+    for (int k0 = kbegin; k0 < kend; k0 += kWgKC) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            *reinterpret_cast<float4*>(&As[buf][sr + 8 * j][sc]) = ga[j];
+            *reinterpret_cast<float4*>(&Bs[buf][sr + 8 * j][sc]) = ya[j];
+        }
+        __syncthreads();
+        if (k0 + kWgKC < kend) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ga[j] = load(G, M, m0, M, vecm, k0 + kWgKC + sr + 8 * j);
+                ya[j] = load(Y, N, n0, N, vecn, k0 + kWgKC + sr + 8 * j);
+            }
+        }
+        __builtin_amdgcn_iglp_opt(0);  // interleave the LDS operand reads with the MFMAs
+#pragma unroll
+        for (int kk = 0; kk < kWgKC; kk += 2) {
+            const float a0 = As[buf][kk + h][wm + i], a1 = As[buf][kk + h][wm + 32 + i];
+            const float b0 = Bs[buf][kk + h][wn + i], b1 = Bs[buf][kk + h][wn + 32 + i];
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        if (n0 == 0 && tid < kWgTile) {
+            const int first = (k0 + a.R - 1) / a.R * a.R;
+            for (int c = first; c < min(kend, k0 + kWgKC); c += a.R) bias += As[buf][c - k0][tid];
+        }
+        buf ^= 1;
     }
     float* P = a.partial[t] + size_t(split) * M * (N + 1);
-    const int ncol = n0 + 32 * (wave >> 1) + (lane & 31);
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int mrow = m0 + 32 * (wave & 1) + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (mrow < M && ncol < N) P[size_t(mrow) * (N + 1) + ncol] = acc[v];
-    }
-    if (n0 == 0 && threadIdx.x < 64) {
-        for (int mm = m0 + int(threadIdx.x); mm < min(M, m0 + 64); mm += 64) {
-            float b = 0.0f;
-            const int first = (kbegin + a.R - 1) / a.R * a.R;
-            for (int c = first; c < kend; c += a.R) b += G[size_t(c) * M + mm];
-            P[size_t(mm) * (N + 1) + N] = b;
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int mrow = m0 + wm + 32 * x + 8 * (v >> 2) + 4 * h + (v & 3), ncol = n0 + wn + 32 * y + i;
+                if (mrow < M && ncol < N) P[size_t(mrow) * (N + 1) + ncol] = acc[x][y][v];
+            }
+    if (n0 == 0 && tid < kWgTile && m0 + tid < M) P[size_t(m0 + tid) * (N + 1) + N] = bias;
+}
+
+// Thin transitions: lanes over the wide side (blocks of up to 256), the block
+// split into S = 256/width streams over the split's columns (4 columns in
+// flight per stream), stream partials combined in stream order.
+__device__ __forceinline__ void wgrad_thin(const WgradArgs& a, int t, int split) {
+    __shared__ float red[256 * 17];
+    const int M = a.M[t], N = a.N[t], K = a.K, R = a.R;
+    const int kbegin = split * a.kchunk[t], kend = min(K, kbegin + a.kchunk[t]);
+    const float* __restrict__ G = a.G[t];
+    const float* __restrict__ Y = a.Y[t];
+    float* P = a.partial[t] + size_t(split) * M * (N + 1);
+    const bool wide_m = N <= 16;  // otherwise M <= 16 and the wide side is n
+    const int wide = wide_m ? M : N, narrow = wide_m ? N : M;
+    const int Wc = min(wide, 256), S = 256 / Wc;
+    const int s = threadIdx.x / Wc, w = threadIdx.x - s * Wc;
+    for (int w0 = 0; w0 < wide; w0 += Wc) {
+        const int wi = w0 + w;
+        float acc[16], bias[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[q] = bias[q] = 0.0f;
+        if (s < S && wi < wide) {
+            int k = kbegin + s;
+            for (; k + 3 * S < kend; k += 4 * S) {
+                float wv[4], nv[4][16];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const size_t kk = size_t(k + u * S);
+                    wv[u] = wide_m ? G[kk * M + wi] : Y[kk * N + wi];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                        if (q < narrow) nv[u][q] = wide_m ? Y[kk * N + q] : G[kk * M + q];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const bool value_row = (k + u * S) % R == 0;
+#pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                        if (q < narrow) {
+                            acc[q] = fmaf(wv[u], nv[u][q], acc[q]);
+                            if (value_row) bias[q] += wide_m ? (q == 0 ? wv[u] : 0.0f) : nv[u][q];
+                        }
+                }
+            }
+            for (; k < kend; k += S) {
+                const size_t kk = size_t(k);
+                const float wvv = wide_m ? G[kk * M + wi] : Y[kk * N + wi];
+                const bool value_row = k % R == 0;
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    if (q < narrow) {
+                        const float nvv = wide_m ? Y[kk * N + q] : G[kk * M + q];
+                        acc[q] = fmaf(wvv, nvv, acc[q]);
+                        if (value_row) bias[q] += wide_m ? (q == 0 ? wvv : 0.0f) : nvv;
+                    }
+            }
+        }
+        // wide_m: entries (wi, q) for q < N and the bias of row wi (in bias[0]);
+        // otherwise entries (q, wi) for q < M, and bias[q] (the same in every
+        // lane of a stream) is the bias of row q
+        __syncthreads();  // readers of the previous wide chunk are done
+#pragma unroll
+        for (int q = 0; q < 16; ++q) red[threadIdx.x * 17 + q] = acc[q];
+        red[threadIdx.x * 17 + 16] = wide_m ? bias[0] : 0.0f;
+        __syncthreads();
+        if (s == 0 && wi < wide) {
+            float tot[17];
+#pragma unroll
+            for (int q = 0; q < 17; ++q) tot[q] = 0.0f;
+            for (int ss = 0; ss < S; ++ss)
+#pragma unroll
+                for (int q = 0; q < 17; ++q) tot[q] += red[(ss * Wc + w) * 17 + q];
+            if (wide_m) {
+                for (int q = 0; q < N; ++q) P[size_t(wi) * (N + 1) + q] = tot[q];
+                P[size_t(wi) * (N + 1) + N] = tot[16];
+            } else {
+                for (int q = 0; q < M; ++q) P[size_t(q) * (N + 1) + wi] = tot[q];
+            }
+        }
+        if (!wide_m && w0 == 0) {
+            __syncthreads();
+            if (w == 0 && s < S)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) red[s * 17 + q] = bias[q];
+            __syncthreads();
+            if (int(threadIdx.x) < M) {
+                float b = 0.0f;
+                for (int ss = 0; ss < S; ++ss) b += red[ss * 17 + threadIdx.x];
+                P[size_t(threadIdx.x) * (N + 1) + N] = b;
+            }
         }
     }
 }
 
-// grad_t[m + M*n] (+)= sum over splits of partial_t[s][m][n], n = N being the
-// bias.  Block = 64 consecutive entries x 4 waves; wave w sums splits
-// s = w, w+4, ... in order, then the four wave sums are added in wave order:
-// a fixed summation order whatever the scheduling.
+__global__ __launch_bounds__(256) void wgrad_grouped_kernel(WgradArgs a) {
+    int t = 0;
+    while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
+    const int local = int(blockIdx.x) - a.block_begin[t];
+    if (a.M[t] <= 16 || a.N[t] <= 16) wgrad_thin(a, t, local);
+    else wgrad_tile(a, t, local);
+}
+
+// grad_t[m + M*n] (+)= sum over splits of the partials of entry (m, n), n = N
+// being the bias.  Split-major partials ([split][entry]): block = 64 consecutive
+// entries x 4 waves, wave w sums splits w, w+4, ... (eight running sums,
+// combined in a fixed order), then the four wave sums in wave order.
+// Split-minor partials ([entry][split]): one wave per entry, lane l sums splits
+// l, l+64, ... in order, then a fixed shuffle tree.  Either way the summation
+// order is fixed whatever the scheduling.
 __global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
     __shared__ float part[4][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int e = blockIdx.x * 64 + lane;
-    const int total = a.begin[a.transitions];
-    float s = 0.0f;
-    int t = 0, j = 0;
-    if (e < total) {
-        while (t + 1 < a.transitions && e >= a.begin[t + 1]) ++t;
-        j = e - a.begin[t];
-        const size_t stride = size_t(a.M[t]) * (a.N[t] + 1);
-        const float* P = a.partial[t] + j;
-        const int S = a.splits[t];
-        float s0 = 0.0f, s1 = 0.0f;
-        int q = wave;
-        for (; q + 4 < S; q += 8) {
-            s0 += P[q * stride];
-            s1 += P[(q + 4) * stride];
+    int t = 0;
+    while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
+    const int local = int(blockIdx.x) - a.block_begin[t];
+    const int M = a.M[t], N1 = a.N[t] + 1, S = a.splits[t];
+    const int count = M * N1;
+    if (!a.split_minor[t]) {
+        const size_t stride = size_t(count);
+        const int j = local * 64 + lane;
+        float s = 0.0f;
+        if (j < count) {
+            const float* P = a.partial[t] + j;
+            float acc[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
+            int q = wave;
+            for (; q + 28 < S; q += 32)
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc[u] += P[(q + 4 * u) * stride];
+            for (int u = 0; q < S; q += 4, ++u) acc[u] += P[q * stride];
+            s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
         }
-        if (q < S) s0 += P[q * stride];
-        s = s0 + s1;
-    }
-    part[wave][lane] = s;
-    __syncthreads();
-    if (wave == 0 && e < total) {
-        const float sum = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
-        const int M = a.M[t], N1 = a.N[t] + 1;
-        const int mrow = j / N1, n = j - mrow * N1;
-        float* g = a.grad[t] + mrow + size_t(M) * n;
-        *g = a.accumulate ? *g + sum : sum;
+        part[wave][lane] = s;
+        __syncthreads();
+        if (wave == 0 && j < count) {
+            const float sum = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+            const int mrow = j / N1, n = j - mrow * N1;
+            float* g = a.grad[t] + mrow + size_t(M) * n;
+            *g = a.accumulate ? *g + sum : sum;
+        }
+    } else {
+        const int j = local * 4 + wave;
+        if (j >= count) return;
+        const float* P = a.partial[t] + size_t(j) * S;
+        float s = 0.0f;
+        for (int q = lane; q < S; q += 64) s += P[q];
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+        if (lane == 0) {
+            const int mrow = j / N1, n = j - mrow * N1;
+            float* g = a.grad[t] + mrow + size_t(M) * n;
+            *g = a.accumulate ? *g + s : s;
+        }
     }
 }
 
@@ -429,8 +572,7 @@ void launch_reduce_grouped(Device& d, const ReduceArgs& a) {
     for (int t = 0; t < a.transitions; ++t)
         bytes += 4.0 * (a.begin[t + 1] - a.begin[t]) * (a.splits[t] + (a.accumulate ? 2 : 1));
     TraceScope trace(d, kTraceSplitReduce, bytes);
-    const int total = a.begin[a.transitions];
-    hipLaunchKernelGGL(reduce_grouped_kernel, (total + 63) / 64, 256, 0, d.stream, a);
+    hipLaunchKernelGGL(reduce_grouped_kernel, a.block_begin[a.transitions], 256, 0, d.stream, a);
     HIP_CHECK(hipGetLastError());
 }
 
@@ -544,34 +686,53 @@ void launch_costs_begin(Device& d, int costs) {
 }
 
 // Array-matching squared loss (cuda/cost_kernels.cuh:6-35) on the output stack
-// y [point][row][outputs]; g receives dE/dy.  One lane per point.
+// y [point][row][outputs]; g receives dE/dy.  One lane per (point, component):
+// each lane forms w (y - t)^2 and 2 w (y - t); the per-point loss is then
+// summed in fp32 in component order (as the reference does) by one lane per
+// point, promoted to double, and reduced over the block in a fixed order.
+// Blocks loop over groups of 256 / (rows*outputs) points.
 __global__ __launch_bounds__(kCostThreads) void matching_kernel(
     const float* __restrict__ y, float* __restrict__ g, const float* __restrict__ target, int target_width,
     const int* __restrict__ target_rows, const float* __restrict__ weights, int weight_samples, int R, int outputs,
     int width, int valid, int offset, int collect, int gradient, CostStats* __restrict__ partials) {
+    extern __shared__ float terms[];
+    const int RO = R * outputs;
+    const int ppb = max(1, kCostThreads / RO);
     CostStats local = empty_cost();
-    for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < width; p += blockDim.x * gridDim.x) {
-        float value = 0.0f;
-        for (int d = 0; d < R; ++d)
-            for (int o = 0; o < outputs; ++o) {
-                const size_t i = (size_t(p) * R + d) * outputs + o;
+    for (int p0 = blockIdx.x * ppb; p0 < width; p0 += gridDim.x * ppb) {
+        for (int e = threadIdx.x; e < ppb * RO; e += blockDim.x) {
+            const int pl = e / RO, c = e - pl * RO;
+            const int p = p0 + pl;
+            float term = 0.0f;
+            if (p < width) {
+                const int d = c / outputs, o = c - d * outputs;
+                const size_t i = size_t(p) * RO + c;
                 float gi = 0.0f;
                 if (p < valid) {
                     const int wp = weight_samples == 1 ? 0 : offset + p;
                     const float w = weights[(size_t(d) * weight_samples + wp) * outputs + o];
                     if (w != 0.0f) {
                         const float r = y[i] - target[(size_t(target_rows[d]) * target_width + offset + p) * outputs + o];
-                        value += w * r * r;
+                        term = w * r * r;
                         gi = 2.0f * w * r;
                     }
                 }
                 if (gradient) {
                     g[i] = gi;
-                    if (p < valid && !isfinite(gi)) mark_bad(local, offset + p, d * outputs + o);
+                    if (p < valid && !isfinite(gi)) mark_bad(local, offset + p, c);
                 }
             }
-        if (!isfinite(value)) mark_bad(local, offset + p, -1);
-        if (collect) local.value += double(value);
+            terms[e] = term;
+        }
+        __syncthreads();
+        if (int(threadIdx.x) < ppb && p0 + int(threadIdx.x) < width) {
+            const int p = p0 + threadIdx.x;
+            float value = 0.0f;
+            for (int c = 0; c < RO; ++c) value += terms[threadIdx.x * RO + c];
+            if (!isfinite(value)) mark_bad(local, offset + p, -1);
+            if (collect) local.value += double(value);
+        }
+        __syncthreads();
     }
     local = block_reduce_cost(local);
     if (threadIdx.x == 0) partials[blockIdx.x] = local;
@@ -581,11 +742,15 @@ void launch_matching(Device& d, const Plan& p, const float* y, float* g, const f
                      const int* target_rows, const float* weights, int weight_samples, int offset, int valid,
                      int cost_index, bool collect, bool gradient) {
     const int outputs = p.net->neurons.back();
-    const int blocks = cost_blocks_for(p.width);
+    const int RO = p.rows * outputs;
+    require(RO <= 16384, "matching cost: rows x outputs exceeds 16384");
+    const int ppb = std::max(1, kCostThreads / RO);
+    const int blocks = std::max(1, std::min(kMaxCostBlocks, (p.width + ppb - 1) / ppb));
+    const size_t lds = sizeof(float) * size_t(ppb) * RO;
     {
     // y and target read, g written
     TraceScope trace(d, kTraceCost, 12.0 * double(p.columns()) * outputs);
-    hipLaunchKernelGGL(matching_kernel, blocks, kCostThreads, 0, d.stream, y, g, target, target_width, target_rows,
+    hipLaunchKernelGGL(matching_kernel, blocks, kCostThreads, lds, d.stream, y, g, target, target_width, target_rows,
                        weights, weight_samples, p.rows, outputs, p.width, valid, offset, int(collect), int(gradient),
                        d.cost_blocks);
     HIP_CHECK(hipGetLastError());
