@@ -175,6 +175,74 @@ def case_poisson(s):
     return rec
 
 
+def tiny_workload(seed=11, order=6, neurons=(2, 8, 8, 1), points=30):
+    schema = W.full_schema(2, order)
+    rng = np.random.default_rng(seed)
+    pts = rng.uniform(0, 1, (points, 2))
+    freq, coef, phase = W.fourier_modes(2, 3, 3, seed)
+    target = W.fourier_target(pts, schema, freq, coef, phase)
+    return W.MatchingWorkload('tiny', list(neurons), pts, schema, target, 1.0 / target.var(axis=1),
+                              W.xavier_weights(list(neurons), seed))
+
+
+def case_polynomial(s):
+    """Sparse residuals (op 7 kind 1) on an order-2 schema: equation 0 is
+    linear, c0 u_xx + c1 u_yy - rhs0; equation 1 quadratic, c2 u u_x - rhs1."""
+    wl = tiny_workload(seed=21, order=2, neurons=(2, 10, 9, 1), points=25)
+    rng = np.random.default_rng(21)
+    P = wl.size
+    keys = [tuple(r[1:]) for r in wl.schema]
+    xx, yy, x, v = keys.index((2, 0)), keys.index((0, 2)), keys.index((1, 0)), keys.index((0, 0))
+    terms = np.array([[0, xx, -1], [0, yy, -1], [1, v, x]], np.int32)
+    coeffs = rng.uniform(0.5, 1.5, (3, P)).astype(np.float32)
+    rhs = rng.standard_normal((2, P)).astype(np.float32)
+    weights = rng.uniform(0.2, 1.0, (2, P)).astype(np.float32)
+    weights[1, :3] = 0
+    d = s.data(wl.inputs, wl.schema)
+    n = s.network(wl.neurons, wl.linear, wl.init)
+    rows = list(range(wl.rows))
+    c = s.polynomial_cost(n, d, rows, 2, terms, coeffs, rhs, weights, chunk=10)
+    value, grads = s.graph_eval(n, [c], SINGLE_LEAF, gradient=True)
+    rec = dict(neurons=np.asarray(wl.neurons, np.int32), schema=wl.schema, points=wl.points, terms=terms,
+               coeffs=coeffs, rhs=rhs, weights=weights, chunk=np.int32(10), loss=np.float64(value))
+    for t, w in enumerate(wl.init):
+        rec[f'init{t}'] = np.asarray(w, np.float32)
+    for t, g in enumerate(grads):
+        rec[f'grad{t}'] = g
+    s.train(n, [c], 1, method=0, fresh=1, log=1)
+    _, layers = wire.decode_state(s.snapshot(n))
+    for t, layer in enumerate(layers):
+        rec[f'after{t}'] = layer['buffers'][0]
+    return rec
+
+
+def case_training(s):
+    """Three RPROP epochs with per-epoch reports and gradient diagnostics, then
+    two Adam epochs (lr 0.01) on a fresh network: reported objectives and the
+    final state blobs."""
+    wl = tiny_workload(seed=31, order=4, neurons=(2, 12, 12, 1), points=40)
+    ids = wl.upload(s, 16)
+    res = s.train(ids['net'], [ids['cost']], 3, method=0, fresh=1, log=1, diagnostics=1, eval_every=2)
+    reports = [(e['completed'], e['updates'], e['after'], e['values'][0]) for e in res['events'] if e['kind'] == 2]
+    diag = [(e['epoch'], e['layers'][0]['sq'], e['layers'][0]['max']) for e in res['events'] if e['kind'] == 5]
+    rprop_state = s.snapshot(ids['net'])
+    wl2 = tiny_workload(seed=31, order=4, neurons=(2, 12, 12, 1), points=40)
+    ids2 = wl2.upload(s, 16)
+    res2 = s.train(ids2['net'], [ids2['cost']], 2, method=1, fresh=1, lr=0.01, log=1)
+    adam_reports = [(e['completed'], e['updates'], e['after'], e['values'][0]) for e in res2['events']
+                    if e['kind'] == 2]
+    adam_state = s.snapshot(ids2['net'])
+    rec = dict(neurons=np.asarray(wl.neurons, np.int32), schema=wl.schema, points=wl.points, target=wl.target,
+               row_weights=wl.row_weights, chunk=np.int32(16),
+               reports=np.asarray(reports, np.float64), diagnostics=np.asarray(diag, np.float64),
+               rprop_state=np.frombuffer(rprop_state, np.uint8), adam_reports=np.asarray(adam_reports, np.float64),
+               adam_state=np.frombuffer(adam_state, np.uint8),
+               completed=np.int64(res['completed']), stopped=np.int32(res['stopped']))
+    for t, w in enumerate(wl.init):
+        rec[f'init{t}'] = np.asarray(w, np.float32)
+    return rec
+
+
 CASES = {
     'tiny_order6': case_tiny_order6,
     'tiny_3var_order4': case_tiny_3var_order4,
@@ -184,6 +252,8 @@ CASES = {
     'large_reduced': case_large_reduced,
     'published': case_published,
     'poisson': case_poisson,
+    'polynomial': case_polynomial,
+    'training': case_training,
 }
 
 
