@@ -39,6 +39,17 @@ PEAK_HBM = 8.0e12           # bytes/s
 MFMA_KINDS = {'gemm_forward', 'gemm_transposed', 'gemm_wgrad', 'fused_forward', 'fused_backward', 'network_forward',
               'network_backward'}
 
+# HBM bytes per launch from rocprofv3 counter passes over this benchmark
+# (profiles/network_kernels_fourier_fit_order6_traffic.md): mean FETCH_SIZE and
+# WRITE_SIZE in KiB per dispatch, scaled by what the same counters read for a
+# plain 256 MiB copy (``--copy-calibration``): 268,435,456 B / 131,084.56 KiB
+# read, 268,435,456 B / 262,144 KiB written.
+COPY_SCALE = (268435456 / (131084.5625 * 1024), 268435456 / (262144 * 1024))
+TRAFFIC_KIB = {
+    'fourier_fit_order6': {'network_backward': (27619.29, 53473.79), 'network_forward': (1483.53, 83919.40),
+                           'gemm_wgrad': (30734.39, 20035.63)},
+}
+
 WORKLOADS = {
     'fourier_fit_order6': lambda: workloads.fourier_fit(6),
     'fourier_fit_order2': lambda: workloads.fourier_fit(2),
@@ -58,9 +69,17 @@ def describe(wl, name):
     }
 
 
-def roofline(report):
+def traffic(workload, kind):
+    kib = TRAFFIC_KIB.get(workload, {}).get(kind)
+    if kib is None:
+        return None
+    return round(kib[0] * 1024 * COPY_SCALE[0] + kib[1] * 1024 * COPY_SCALE[1])
+
+
+def roofline(report, workload):
     """Dominant kernel class by device time; achieved = its algorithmic work
-    per launch divided by its mean launch duration."""
+    per launch divided by its mean launch duration; traffic = its measured HBM
+    bytes per launch where a counter pass exists for this workload."""
     kind = max(report, key=lambda k: report[k][1])
     launches, ms, work = report[kind]
     seconds = ms / 1e3
@@ -69,16 +88,48 @@ def roofline(report):
     else:
         achieved, peak, unit, bound = work / seconds / 1e9, PEAK_HBM / 1e9, 'GB/s', 'hbm'
     return {'kernel': kind, 'bound': bound, 'achieved': round(achieved, 3), 'peak': peak, 'unit': unit,
-            'frac': round(achieved / peak, 4), 'traffic': None,
+            'frac': round(achieved / peak, 4), 'traffic': traffic(workload, kind),
             'launches': launches, 'mean_launch_us': round(ms * 1e3 / launches, 3),
             'work_per_launch': work / launches}
 
 
+def server_op90(wl, warm=20, iterations=100, batches=7):
+    """The reference's own timing scope through the protocol server (op 90:
+    forward + cost + weight gradient, no optimizer; C++ host, no Python in the
+    loop): median over batches of per-epoch wall and device milliseconds."""
+    from cpde_amd import wire
+    from cpde_amd.build import SERVER
+    with wire.Session(SERVER) as s:
+        ids = wl.upload(s)
+        r = s.timing(ids['net'], ids['cost'], warm=warm, iterations=iterations, batches=batches,
+                     layers=len(wl.neurons) - 1)
+    wall, gpu = float(np.median(r['wall_ms'])), float(np.median(r['gpu_ms']))
+    return {'ms_per_epoch_wall': round(wall, 5), 'ms_per_epoch_device': round(gpu, 5),
+            'points_derivs_per_s': round(wl.size * wl.rows / (wall / 1e3), 1),
+            'vs_published_5.65ms': round(5.65 / wall, 2) if wl.name.endswith('order6') and wl.size == 729 else None,
+            'loss': r['loss'], 'scope': f'op 90: {batches} batches x {iterations} epochs after {warm} warm-ups'}
+
+
 def cpu_baseline(wl):
-    """The CPU restatement of the same epoch (oracle/, single thread), timed on
-    one full epoch of the workload."""
+    """The CPU side of the same epoch, single thread, one full epoch of the
+    workload.  Preferred: the reference's own CPU server built from its sources
+    (oracle/_ref), driven over the wire protocol with one training epoch (op 8:
+    forward + cost + weight gradient + statistics + RPROP).  Otherwise the C
+    restatement of the same epoch."""
     sys.path.insert(0, str(ROOT / 'oracle'))
     import oracle
+    ref = oracle.reference_server()
+    if ref is not None:
+        from cpde_amd import wire
+        with wire.Session(ref) as s:
+            ids = wl.upload(s)
+            t0 = time.perf_counter()
+            s.train(ids['net'], [ids['cost']], 1, method=0, fresh=1, log=0)
+            seconds = time.perf_counter() - t0
+        return {'value': round(wl.size * wl.rows / seconds, 1), 'unit': 'points·derivs/s', 'cores': 1,
+                'kind': 'reference', 'seconds': round(seconds, 3),
+                'sample': f'one training epoch ({wl.size} points x {wl.rows} rows, {wl.name}) of the reference CPU '
+                          'server (serial BLAS), op 8 train: fwd+cost+wgrad+stats+RPROP, single thread'}
     x = wl.inputs.transpose(0, 2, 1)
     t0 = time.perf_counter()
     oracle.matching_epoch(wl.neurons, wl.linear, wl.init, wl.schema, x, wl.target[:, :, None],
@@ -94,6 +145,21 @@ def cpu_baseline(wl):
                       'fwd+cost+wgrad+RPROP, single thread'}
 
 
+def copy_calibration(mib=256, repeats=5):
+    """A plain device-to-device copy of known size: what FETCH_SIZE and
+    WRITE_SIZE read for it converts those counters into bytes for the kernels
+    measured under the same profiler."""
+    import torch
+    x = torch.ones(mib << 18, dtype=torch.float32, device='cuda')
+    y = torch.empty_like(x)
+    for _ in range(repeats):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({'copy_bytes_read': x.numel() * 4, 'copy_bytes_written': y.numel() * 4,
+                      'launches': repeats}), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -102,13 +168,21 @@ def main(argv=None):
     ap.add_argument('--workload', default='fourier_fit_order6', choices=sorted(WORKLOADS))
     ap.add_argument('--trace-steps', type=int, default=20)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-op90', action='store_true', help='skip the protocol-server timing (op 90)')
+    ap.add_argument('--copy-calibration', action='store_true',
+                    help='only run a plain 256 MiB device copy five times (the reference for HBM byte counters)')
     args = ap.parse_args(argv)
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: the cPDE hot path runs on a single device '
               '(multi-GPU point sharding is a design, not a build, here); run with --gpus 1', file=sys.stderr)
         return 2
 
     wl = WORKLOADS[args.workload]()
+    # The protocol server runs as a child process, started before this process
+    # touches the device.
+    op90 = None if args.no_op90 else server_op90(wl)
     device = hip.Device(0)
     name, cus = device.info()
     run = hip.MatchingRun(device, wl)
@@ -159,13 +233,14 @@ def main(argv=None):
         'epoch_roofline': {'t_roof_us': round(t_roof * 1e6, 2), 'frac': round(t_roof / (ms / 1e3), 4),
                            'gflop': wl.flops_per_epoch() / 1e9, 'gbytes': wl.bytes_per_epoch() / 1e9},
         'loss_after_timed_steps': loss,
-        'roofline': roofline(report),
+        'roofline': roofline(report, args.workload),
         'kernels': {k: {'launches_per_step': v[0] / args.trace_steps, 'us_per_step': round(v[1] * 1e3 /
                         args.trace_steps, 3)} for k, v in sorted(report.items(), key=lambda kv: -kv[1][1])},
         'cpu_baseline': None,
     }
     run.close()
     device.close()
+    out['op90'] = op90
     if not args.no_cpu_baseline:
         out['cpu_baseline'] = cpu_baseline(wl)
     print(json.dumps(out), flush=True)
