@@ -2,14 +2,17 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
 
-One step is one training epoch of a matching cost on the derivative stack:
-forward propagation of every derivative row through the network, the squared
-matching loss against the analytic Fourier derivatives, the weight gradient
-(adjoint compositions, transposed products, split-K weight contraction) and
-one RPROP update -- the work of Server::pass + network::train
-(cuda/cpde_server.cu:223-257, cuda/cpde_engine.cuh:993-1014), a superset of
-the reference's "fwd+cost+wgrad" timing scope.  Inputs, targets and weights are
-resident in HBM before the timed region starts.
+One step is one training epoch: forward propagation of every derivative row
+through the network, the cost, the weight gradient (adjoint compositions,
+transposed products, split-K weight contraction) and one RPROP update -- the
+work of Server::pass + network::train (cuda/cpde_server.cu:223-257,
+cuda/cpde_engine.cuh:993-1014), a superset of the reference's
+"fwd+cost+wgrad" timing scope.  Inputs, targets and weights are resident in
+HBM before the timed region starts.
+
+Matching workloads drive the device library directly through its C ABI; the
+Poisson workload (two expression costs combined by a cost graph) runs through
+the protocol server's training command.
 
 Prints one JSON line.  ``value`` is points x derivative rows per second for the
 whole job; ``ms_per_step`` the wall-clock milliseconds per epoch.
@@ -20,8 +23,11 @@ import argparse
 import json
 import os
 import sys
+import tempfile
 import time
+from dataclasses import dataclass
 from pathlib import Path
+from typing import Callable
 
 import numpy as np
 
@@ -38,6 +44,10 @@ PEAK_FP32_MFMA = 157.3e12   # flop/s, dense
 PEAK_HBM = 8.0e12           # bytes/s
 MFMA_KINDS = {'gemm_forward', 'gemm_transposed', 'gemm_wgrad', 'fused_forward', 'fused_backward', 'network_forward',
               'network_backward'}
+# CPU baseline sample: about this many multiply-adds of the linear steps
+# (rows x points x sum of n_in*n_out), ~12 s of the reference CPU server on
+# one core of the benchmark host.
+CPU_SAMPLE_MACS = 3.0e9
 
 # HBM bytes per launch from rocprofv3 counter passes over this benchmark
 # (profiles/network_kernels_fourier_fit_order6_traffic.md): mean FETCH_SIZE and
@@ -50,15 +60,31 @@ TRAFFIC_KIB = {
                            'gemm_wgrad': (30734.39, 20035.63)},
 }
 
+
+@dataclass
+class Spec:
+    make: Callable
+    steps: int          # timed epochs by default
+    warmup: int
+    trace_steps: int
+    op90: tuple | None  # (warm-ups, epochs per batch, batches) of the server timing command
+    server: bool = False
+
+
 WORKLOADS = {
-    'fourier_fit_order6': lambda: workloads.fourier_fit(6),
-    'fourier_fit_order2': lambda: workloads.fourier_fit(2),
-    'fourier_3d_order4': lambda: workloads.fourier_3d(),
-    'fourier_large_order6': lambda: workloads.fourier_large(),
+    'fourier_fit_order6': Spec(lambda: workloads.fourier_fit(6), 500, 50, 20, (20, 100, 7)),
+    'fourier_fit_order2': Spec(lambda: workloads.fourier_fit(2), 500, 50, 20, (20, 100, 7)),
+    'poisson_disk_order2': Spec(lambda: workloads.PoissonWorkload(), 500, 50, 20, None, server=True),
+    'fourier_3d_order4': Spec(lambda: workloads.fourier_3d(), 30, 3, 3, (3, 10, 3)),
+    'fourier_large_order6': Spec(lambda: workloads.fourier_large(), 10, 2, 2, (2, 3, 3)),
 }
 
 
 def describe(wl, name):
+    if isinstance(wl, workloads.PoissonWorkload):
+        return {'workload': name, 'network': '→'.join(str(n) for n in wl.neurons) + ' sigmoid',
+                'points': wl.size, 'leaves': [{'rows': r, 'points': p} for r, p in wl.leaves()],
+                'step': 'graph pass (interior (u_xx+u_yy+f)^2 + boundary u^2, hipRTC) + weight gradient + RPROP'}
     return {
         'workload': name,
         'network': '→'.join(str(n) for n in wl.neurons) + ' sigmoid',
@@ -67,6 +93,14 @@ def describe(wl, name):
         'chunk': wl.chunk or wl.size,
         'step': 'forward + matching cost + weight gradient + RPROP',
     }
+
+
+def point_rows(wl):
+    return wl.point_rows() if isinstance(wl, workloads.PoissonWorkload) else wl.size * wl.rows
+
+
+def linear_macs(wl):
+    return point_rows(wl) * sum(a * b for a, b in zip(wl.neurons, wl.neurons[1:]))
 
 
 def traffic(workload, kind):
@@ -93,7 +127,7 @@ def roofline(report, workload):
             'work_per_launch': work / launches}
 
 
-def server_op90(wl, warm=20, iterations=100, batches=7):
+def server_op90(wl, warm, iterations, batches):
     """The reference's own timing scope through the protocol server (op 90:
     forward + cost + weight gradient, no optimizer; C++ host, no Python in the
     loop): median over batches of per-epoch wall and device milliseconds."""
@@ -106,43 +140,67 @@ def server_op90(wl, warm=20, iterations=100, batches=7):
     wall, gpu = float(np.median(r['wall_ms'])), float(np.median(r['gpu_ms']))
     return {'ms_per_epoch_wall': round(wall, 5), 'ms_per_epoch_device': round(gpu, 5),
             'points_derivs_per_s': round(wl.size * wl.rows / (wall / 1e3), 1),
-            'vs_published_5.65ms': round(5.65 / wall, 2) if wl.name.endswith('order6') and wl.size == 729 else None,
+            'vs_published_5.65ms': round(5.65 / wall, 2) if wl.name == 'fourier_fit_order6' else None,
             'loss': r['loss'], 'scope': f'op 90: {batches} batches x {iterations} epochs after {warm} warm-ups'}
 
 
+def cpu_sample(wl):
+    """A bounded sample of the workload for the CPU baseline: all of it when it
+    is small, else evenly spaced points; plus the number of epochs to run."""
+    if isinstance(wl, workloads.PoissonWorkload):
+        return wl, max(1, round(CPU_SAMPLE_MACS / linear_macs(wl)))
+    per_point = linear_macs(wl) / wl.size
+    points = min(wl.size, max(64, int(CPU_SAMPLE_MACS / per_point)))
+    sample = wl if points == wl.size else wl.subset(points)
+    return sample, max(1, round(CPU_SAMPLE_MACS / linear_macs(sample)))
+
+
+def upload_all(session, wl):
+    ids = wl.upload(session)
+    if isinstance(wl, workloads.PoissonWorkload):
+        return ids['net'], ids['costs'], wl.graph()
+    return ids['net'], [ids['cost']], None
+
+
 def cpu_baseline(wl):
-    """The CPU side of the same epoch, single thread, one full epoch of the
-    workload.  Preferred: the reference's own CPU server built from its sources
-    (oracle/_ref), driven over the wire protocol with one training epoch (op 8:
-    forward + cost + weight gradient + statistics + RPROP).  Otherwise the C
-    restatement of the same epoch."""
+    """The CPU side of the same epoch on one thread.  Preferred: the
+    reference's own CPU server built from its sources (oracle/_ref), driven over
+    the wire protocol with training epochs (op 8/15: forward + cost + weight
+    gradient + statistics + RPROP).  Otherwise the C restatement of the same
+    matching epoch."""
     sys.path.insert(0, str(ROOT / 'oracle'))
     import oracle
+    sample, epochs = cpu_sample(wl)
     ref = oracle.reference_server()
+    what = (f'{epochs} training epoch(s) of {sample.name} ({point_rows(sample)} point-rows'
+            f'{")" if sample is wl else f", a {sample.size}-point even subsample of the {wl.size}-point workload)"}')
     if ref is not None:
         from cpde_amd import wire
         with wire.Session(ref) as s:
-            ids = wl.upload(s)
+            net, costs, graph = upload_all(s, sample)
             t0 = time.perf_counter()
-            s.train(ids['net'], [ids['cost']], 1, method=0, fresh=1, log=0)
+            s.train(net, costs, epochs, method=0, fresh=1, log=0, graph=graph)
             seconds = time.perf_counter() - t0
-        return {'value': round(wl.size * wl.rows / seconds, 1), 'unit': 'points·derivs/s', 'cores': 1,
+        return {'value': round(point_rows(sample) * epochs / seconds, 1), 'unit': 'points·derivs/s', 'cores': 1,
                 'kind': 'reference', 'seconds': round(seconds, 3),
-                'sample': f'one training epoch ({wl.size} points x {wl.rows} rows, {wl.name}) of the reference CPU '
-                          'server (serial BLAS), op 8 train: fwd+cost+wgrad+stats+RPROP, single thread'}
-    x = wl.inputs.transpose(0, 2, 1)
+                'sample': f'{what} on the reference CPU server (serial BLAS): fwd+cost+wgrad+stats+RPROP, '
+                          'single thread'}
+    if isinstance(wl, workloads.PoissonWorkload):
+        return None
+    x = sample.inputs.transpose(0, 2, 1)
     t0 = time.perf_counter()
-    oracle.matching_epoch(wl.neurons, wl.linear, wl.init, wl.schema, x, wl.target[:, :, None],
-                          wl.row_weights[:, None, None], chunk=wl.chunk, outputs=False)
-    W = [np.array(w, np.float32) for w in wl.init]
-    for w in W:  # one RPROP pass over the parameters, as in the timed step
-        z = np.zeros_like(w)
-        oracle.rprop(w, np.full_like(w, 0.002), z, z)
+    for _ in range(epochs):
+        oracle.matching_epoch(sample.neurons, sample.linear, sample.init, sample.schema, x,
+                              sample.target[:, :, None], sample.row_weights[:, None, None], chunk=sample.chunk,
+                              outputs=False)
+        for w in sample.init:  # one RPROP pass over the parameters, as in the timed step
+            w = np.array(w, np.float32)
+            z = np.zeros_like(w)
+            oracle.rprop(w, np.full_like(w, 0.002), z, z)
     seconds = time.perf_counter() - t0
-    return {'value': round(wl.size * wl.rows / seconds, 1), 'unit': 'points·derivs/s', 'cores': 1,
+    return {'value': round(point_rows(sample) * epochs / seconds, 1), 'unit': 'points·derivs/s', 'cores': 1,
             'kind': 'port', 'seconds': round(seconds, 3),
-            'sample': f'one full epoch ({wl.size} points x {wl.rows} rows, {wl.name}) of the C restatement, '
-                      'fwd+cost+wgrad+RPROP, single thread'}
+            'sample': f'{what} of the C restatement: fwd+cost+wgrad+RPROP, single thread'}
 
 
 def copy_calibration(mib=256, repeats=5):
@@ -160,13 +218,69 @@ def copy_calibration(mib=256, repeats=5):
     return 0
 
 
+def run_direct(wl, steps, warmup, trace_steps):
+    """Matching epochs through the C ABI: returns (wall ms per step, device ms
+    per step, loss, device description, trace report)."""
+    device = hip.Device(0)
+    name, cus = device.info()
+    run = hip.MatchingRun(device, wl)
+
+    def step():
+        run.step(collect=True)
+        run.net.rprop()
+
+    for _ in range(warmup):
+        step()
+    device.synchronize()
+    device.mark(0)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    device.mark(1)
+    device.synchronize()
+    wall = time.perf_counter() - t0
+    device_ms = device.elapsed(0, 1)
+    loss = run.loss()
+    device.trace(True)
+    for _ in range(trace_steps):
+        step()
+    report = device.trace_report()
+    device.trace(False)
+    run.close()
+    device.close()
+    return wall * 1e3 / steps, device_ms / steps, loss, f'{name}, {cus} CUs', report
+
+
+def run_server(wl, steps, warmup, trace_steps):
+    """Graph training epochs through the protocol server (op 15): the server's
+    own loop, with the per-epoch scalar download and validation the protocol
+    requires.  A second session with CPDE_TRACE_FILE set gives the kernel report."""
+    from cpde_amd import wire
+    from cpde_amd.build import SERVER
+    with wire.Session(SERVER) as s:
+        net, costs, graph = upload_all(s, wl)
+        s.train(net, costs, warmup, method=0, fresh=1, log=0, graph=graph)
+        t0 = time.perf_counter()
+        s.train(net, costs, steps, method=0, fresh=0, log=0, graph=graph)
+        wall = time.perf_counter() - t0
+        value, _ = s.graph_eval(net, costs, graph, gradient=False)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / 'trace.json'
+        env = dict(os.environ, CPDE_TRACE_FILE=str(path))
+        with wire.Session(SERVER, env=env) as s:
+            net, costs, graph = upload_all(s, wl)
+            s.train(net, costs, trace_steps, method=0, fresh=1, log=0, graph=graph)
+        report = {k: tuple(v) for k, v in json.loads(path.read_text()).items()}
+    return wall * 1e3 / steps, None, value, 'device 0 (protocol server)', report
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=500)
-    ap.add_argument('--warmup', type=int, default=50)
+    ap.add_argument('--steps', type=int, default=None, help='timed epochs (default: per workload)')
+    ap.add_argument('--warmup', type=int, default=None)
     ap.add_argument('--workload', default='fourier_fit_order6', choices=sorted(WORKLOADS))
-    ap.add_argument('--trace-steps', type=int, default=20)
+    ap.add_argument('--trace-steps', type=int, default=None)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-op90', action='store_true', help='skip the protocol-server timing (op 90)')
     ap.add_argument('--copy-calibration', action='store_true',
@@ -178,69 +292,47 @@ def main(argv=None):
         print('bench.py measures one GPU only: the cPDE hot path runs on a single device '
               '(multi-GPU point sharding is a design, not a build, here); run with --gpus 1', file=sys.stderr)
         return 2
+    spec = WORKLOADS[args.workload]
+    steps = args.steps if args.steps is not None else spec.steps
+    warmup = args.warmup if args.warmup is not None else spec.warmup
+    trace_steps = args.trace_steps if args.trace_steps is not None else spec.trace_steps
 
-    wl = WORKLOADS[args.workload]()
+    wl = spec.make()
     # The protocol server runs as a child process, started before this process
     # touches the device.
-    op90 = None if args.no_op90 else server_op90(wl)
-    device = hip.Device(0)
-    name, cus = device.info()
-    run = hip.MatchingRun(device, wl)
+    op90 = None if args.no_op90 or spec.op90 is None else server_op90(wl, *spec.op90)
+    runner = run_server if spec.server else run_direct
+    ms, device_ms, loss, device, report = runner(wl, steps, warmup, trace_steps)
 
-    def step():
-        run.step(collect=True)
-        run.net.rprop()
-
-    for _ in range(args.warmup):
-        step()
-    device.synchronize()
-    device.mark(0)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    device.mark(1)
-    device.synchronize()
-    wall = time.perf_counter() - t0
-    device_ms = device.elapsed(0, 1)
-    loss = run.loss()
-
-    device.trace(True)
-    for _ in range(args.trace_steps):
-        step()
-    report = device.trace_report()
-    device.trace(False)
-
-    ms = wall * 1e3 / args.steps
-    value = wl.size * wl.rows / (ms / 1e3)
+    value = point_rows(wl) / (ms / 1e3)
     t_roof = wl.flops_per_epoch() / PEAK_FP32_MFMA + wl.bytes_per_epoch() / PEAK_HBM
     out = {
         'metric': METRIC,
         'value': round(value, 1),
         'unit': 'points·derivs/s',
         'n_gpus': 1,
-        'steps': args.steps,
-        'warmup': args.warmup,
+        'steps': steps,
+        'warmup': warmup,
         'ms_per_step': round(ms, 5),
         'higher_is_better': True,
         'scaling': 'weak',
         'vs_baseline': round(value / PUBLISHED_POINTS_DERIVS_PER_S, 3) if args.workload == 'fourier_fit_order6'
         else None,
         'dtype': 'f32',
-        'data': 'synthetic (seeded Fourier-sum targets with analytic derivatives, Xavier-uniform weights)',
+        'data': 'synthetic (seeded Fourier-sum targets with analytic derivatives / seeded Gaussian sources, '
+                'Xavier-uniform weights)',
         'config': describe(wl, args.workload),
-        'device': f'{name}, {cus} CUs',
-        'device_ms_per_step': round(device_ms / args.steps, 5),
+        'device': device,
+        'device_ms_per_step': None if device_ms is None else round(device_ms, 5),
         'epoch_roofline': {'t_roof_us': round(t_roof * 1e6, 2), 'frac': round(t_roof / (ms / 1e3), 4),
                            'gflop': wl.flops_per_epoch() / 1e9, 'gbytes': wl.bytes_per_epoch() / 1e9},
         'loss_after_timed_steps': loss,
         'roofline': roofline(report, args.workload),
-        'kernels': {k: {'launches_per_step': v[0] / args.trace_steps, 'us_per_step': round(v[1] * 1e3 /
-                        args.trace_steps, 3)} for k, v in sorted(report.items(), key=lambda kv: -kv[1][1])},
+        'kernels': {k: {'launches_per_step': v[0] / trace_steps, 'us_per_step': round(v[1] * 1e3 / trace_steps, 3)}
+                    for k, v in sorted(report.items(), key=lambda kv: -kv[1][1])},
+        'op90': op90,
         'cpu_baseline': None,
     }
-    run.close()
-    device.close()
-    out['op90'] = op90
     if not args.no_cpu_baseline:
         out['cpu_baseline'] = cpu_baseline(wl)
     print(json.dumps(out), flush=True)

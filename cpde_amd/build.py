@@ -86,7 +86,8 @@ def warm_jit():
                            (W.full_schema(2, 2), [2, 128, 128, 128, 128, 1]),
                            (W.full_schema(3, 4), [3, 128, 128, 128, 128, 128, 1]),
                            (W.full_schema(2, 6), [2, 256, 256, 256, 256, 1]),
-                           (W.closed_schema(2, [(2, 0), (0, 2)]), [2, 64, 64, 64, 1])]:
+                           (W.closed_schema(2, [(2, 0), (0, 2)]), [2, 64, 64, 64, 1]),
+                           (W.closed_schema(2, []), [2, 64, 64, 64, 1])]:
         hip.jit_prepare(table, neurons, ARCH)
 
 

@@ -185,10 +185,13 @@ struct NetArgsHost {
     float* partial_out;
 };
 
-static FusedTuning tuning() {
+// Tuning of the fused kernels for a schema of `rows` derivative rows.  The
+// network-fused kernels put as many points in a workgroup as fill one 32-column
+// matrix-core tile (one point when the rows alone need a tile or more).
+static FusedTuning tuning(int rows) {
     FusedTuning t;
     t.points_per_block = std::max(1, env_int("CPDE_FUSED_POINTS", t.points_per_block));
-    t.net_points_per_block = std::max(1, env_int("CPDE_NET_POINTS", t.net_points_per_block));
+    t.net_points_per_block = std::max(1, env_int("CPDE_NET_POINTS", rows <= 16 ? 32 / rows : 1));
     t.max_split = std::max(1, env_int("CPDE_NET_SPLIT", t.max_split));
     t.max_split_adjoint = std::max(1, env_int("CPDE_NET_SPLIT_ADJOINT", t.max_split_adjoint));
     t.forward_blocks = std::max(1, env_int("CPDE_NET_FWD_OCC", t.forward_blocks));
@@ -197,7 +200,7 @@ static FusedTuning tuning() {
 }
 
 static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const std::vector<int>& neurons) {
-    const FusedTuning tune = tuning();
+    const FusedTuning tune = tuning(t.rows);
     const std::string src = fused_source(t, neurons, tune);
     for (auto& kv : d.fused_modules)
         if (kv.first == src) return kv.second;
@@ -922,7 +925,7 @@ int cpde_jit_prepare(int rows, int variables, const int* table, int layers, cons
         const Tables t = build_tables(rows, variables, table);
         std::string text;
         try {
-            compile_module(fused_source(t, std::vector<int>(neurons, neurons + layers), tuning()), arch, &text);
+            compile_module(fused_source(t, std::vector<int>(neurons, neurons + layers), tuning(t.rows)), arch, &text);
         } catch (...) {
             if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
             throw;

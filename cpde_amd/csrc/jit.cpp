@@ -360,11 +360,9 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
       << ") void network_backward_k(NetArgs a, int points) {\n"
          "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
          "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n"
-         "    static_assert(kNPB * " << neurons[L - 1] + 1 << " * " << neurons[L - 2]
-      << " <= kNNC * kS, \"output-gradient scratch exceeds the LDS tile\");\n"
          "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
          "    net_output_backward<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2
-      << ", X, T, p0, npts);\n";
+      << ", X, p0, npts);\n";
     for (int t = L - 3; t >= 1; --t)
         o << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t
           << ", X, T, p0, npts);\n";

@@ -523,6 +523,7 @@ public:
     // handshake and request validation work on a machine without a GPU.
     explicit Server(int ordinal) : ordinal_(ordinal) {}
     ~Server() {
+        if (dev_ && !trace_file_.empty()) write_trace();
         costs_.clear();
         nets_.clear();
         data_.clear();
@@ -536,8 +537,32 @@ private:
     int ordinal_ = 0;
     cpde_device* dev_ = nullptr;
     uint64_t next_id_ = 1;
+    // With CPDE_TRACE_FILE set, every launch of the session is timed per kernel
+    // class and the totals are written there as JSON when the server ends.
+    std::string trace_file_;
     void open_device() {
-        if (!dev_) call(cpde_device_open(ordinal_, &dev_));
+        if (dev_) return;
+        call(cpde_device_open(ordinal_, &dev_));
+        if (const char* path = std::getenv("CPDE_TRACE_FILE")) {
+            trace_file_ = path;
+            call(cpde_trace_enable(dev_, 1));
+        }
+    }
+    void write_trace() {
+        std::FILE* f = std::fopen(trace_file_.c_str(), "w");
+        if (!f) return;
+        std::fprintf(f, "{");
+        bool first = true;
+        for (int k = 0; k < cpde_trace_kinds(); ++k) {
+            uint64_t launches = 0;
+            double ms = 0, work = 0;
+            if (cpde_trace_read(dev_, k, &launches, &ms, &work) != CPDE_OK || launches == 0) continue;
+            std::fprintf(f, "%s\"%s\": [%llu, %.9g, %.17g]", first ? "" : ", ", cpde_trace_name(k),
+                         (unsigned long long)launches, ms, work);
+            first = false;
+        }
+        std::fprintf(f, "}\n");
+        std::fclose(f);
     }
     std::unordered_map<uint64_t, std::unique_ptr<DataRecord>> data_;
     std::unordered_map<uint64_t, std::unique_ptr<NetRecord>> nets_;

@@ -151,6 +151,13 @@ class MatchingWorkload:
         params = sum(b * (a + 1) for a, b in zip(self.neurons, self.neurons[1:]))
         return 4 * rp * (5 * hidden + 3 * self.neurons[-1]) + 28 * params
 
+    def subset(self, count):
+        """The same workload on `count` evenly spaced points (same network,
+        weights, row weights and targets), unchunked."""
+        idx = np.linspace(0, self.size - 1, count).astype(int)
+        return MatchingWorkload(f'{self.name}[{count} points]', self.neurons, self.points[idx], self.schema,
+                                self.target[:, idx], self.row_weights, self.init)
+
     def upload(self, session, chunk=None):
         """Creates data, target, network and cost objects; returns their ids."""
         d = session.data(self.inputs, self.schema)
@@ -268,6 +275,31 @@ class PoissonWorkload:
         self.f = gaussian_source(self.interior)
         self.schema = closed_schema(2, [(2, 0), (0, 2)])   # rows: 1, y, x, yy, xx
         self.init = xavier_weights(neurons, seed)
+
+    name = 'poisson_disk_order2'
+
+    def leaves(self):
+        """(rows, points) of the interior and boundary costs."""
+        return [(len(self.schema), len(self.interior)), (1, len(self.boundary))]
+
+    @property
+    def size(self):
+        return len(self.interior) + len(self.boundary)
+
+    def point_rows(self):
+        return sum(r * p for r, p in self.leaves())
+
+    def flops_per_epoch(self):
+        """Forward + transposed (not the input layer) + weight-gradient flops of
+        one forward and one backward per leaf (the graph's multipliers are known)."""
+        pairs = list(zip(self.neurons, self.neurons[1:]))
+        fwd = sum(a * b for a, b in pairs)
+        return 2 * self.point_rows() * (2 * fwd + sum(a * b for a, b in pairs[1:]))
+
+    def bytes_per_epoch(self):
+        hidden = sum(self.neurons[1:-1])
+        params = sum(b * (a + 1) for a, b in zip(self.neurons, self.neurons[1:]))
+        return 4 * self.point_rows() * (5 * hidden + 3 * self.neurons[-1]) + 28 * params
 
     def row_of(self, counts):
         for r, row in enumerate(self.schema):
