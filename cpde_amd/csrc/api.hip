@@ -183,6 +183,7 @@ struct NetArgsHost {
     const float* X;
     float* partial_in;
     float* partial_out;
+    float* WT[32];
 };
 
 // Tuning of the fused kernels for a schema of `rows` derivative rows.  The
@@ -232,7 +233,10 @@ static void launch_module(Device& d, hipFunction_t f, unsigned gx, unsigned gy, 
 
 static NetArgsHost net_args(Net& n) {
     NetArgsHost a{};
-    for (int t = 0; t + 1 < n.layers; ++t) a.W[t] = n.state[0][t];
+    for (int t = 0; t + 1 < n.layers; ++t) {
+        a.W[t] = n.state[0][t];
+        a.WT[t] = n.wt[t];
+    }
     for (int l = 0; l < n.layers; ++l) {
         a.Z[l] = n.z[l];
         a.Y[l] = n.y[l];
@@ -536,6 +540,7 @@ int cpde_net_create(cpde_device* dev, int layers, const int* neurons, const int*
         n->linear.assign(linear, linear + layers);
         const int T = layers - 1;
         for (auto& s : n->state) s.assign(T, nullptr);
+        n->wt.assign(T, nullptr);
         n->active.assign(T, 1);
         n->z.assign(layers, nullptr);
         n->y.assign(layers, nullptr);
@@ -544,6 +549,7 @@ int cpde_net_create(cpde_device* dev, int layers, const int* neurons, const int*
         for (int t = 0; t < T; ++t) {
             const size_t count = n->param_count(t);
             for (int b = 0; b < 4; ++b) HIP_CHECK(hipMalloc(&n->state[b][t], count * sizeof(float)));
+            HIP_CHECK(hipMalloc(&n->wt[t], size_t(n->neurons[t]) * n->neurons[t + 1] * sizeof(float)));
             if (initial && initial[t])
                 HIP_CHECK(hipMemcpyAsync(n->state[0][t], initial[t], count * sizeof(float), hipMemcpyHostToDevice,
                                          dev->stream));
@@ -565,6 +571,7 @@ int cpde_net_destroy(cpde_net* net) {
         (void)hipStreamSynchronize(net->dev->stream);
         for (auto& s : net->state)
             for (float* p : s) (void)hipFree(p);
+        for (float* p : net->wt) (void)hipFree(p);
         for (auto* v : {&net->z, &net->y, &net->g})
             for (float* p : *v) (void)hipFree(p);
         (void)hipFree(net->partials);

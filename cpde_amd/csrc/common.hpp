@@ -75,6 +75,9 @@ struct Net {
     // Per transition t: four state buffers of n_{t+1} x (n_t+1) floats.
     std::vector<float*> state[4];
     std::vector<int> active;  // 1 or 2 per transition
+    // Per transition: n_t x n_{t+1} row-major copy of the weights (without the
+    // bias), refreshed by every network-fused forward for the backward's products.
+    std::vector<float*> wt;
     // Stack arena shared by every plan of the network (contexts are views,
     // the reference's layer banks, cuda/cpde_engine.cuh:661-693).
     std::vector<float*> z, y, g;      // per layer

@@ -349,8 +349,10 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     o << "\nextern \"C\" __global__ __launch_bounds__(256, " << tuning.forward_blocks << ") void network_forward_k(NetArgs a, int points) {\n"
          "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
          "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n"
-         "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
-         "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
+         "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n";
+    for (int t = 1; t + 2 < L; ++t)
+        o << "    net_transpose<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ");\n";
+    o << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
          "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
          "    __syncthreads();\n";
     for (int t = 1; t + 2 < L; ++t)
