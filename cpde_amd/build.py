@@ -82,13 +82,13 @@ def warm_jit():
     if cache.exists():
         shutil.rmtree(cache)
     hip.load(LIB)
-    for table, neurons in [(W.full_schema(2, 6), [2, 128, 128, 128, 128, 1]),
-                           (W.full_schema(2, 2), [2, 128, 128, 128, 128, 1]),
-                           (W.full_schema(3, 4), [3, 128, 128, 128, 128, 128, 1]),
-                           (W.full_schema(2, 6), [2, 256, 256, 256, 256, 1]),
-                           (W.closed_schema(2, [(2, 0), (0, 2)]), [2, 64, 64, 64, 1]),
-                           (W.closed_schema(2, []), [2, 64, 64, 64, 1])]:
-        hip.jit_prepare(table, neurons, ARCH)
+    for table, neurons, width in [(W.full_schema(2, 6), [2, 128, 128, 128, 128, 1], 729),
+                                  (W.full_schema(2, 2), [2, 128, 128, 128, 128, 1], 729),
+                                  (W.full_schema(3, 4), [3, 128, 128, 128, 128, 128, 1], 32768),
+                                  (W.full_schema(2, 6), [2, 256, 256, 256, 256, 1], 65536),
+                                  (W.closed_schema(2, [(2, 0), (0, 2)]), [2, 64, 64, 64, 1], 4096),
+                                  (W.closed_schema(2, []), [2, 64, 64, 64, 1], 256)]:
+        hip.jit_prepare(table, neurons, width, 256, ARCH)
 
 
 def main(argv):

@@ -186,13 +186,20 @@ struct NetArgsHost {
     float* WT[32];
 };
 
-// Tuning of the fused kernels for a schema of `rows` derivative rows.  The
-// network-fused kernels put as many points in a workgroup as fill one 32-column
-// matrix-core tile (one point when the rows alone need a tile or more).
-static FusedTuning tuning(int rows) {
+// Tuning of the fused kernels for a schema of `rows` derivative rows over chunks
+// of `width` points (0: unknown) on `compute_units` CUs.  The network-fused
+// kernels put as many points in a workgroup as fill one 32-column matrix-core
+// tile (one point when the rows alone need a tile or more), but no more than
+// spread the chunk over about one workgroup per CU.
+static FusedTuning tuning(int rows, int width, int compute_units) {
     FusedTuning t;
+    int npb = rows <= 16 ? 32 / rows : 1;
+    if (width > 0) {
+        const int spread = std::max(1, env_int("CPDE_NET_MIN_BLOCKS", compute_units));
+        npb = std::max(1, std::min(npb, (width + spread - 1) / spread));
+    }
     t.points_per_block = std::max(1, env_int("CPDE_FUSED_POINTS", t.points_per_block));
-    t.net_points_per_block = std::max(1, env_int("CPDE_NET_POINTS", rows <= 16 ? 32 / rows : 1));
+    t.net_points_per_block = std::max(1, env_int("CPDE_NET_POINTS", npb));
     t.max_split = std::max(1, env_int("CPDE_NET_SPLIT", t.max_split));
     t.max_split_adjoint = std::max(1, env_int("CPDE_NET_SPLIT_ADJOINT", t.max_split_adjoint));
     t.forward_blocks = std::max(1, env_int("CPDE_NET_FWD_OCC", t.forward_blocks));
@@ -200,8 +207,9 @@ static FusedTuning tuning(int rows) {
     return t;
 }
 
-static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const std::vector<int>& neurons) {
-    const FusedTuning tune = tuning(t.rows);
+static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const std::vector<int>& neurons,
+                                               int width) {
+    const FusedTuning tune = tuning(t.rows, width, d.compute_units);
     const std::string src = fused_source(t, neurons, tune);
     for (auto& kv : d.fused_modules)
         if (kv.first == src) return kv.second;
@@ -303,6 +311,10 @@ struct GradientPlan {
     size_t total = 0;
 };
 
+// Weight-gradient tiles per compute unit the split-K decomposition aims for
+// (CPDE_WGRAD_OCC; two keep a second wave on every SIMD to cover stalls).
+static double wgrad_blocks_per_cu() { return std::max(1, env_int("CPDE_WGRAD_OCC", 1)); }
+
 static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<int>& external_splits) {
     Net& n = *p.net;
     Device& d = *n.dev;
@@ -310,9 +322,14 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
     GradientPlan g;
     g.offset.assign(T, 0);
     auto thin = [&](int t) { return n.neurons[t + 1] <= 16 || n.neurons[t] <= 16; };
+    auto tile_of = [&](int t) { return n.neurons[t + 1] <= 64 && n.neurons[t] <= 64 ? 64 : 128; };
+    auto tiles_of = [&](int t) {
+        const int T0 = tile_of(t);
+        return ((n.neurons[t + 1] + T0 - 1) / T0) * ((n.neurons[t] + T0 - 1) / T0);
+    };
     double total_tiles = 0;
     for (int t = 0; t < T; ++t)
-        if (!thin(t) && !external_splits[t]) total_tiles += ((n.neurons[t + 1] + 127) / 128) * ((n.neurons[t] + 127) / 128);
+        if (!thin(t) && !external_splits[t]) total_tiles += tiles_of(t);
     g.wa.K = K;
     g.wa.R = p.rows;
     g.wa.block_begin[0] = 0;
@@ -325,8 +342,8 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
         const int M = n.neurons[t + 1], N = n.neurons[t];
         int s = external_splits[t];
         if (!s) {
-            const int tiles = thin(t) ? 1 : ((M + 127) / 128) * ((N + 127) / 128);
-            s = thin(t) ? 2 * d.compute_units : int(double(d.compute_units) / total_tiles + 0.5);
+            const int tiles = thin(t) ? 1 : tiles_of(t);
+            s = thin(t) ? 2 * d.compute_units : int(wgrad_blocks_per_cu() * d.compute_units / total_tiles + 0.5);
             s = std::max(1, std::min(s, std::max(1, K / 64)));
             int chunk = (K + s - 1) / s;
             chunk = (chunk + 31) / 32 * 32;
@@ -334,6 +351,7 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
             g.wa.M[w] = M;
             g.wa.N[w] = N;
             g.wa.kchunk[w] = chunk;
+            g.wa.tile[w] = tile_of(t);
             g.wa.block_begin[w + 1] = g.wa.block_begin[w] + tiles * s;
             g.wa.G[w] = n.g[t + 1];
             g.wa.Y[w] = n.linear[t] ? n.z[t] : n.y[t];
@@ -449,6 +467,7 @@ int cpde_device_open(int ordinal, cpde_device** out) {
         for (auto& e : d->marks) HIP_CHECK(hipEventCreate(&e));
         d->reserve_costs(8);
         d->reserve_grads(8);
+        HIP_CHECK(hipHostMalloc(&d->host_summary, sizeof(cpde_graph_summary), hipHostMallocDefault));
         *out = d.release();
     });
 }
@@ -465,6 +484,7 @@ int cpde_device_close(cpde_device* dev) {
         (void)hipFree(dev->grad_totals);
         (void)hipHostFree(dev->host_costs);
         (void)hipHostFree(dev->host_grads);
+        (void)hipHostFree(dev->host_summary);
         (void)hipStreamDestroy(dev->stream);
         delete dev;
     });
@@ -625,7 +645,7 @@ int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, i
                                  net->dev->stream));
         reserve_arena(*net, *p);
         if (fused_eligible(*net, *p)) {
-            p->fused = load_fused(*net->dev, p->tables, net->neurons);
+            p->fused = load_fused(*net->dev, p->tables, net->neurons, width);
             p->network = network_mode();
         }
         HIP_CHECK(hipStreamSynchronize(net->dev->stream));
@@ -759,25 +779,45 @@ int cpde_backward(cpde_plan* plan, int accumulate) {
 int cpde_inspect_gradients(cpde_net* net) {
     return guarded([&] {
         Device& d = *net->dev;
-        d.reserve_grads(net->layers - 1);
-        for (int t = 0; t + 1 < net->layers; ++t)
-            launch_grad_stats(d, net->state[net->active[t]][t], net->param_count(t), t);
+        const int T = net->layers - 1;
+        d.reserve_grads(T);
+        for (int first = 0; first < T; first += kMaxTransitions) {
+            const int n = std::min(kMaxTransitions, T - first);
+            const float* g[kMaxTransitions];
+            int counts[kMaxTransitions];
+            for (int k = 0; k < n; ++k) {
+                g[k] = net->state[net->active[first + k]][first + k];
+                counts[k] = net->param_count(first + k);
+            }
+            launch_grad_stats(d, g, counts, n, first);
+        }
     });
 }
 
 int cpde_scalars_download(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
                           cpde_gradient_stats* gradient_out) {
+    return cpde_scalars_download_graph(dev, costs, cost_out, layers, gradient_out, nullptr, nullptr);
+}
+
+int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
+                                cpde_gradient_stats* gradient_out, const cpde_graph_summary* summary,
+                                cpde_graph_summary* summary_out) {
     return guarded([&] {
         require(costs <= dev->cost_capacity && layers <= dev->grad_capacity, "scalar slots out of range");
+        require((summary == nullptr) == (summary_out == nullptr), "graph summary source and destination go together");
         if (costs)
             HIP_CHECK(hipMemcpyAsync(dev->host_costs, dev->cost_totals, sizeof(CostStats) * costs,
                                      hipMemcpyDeviceToHost, dev->stream));
         if (layers)
             HIP_CHECK(hipMemcpyAsync(dev->host_grads, dev->grad_totals, sizeof(GradStats) * layers,
                                      hipMemcpyDeviceToHost, dev->stream));
+        if (summary)
+            HIP_CHECK(hipMemcpyAsync(dev->host_summary, summary, sizeof(cpde_graph_summary), hipMemcpyDeviceToHost,
+                                     dev->stream));
         HIP_CHECK(hipStreamSynchronize(dev->stream));
         if (costs && cost_out) std::memcpy(cost_out, dev->host_costs, sizeof(CostStats) * costs);
         if (layers && gradient_out) std::memcpy(gradient_out, dev->host_grads, sizeof(GradStats) * layers);
+        if (summary) *summary_out = *dev->host_summary;
     });
 }
 
@@ -802,8 +842,13 @@ int cpde_restore_steps(cpde_net* net, float floor_value) {
 
 int cpde_zero_gradient(cpde_net* net) {
     return guarded([&] {
-        for (int t = 0; t + 1 < net->layers; ++t)
-            launch_fill(*net->dev, net->state[net->active[t]][t], net->param_count(t), 0.0f);
+        std::vector<float*> p;
+        std::vector<int> counts;
+        for (int t = 0; t + 1 < net->layers; ++t) {
+            p.push_back(net->state[net->active[t]][t]);
+            counts.push_back(net->param_count(t));
+        }
+        launch_fill_grouped(*net->dev, p.data(), counts.data(), int(p.size()), 0.0f);
     });
 }
 
@@ -925,14 +970,16 @@ const char* cpde_trace_name(int kind) {
 
 int cpde_trace_kinds(void) { return kTraceKinds; }
 
-int cpde_jit_prepare(int rows, int variables, const int* table, int layers, const int* neurons, const char* arch,
-                     char* log, size_t log_capacity) {
+int cpde_jit_prepare(int rows, int variables, const int* table, int layers, const int* neurons, int width,
+                     int compute_units, const char* arch, char* log, size_t log_capacity) {
     return guarded([&] {
         require(table && neurons && arch && layers >= 3, "invalid argument");
         const Tables t = build_tables(rows, variables, table);
         std::string text;
         try {
-            compile_module(fused_source(t, std::vector<int>(neurons, neurons + layers), tuning(t.rows)), arch, &text);
+            compile_module(fused_source(t, std::vector<int>(neurons, neurons + layers),
+                                        tuning(t.rows, width, compute_units)),
+                           arch, &text);
         } catch (...) {
             if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
             throw;

@@ -134,6 +134,7 @@ struct Device {
     GradStats* grad_totals = nullptr;   // grad_capacity
     CostStats* host_costs = nullptr;
     GradStats* host_grads = nullptr;
+    cpde_graph_summary* host_summary = nullptr;  // pinned: one graph summary
     int cost_capacity = 0, grad_capacity = 0;
     hipEvent_t marks[8] = {};
     // tracing
@@ -155,6 +156,7 @@ struct WgradArgs {
     const float* Y[kMaxTransitions];
     float* partial[kMaxTransitions];
     int M[kMaxTransitions], N[kMaxTransitions], kchunk[kMaxTransitions];
+    int tile[kMaxTransitions];  // 128, or 64 when both sides are at most 64
     int block_begin[kMaxTransitions + 1];
     int transitions, K, R;
 };
@@ -220,7 +222,9 @@ void launch_polynomial(Device& d, const Plan& p, const float* y, float* g, const
 void launch_sample_reduce(Device& d, const double* values, const int* bad, int valid, int offset, int cost_index);
 void launch_scale_adjoint(Device& d, const Plan& p, float* g, const double* multiplier);
 void launch_costs_begin(Device& d, int costs);
-void launch_grad_stats(Device& d, const float* g, int count, int slot);
+// Statistics of `transitions` (<= kMaxTransitions) gradients into slots first_slot...
+void launch_grad_stats(Device& d, const float* const* g, const int* counts, int transitions, int first_slot);
+void launch_fill_grouped(Device& d, float* const* p, const int* counts, int buffers, float value);
 void launch_fill(Device& d, float* p, size_t count, float value);
 void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, int NI, int NO, int R, int columns);
 void launch_wgrad_grouped(Device& d, const WgradArgs& a, double flops);

@@ -309,30 +309,36 @@ void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, 
 // split's partial row-major [m][N+1] (entry N: the bias gradient, the sum over
 // value-row columns), reduced in split order by reduce_grouped_kernel so the
 // result does not depend on scheduling.  Two block roles:
-//  * matrix-core tiles (M, N > 16): a 64x64 tile, K staged through LDS in
-//    chunks of 16 columns (double-buffered, the next chunk's global loads in
-//    flight during the current chunk's MFMAs); wave = 32x32 sub-tile;
+//  * matrix-core tiles (M, N > 16): a 128x128 (or 64x64) tile, K staged
+//    through LDS in chunks of 32 columns (double-buffered, the next chunk's
+//    global loads in flight during the current chunk's MFMAs);
 //  * thin transitions (M or N <= 16: the input and output layers): lanes
 //    stride the wide side and accumulate the narrow side in registers.
-constexpr int kWgKC = 32;        // columns per LDS chunk
-constexpr int kWgLd = 128 + 4;   // LDS row stride of a chunk
-constexpr int kWgTile = 128;     // block tile (M x N)
+constexpr int kWgKC = 32;                          // columns per LDS chunk
+constexpr int kWgLds = 2 * 2 * kWgKC * (128 + 4);  // floats of LDS shared by the block roles
 
-// Matrix-core tile of one split: 128x128 of dW, wave = 64x64 quadrant made of
-// 2x2 MFMA 32x32 blocks (per k-step: 2 A + 2 B operands feed 4 MFMAs).
-__device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local) {
-    __shared__ __attribute__((aligned(16))) float As[2][kWgKC][kWgLd];
-    __shared__ __attribute__((aligned(16))) float Bs[2][kWgKC][kWgLd];
+// Matrix-core tile of one split: TILE x TILE of dW (TILE = 128, or 64 for
+// transitions no wider than 64), wave = quadrant of (TILE/64)^2 MFMA 32x32
+// blocks (per k-step: TILE/64 A + TILE/64 B operands feed (TILE/64)^2 MFMAs).
+template <int TILE>
+__device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local, float* lds) {
+    constexpr int LD = TILE + 4;    // LDS row stride of a chunk
+    constexpr int WX = TILE / 64;   // MFMA blocks per wave and dimension
+    constexpr int RP = 1024 / TILE; // staged rows per pass (256 threads x float4)
+    constexpr int J = kWgKC / RP;   // passes per chunk
+    typedef float Chunk[kWgKC][LD];
+    Chunk* As = reinterpret_cast<Chunk*>(lds);
+    Chunk* Bs = reinterpret_cast<Chunk*>(lds + 2 * kWgKC * LD);
     const int M = a.M[t], N = a.N[t], K = a.K;
-    const int tiles_m = (M + kWgTile - 1) / kWgTile, tiles_n = (N + kWgTile - 1) / kWgTile;
+    const int tiles_m = (M + TILE - 1) / TILE, tiles_n = (N + TILE - 1) / TILE;
     const int tile = local % (tiles_m * tiles_n), split = local / (tiles_m * tiles_n);
-    const int m0 = (tile % tiles_m) * kWgTile, n0 = (tile / tiles_m) * kWgTile;
+    const int m0 = (tile % tiles_m) * TILE, n0 = (tile / tiles_m) * TILE;
     const int kbegin = split * a.kchunk[t], kend = min(K, kbegin + a.kchunk[t]);
     const float* __restrict__ G = a.G[t];
     const float* __restrict__ Y = a.Y[t];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
-    // staging: thread -> 4 consecutive columns at 4*(tid%32) of rows tid/32 + 8j (j < 4)
-    const int sc = 4 * (tid & 31), sr = tid >> 5;
+    // staging: thread -> 4 consecutive columns at 4*(tid % (TILE/4)) of rows tid/(TILE/4) + RP*j
+    const int sc = 4 * (tid % (TILE / 4)), sr = tid / (TILE / 4);
     const bool vecm = (M % 4) == 0, vecn = (N % 4) == 0;
     auto load = [&](const float* src, int ld, int c0, int cmax, bool vec, int k) -> float4 {
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -348,47 +354,52 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local)
         }
         return v;
     };
-    floatx16 acc[2][2];
+    floatx16 acc[WX][WX];
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+    for (int x = 0; x < WX; ++x)
 #pragma unroll
-        for (int y = 0; y < 2; ++y)
+        for (int y = 0; y < WX; ++y)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[x][y][v] = 0.0f;
-    float bias = 0.0f;  // tile column 0 blocks: thread tid < 128 sums G[k][m0+tid] over value rows
-    const int wm = 64 * (wave & 1), wn = 64 * (wave >> 1);
-    float4 ga[4], ya[4];
+    float bias = 0.0f;  // tile column 0 blocks: thread tid < TILE sums G[k][m0+tid] over value rows
+    const int wm = (TILE / 2) * (wave & 1), wn = (TILE / 2) * (wave >> 1);
+    float4 ga[J], ya[J];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        ga[j] = load(G, M, m0, M, vecm, kbegin + sr + 8 * j);
-        ya[j] = load(Y, N, n0, N, vecn, kbegin + sr + 8 * j);
+    for (int j = 0; j < J; ++j) {
+        ga[j] = load(G, M, m0, M, vecm, kbegin + sr + RP * j);
+        ya[j] = load(Y, N, n0, N, vecn, kbegin + sr + RP * j);
     }
     int buf = 0;
     for (int k0 = kbegin; k0 < kend; k0 += kWgKC) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            *reinterpret_cast<float4*>(&As[buf][sr + 8 * j][sc]) = ga[j];
-            *reinterpret_cast<float4*>(&Bs[buf][sr + 8 * j][sc]) = ya[j];
+        for (int j = 0; j < J; ++j) {
+            *reinterpret_cast<float4*>(&As[buf][sr + RP * j][sc]) = ga[j];
+            *reinterpret_cast<float4*>(&Bs[buf][sr + RP * j][sc]) = ya[j];
         }
         __syncthreads();
         if (k0 + kWgKC < kend) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                ga[j] = load(G, M, m0, M, vecm, k0 + kWgKC + sr + 8 * j);
-                ya[j] = load(Y, N, n0, N, vecn, k0 + kWgKC + sr + 8 * j);
+            for (int j = 0; j < J; ++j) {
+                ga[j] = load(G, M, m0, M, vecm, k0 + kWgKC + sr + RP * j);
+                ya[j] = load(Y, N, n0, N, vecn, k0 + kWgKC + sr + RP * j);
             }
         }
         __builtin_amdgcn_iglp_opt(0);  // interleave the LDS operand reads with the MFMAs
 #pragma unroll
         for (int kk = 0; kk < kWgKC; kk += 2) {
-            const float a0 = As[buf][kk + h][wm + i], a1 = As[buf][kk + h][wm + 32 + i];
-            const float b0 = Bs[buf][kk + h][wn + i], b1 = Bs[buf][kk + h][wn + 32 + i];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+            float av[WX], bv[WX];
+#pragma unroll
+            for (int x = 0; x < WX; ++x) {
+                av[x] = As[buf][kk + h][wm + 32 * x + i];
+                bv[x] = Bs[buf][kk + h][wn + 32 * x + i];
+            }
+#pragma unroll
+            for (int x = 0; x < WX; ++x)
+#pragma unroll
+                for (int y = 0; y < WX; ++y)
+                    acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[x], bv[y], acc[x][y], 0, 0, 0);
         }
-        if (n0 == 0 && tid < kWgTile) {
+        if (n0 == 0 && tid < TILE) {
             const int first = (k0 + a.R - 1) / a.R * a.R;
             for (int c = first; c < min(kend, k0 + kWgKC); c += a.R) bias += As[buf][c - k0][tid];
         }
@@ -396,22 +407,18 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local)
     }
     float* P = a.partial[t] + size_t(split) * M * (N + 1);
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+    for (int x = 0; x < WX; ++x)
 #pragma unroll
-        for (int y = 0; y < 2; ++y)
+        for (int y = 0; y < WX; ++y)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int mrow = m0 + wm + 32 * x + 8 * (v >> 2) + 4 * h + (v & 3), ncol = n0 + wn + 32 * y + i;
                 if (mrow < M && ncol < N) P[size_t(mrow) * (N + 1) + ncol] = acc[x][y][v];
             }
-    if (n0 == 0 && tid < kWgTile && m0 + tid < M) P[size_t(m0 + tid) * (N + 1) + N] = bias;
+    if (n0 == 0 && tid < TILE && m0 + tid < M) P[size_t(m0 + tid) * (N + 1) + N] = bias;
 }
 
-// Thin transitions: lanes over the wide side (blocks of up to 256), the block
-// split into S = 256/width streams over the split's columns (4 columns in
-// flight per stream), stream partials combined in stream order.
-__device__ __forceinline__ void wgrad_thin(const WgradArgs& a, int t, int split) {
-    __shared__ float red[256 * 17];
+__device__ __forceinline__ void wgrad_thin(const WgradArgs& a, int t, int split, float* red) {
     const int M = a.M[t], N = a.N[t], K = a.K, R = a.R;
     const int kbegin = split * a.kchunk[t], kend = min(K, kbegin + a.kchunk[t]);
     const float* __restrict__ G = a.G[t];
@@ -500,11 +507,14 @@ __device__ __forceinline__ void wgrad_thin(const WgradArgs& a, int t, int split)
 }
 
 __global__ __launch_bounds__(256) void wgrad_grouped_kernel(WgradArgs a) {
+    __shared__ __attribute__((aligned(16))) float lds[kWgLds];
+    static_assert(256 * 17 <= kWgLds, "thin-transition scratch exceeds the shared LDS");
     int t = 0;
     while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
     const int local = int(blockIdx.x) - a.block_begin[t];
-    if (a.M[t] <= 16 || a.N[t] <= 16) wgrad_thin(a, t, local);
-    else wgrad_tile(a, t, local);
+    if (a.M[t] <= 16 || a.N[t] <= 16) wgrad_thin(a, t, local, lds);
+    else if (a.tile[t] == 64) wgrad_tile<64>(a, t, local, lds);
+    else wgrad_tile<128>(a, t, local, lds);
 }
 
 // grad_t[m + M*n] (+)= sum over splits of the partials of entry (m, n), n = N
@@ -889,38 +899,93 @@ __device__ GradStats block_reduce_grad(GradStats v) {
     return r;
 }
 
-__global__ __launch_bounds__(256) void grad_blocks_kernel(const float* __restrict__ g, int count,
-                                                          GradStats* __restrict__ partials) {
-    GradStats local{0.0, 0.0, 0ull, INT_MAX, 0};
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += blockDim.x * gridDim.x) {
+// Statistics of several transitions' gradients in two launches: blocks
+// [block_begin[t], block_begin[t+1]) stride transition t's entries, then one
+// block per transition combines its partials in block order.
+struct GradGroupArgs {
+    const float* g[kMaxTransitions];
+    int count[kMaxTransitions];
+    int block_begin[kMaxTransitions + 1];
+    int transitions;
+};
+
+__global__ __launch_bounds__(256) void grad_blocks_kernel(GradGroupArgs a, GradStats* __restrict__ partials) {
+    int t = 0;
+    while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
+    const int local = int(blockIdx.x) - a.block_begin[t], blocks = a.block_begin[t + 1] - a.block_begin[t];
+    const float* __restrict__ g = a.g[t];
+    GradStats acc{0.0, 0.0, 0ull, INT_MAX, 0};
+    for (int i = local * blockDim.x + threadIdx.x; i < a.count[t]; i += blockDim.x * blocks) {
         const double v = g[i];
         if (!isfinite(v)) {
-            ++local.nonfinite;
-            if (i < local.first) local.first = i;
+            ++acc.nonfinite;
+            if (i < acc.first) acc.first = i;
         } else {
-            local.squared_norm += v * v;
+            acc.squared_norm += v * v;
             const double mag = fabs(v);
-            if (mag > local.max_abs) local.max_abs = mag;
+            if (mag > acc.max_abs) acc.max_abs = mag;
         }
     }
-    local = block_reduce_grad(local);
-    if (threadIdx.x == 0) partials[blockIdx.x] = local;
+    acc = block_reduce_grad(acc);
+    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
 }
 
-__global__ __launch_bounds__(256) void grad_finish_kernel(const GradStats* __restrict__ blocks, int count,
-                                                          GradStats* __restrict__ total) {
+__global__ __launch_bounds__(256) void grad_finish_kernel(GradGroupArgs a, const GradStats* __restrict__ partials,
+                                                          GradStats* __restrict__ totals) {
+    const int t = blockIdx.x;
     GradStats v{0.0, 0.0, 0ull, INT_MAX, 0};
-    for (int i = threadIdx.x; i < count; i += blockDim.x) v = combine_grad(v, blocks[i]);
+    for (int i = a.block_begin[t] + threadIdx.x; i < a.block_begin[t + 1]; i += blockDim.x)
+        v = combine_grad(v, partials[i]);
     v = block_reduce_grad(v);
-    if (threadIdx.x == 0) *total = v;
+    if (threadIdx.x == 0) totals[t] = v;
 }
 
-void launch_grad_stats(Device& d, const float* g, int count, int slot) {
-    const int blocks = cost_blocks_for(count);
-    hipLaunchKernelGGL(grad_blocks_kernel, blocks, 256, 0, d.stream, g, count, d.grad_blocks);
+void launch_grad_stats(Device& d, const float* const* g, const int* counts, int transitions, int first_slot) {
+    GradGroupArgs a{};
+    a.transitions = transitions;
+    a.block_begin[0] = 0;
+    const int cap = std::max(1, kMaxCostBlocks / transitions);
+    for (int t = 0; t < transitions; ++t) {
+        a.g[t] = g[t];
+        a.count[t] = counts[t];
+        a.block_begin[t + 1] = a.block_begin[t] + std::min(cap, cost_blocks_for(counts[t]));
+    }
+    hipLaunchKernelGGL(grad_blocks_kernel, a.block_begin[transitions], 256, 0, d.stream, a, d.grad_blocks);
     HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(grad_finish_kernel, 1, 256, 0, d.stream, d.grad_blocks, blocks, d.grad_totals + slot);
+    hipLaunchKernelGGL(grad_finish_kernel, transitions, 256, 0, d.stream, a, d.grad_blocks, d.grad_totals + first_slot);
     HIP_CHECK(hipGetLastError());
+}
+
+// value into several buffers in one launch (buffer t holds begin[t+1]-begin[t] floats)
+struct FillArgs {
+    float* p[kMaxTransitions];
+    int begin[kMaxTransitions + 1];
+    int transitions;
+};
+
+__global__ void fill_grouped_kernel(FillArgs a, float value) {
+    const int total = a.begin[a.transitions];
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += blockDim.x * gridDim.x) {
+        int t = 0;
+        while (t + 1 < a.transitions && i >= a.begin[t + 1]) ++t;
+        a.p[t][i - a.begin[t]] = value;
+    }
+}
+
+void launch_fill_grouped(Device& d, float* const* p, const int* counts, int buffers, float value) {
+    for (int first = 0; first < buffers; first += kMaxTransitions) {
+        FillArgs a{};
+        a.transitions = std::min(kMaxTransitions, buffers - first);
+        a.begin[0] = 0;
+        for (int k = 0; k < a.transitions; ++k) {
+            a.p[k] = p[first + k];
+            a.begin[k + 1] = a.begin[k] + counts[first + k];
+        }
+        if (!a.begin[a.transitions]) continue;
+        const int blocks = std::max(1, std::min(1024, (a.begin[a.transitions] + 255) / 256));
+        hipLaunchKernelGGL(fill_grouped_kernel, blocks, 256, 0, d.stream, a, value);
+        HIP_CHECK(hipGetLastError());
+    }
 }
 
 __global__ void fill_kernel(float* __restrict__ p, size_t count, float value) {

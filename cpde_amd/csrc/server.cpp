@@ -636,7 +636,8 @@ private:
     void pass(NetRecord& n, CostRecord& c, int slot, bool& first, const Pass& how);
     void prepare_costs(NetRecord& n, const std::vector<uint64_t>& ids, uint64_t ni);
     void graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord& graph, bool backward);
-    void download(int costs, int layers, std::vector<cpde_cost_stats>& cs, std::vector<cpde_gradient_stats>& gs);
+    void download(int costs, int layers, std::vector<cpde_cost_stats>& cs, std::vector<cpde_gradient_stats>& gs,
+                  GraphRecord* graph = nullptr);
     void validate_costs(const std::vector<cpde_cost_stats>& cs, std::vector<double>& values, bool before_update);
     void evaluate_costs(NetRecord& n, const std::vector<uint64_t>& ids, std::vector<double>& values, GraphRecord* graph);
     uint64_t evaluate(uint64_t ni, uint64_t di, int chunk);
@@ -726,10 +727,17 @@ void Server::prepare_costs(NetRecord& n, const std::vector<uint64_t>& ids, uint6
     reserve_slots(int(ids.size()));
 }
 
-void Server::download(int costs, int layers, std::vector<cpde_cost_stats>& cs, std::vector<cpde_gradient_stats>& gs) {
+// Cost and gradient scalars, and the graph summary of the last graph pass, in
+// one synchronisation (Workspace::download, cuda/reduction_kernels.cuh:171-177).
+void Server::download(int costs, int layers, std::vector<cpde_cost_stats>& cs, std::vector<cpde_gradient_stats>& gs,
+                      GraphRecord* graph) {
     cs.resize(std::max(costs, 1));
     gs.resize(std::max(layers, 1));
-    call(cpde_scalars_download(dev_, costs, cs.data(), layers, gs.data()));
+    if (graph)
+        call(cpde_scalars_download_graph(dev_, costs, cs.data(), layers, gs.data(),
+                                         graph->summary.as<cpde_graph_summary>(), &graph->host));
+    else
+        call(cpde_scalars_download(dev_, costs, cs.data(), layers, gs.data()));
     cs.resize(costs);
     gs.resize(layers);
 }
@@ -803,7 +811,6 @@ void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
                 pass(n, cost(ids[i]), int(i), first,
                      Pass{true, false, multipliers + i, 0, int(i) == reuse ? last_offset : INT_MAX, false});
     }
-    call(cpde_buffer_download(dev_, &graph.host, graph.summary.ptr, sizeof graph.host));
 }
 
 void Server::evaluate_costs(NetRecord& n, const std::vector<uint64_t>& ids, std::vector<double>& values,
@@ -812,7 +819,7 @@ void Server::evaluate_costs(NetRecord& n, const std::vector<uint64_t>& ids, std:
     std::vector<cpde_gradient_stats> gs;
     if (graph) {
         graph_pass(n, ids, *graph, false);
-        download(int(ids.size()), 0, cs, gs);
+        download(int(ids.size()), 0, cs, gs, graph);
         validate_costs(cs, values, false);
         graph->validate();
         return;
@@ -1009,7 +1016,7 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
                 pass(n, cost(ids[i]), int(i), first, Pass{true, collect, nullptr, 0, INT_MAX, false});
         }
         call(cpde_inspect_gradients(n.net));
-        download(int(ids.size()), layers, cs, gs);
+        download(int(ids.size()), layers, cs, gs, graph.get());
         bool bad_gradient = false;
         for (const auto& g : gs) bad_gradient = bad_gradient || g.nonfinite_count != 0;
         if (bad_gradient || (diagnostics && ((completed + 1) % diagnostics == 0 || completed + 1 == epochs))) {
@@ -1407,7 +1414,7 @@ void Server::command(uint32_t op, Frame& b, std::atomic<bool>& stop) {
             if (gradient) call(cpde_inspect_gradients(n.net));
             std::vector<cpde_cost_stats> cs;
             std::vector<cpde_gradient_stats> gs;
-            download(int(ids.size()), gradient ? n.transitions() : 0, cs, gs);
+            download(int(ids.size()), gradient ? n.transitions() : 0, cs, gs, &graph);
             validate_costs(cs, values, false);
             graph.validate();
             out.put<double>(graph.host.value);

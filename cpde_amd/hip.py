@@ -67,6 +67,7 @@ SIGNATURES = {
     'cpde_backward': (i32, [vp, i32]),
     'cpde_inspect_gradients': (i32, [vp]),
     'cpde_scalars_download': (i32, [vp, i32, vp, i32, vp]),
+    'cpde_scalars_download_graph': (i32, [vp, i32, vp, i32, vp, vp, vp]),
     'cpde_rprop': (i32, [vp]),
     'cpde_adam': (i32, [vp, i32, f32]),
     'cpde_set_steps': (i32, [vp, f32]),
@@ -77,7 +78,7 @@ SIGNATURES = {
     'cpde_program_destroy': (i32, [vp]),
     'cpde_cost_expression': (i32, [vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, i32]),
     'cpde_graph_execute': (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, i32]),
-    'cpde_jit_prepare': (i32, [i32, i32, vp, i32, vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
+    'cpde_jit_prepare': (i32, [i32, i32, vp, i32, vp, i32, i32, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     'cpde_trace_enable': (i32, [vp, i32]),
     'cpde_trace_read': (i32, [vp, i32, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_double),
                               ctypes.POINTER(ctypes.c_double)]),
@@ -319,14 +320,15 @@ class Plan:
             self.handle = None
 
 
-def jit_prepare(table, neurons, arch='gfx950'):
-    """Compile the fused kernels of (schema, architecture) into the code-object
-    cache; no device needed.  Returns the compiler log."""
+def jit_prepare(table, neurons, width=0, compute_units=256, arch='gfx950'):
+    """Compile the fused kernels of (schema, architecture) for chunks of `width`
+    points on a device of `compute_units` CUs into the code-object cache; no
+    device needed.  Returns the compiler log."""
     t = np.ascontiguousarray(table, np.int32)
     n = np.ascontiguousarray(neurons, np.int32)
     log = ctypes.create_string_buffer(1 << 16)
-    code = load().cpde_jit_prepare(t.shape[0], t.shape[1] - 1, _ptr(t), len(n), _ptr(n), arch.encode(), log,
-                                   len(log))
+    code = load().cpde_jit_prepare(t.shape[0], t.shape[1] - 1, _ptr(t), len(n), _ptr(n), width, compute_units,
+                                   arch.encode(), log, len(log))
     if code != OK:
         raise CpdeError(code, load().cpde_last_error().decode('utf-8', 'replace') + log.value.decode())
     return log.value.decode()

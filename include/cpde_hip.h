@@ -160,6 +160,13 @@ int cpde_inspect_gradients(cpde_net* net);
 /* Synchronous download of cost slots and gradient-statistics slots (Workspace::download). */
 int cpde_scalars_download(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
                           cpde_gradient_stats* gradient_out);
+/* The same, plus a scalar graph's summary (device, written by cpde_graph_execute)
+ * in the same synchronisation: one host round trip per graph epoch, as the
+ * reference queues the graph copy before its scalar download
+ * (cuda/cpde_server.cu:317, cuda/reduction_kernels.cuh:171-177). */
+int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
+                                cpde_gradient_stats* gradient_out, const cpde_graph_summary* summary,
+                                cpde_graph_summary* summary_out);
 /* RPROP over every transition, then switch the active gradient buffer
  * (Resile_k + switch_active, cuda/derivative_kernels_v4.cu:752-778). */
 int cpde_rprop(cpde_net* net);
@@ -191,12 +198,13 @@ int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int coun
                        double* values, double* adjoints, double* multipliers, int* active,
                        cpde_graph_summary* summary, int gradient);
 
-/* Compile the schema-specialised layer-fused kernels of (schema, architecture)
- * for a GPU architecture (e.g. "gfx950") into the on-disk code-object cache,
+/* Compile the schema-specialised fused kernels of (schema, architecture) for
+ * chunks of `width` points (0: any) on a device of `compute_units` CUs, for a
+ * GPU architecture (e.g. "gfx950"), into the on-disk code-object cache,
  * without a device.  The reference's analogue is its per-expression NVRTC
  * compile (cuda/expression_program.hpp:104-121), done lazily at first use. */
-int cpde_jit_prepare(int rows, int variables, const int* table, int layers, const int* neurons, const char* arch,
-                     char* log, size_t log_capacity);
+int cpde_jit_prepare(int rows, int variables, const int* table, int layers, const int* neurons, int width,
+                     int compute_units, const char* arch, char* log, size_t log_capacity);
 
 /* ---- timing ---------------------------------------------------------------------- */
 /* Kernel tracing (no counterpart in the reference, which has no built-in
