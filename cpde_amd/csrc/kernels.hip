@@ -522,8 +522,9 @@ __global__ __launch_bounds__(256) void wgrad_grouped_kernel(WgradArgs a) {
 // entries x 4 waves, wave w sums splits w, w+4, ... (eight running sums,
 // combined in a fixed order), then the four wave sums in wave order.
 // Split-minor partials ([entry][split]): one wave per entry, lane l sums splits
-// l, l+64, ... in order, then a fixed shuffle tree.  Either way the summation
-// order is fixed whatever the scheduling.
+// l + 64u (+ 256i) into running sum u (four, combined in a fixed order), then a
+// fixed shuffle tree.  Either way the summation order is fixed whatever the
+// scheduling.
 __global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
     __shared__ float part[4][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -560,8 +561,13 @@ __global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
         const int j = local * 4 + wave;
         if (j >= count) return;
         const float* P = a.partial[t] + size_t(j) * S;
-        float s = 0.0f;
-        for (int q = lane; q < S; q += 64) s += P[q];
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four loads in flight per lane
+        int q = lane;
+        for (; q + 192 < S; q += 256)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[u] += P[q + 64 * u];
+        for (int u = 0; q < S; q += 64, ++u) acc[u] += P[q];
+        float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
         for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
         if (lane == 0) {
             const int mrow = j / N1, n = j - mrow * N1;
@@ -589,22 +595,29 @@ void launch_reduce_grouped(Device& d, const ReduceArgs& a) {
 // ------------------------------------------------------------------------------------------
 // Activation of a chunk (Server::activate, cuda/cpde_server.cu:158-170) and the
 // evaluation copy-out (:180): wire layout [row][sample][channel] <-> stack.
+// One lane per (point, row) of the chunk: copies that row's channels (32-bit
+// index arithmetic; the host checks width * R fits).
 __global__ void activate_kernel(float* __restrict__ x, const float* __restrict__ data, int data_width, int channels,
                                 const int* __restrict__ rows, int R, int width, int offset, int valid) {
-    const size_t total = size_t(width) * R * channels;
-    for (size_t e = blockIdx.x * size_t(blockDim.x) + threadIdx.x; e < total; e += size_t(gridDim.x) * blockDim.x) {
-        const int c = int(e % channels);
-        const size_t pr = e / channels;
-        const int r = int(pr % R), p = int(pr / R);
-        x[e] = p < valid ? data[(size_t(rows[r]) * data_width + offset + p) * channels + c] : 0.0f;
+    const int total = width * R;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        const int p = e / R, r = e - p * R;
+        float* dst = x + size_t(e) * channels;
+        if (p < valid) {
+            const float* src = data + (size_t(rows[r]) * data_width + offset + p) * channels;
+            for (int c = 0; c < channels; ++c) dst[c] = src[c];
+        } else {
+            for (int c = 0; c < channels; ++c) dst[c] = 0.0f;
+        }
     }
 }
 
 void launch_activate(Device& d, float* x, const float* data, int data_width, int channels, const int* rows_dev,
                      int rows, int width, int offset, int valid) {
-    const size_t total = size_t(width) * rows * channels;
+    const size_t total = size_t(width) * rows;
+    require(total < (size_t(1) << 31), "chunk too large for one activation");
     const int blocks = int(std::min<size_t>((total + 255) / 256, 4096));
-    TraceScope trace(d, kTraceActivate, 8.0 * double(total));
+    TraceScope trace(d, kTraceActivate, 8.0 * double(total) * channels);
     hipLaunchKernelGGL(activate_kernel, blocks, 256, 0, d.stream, x, data, data_width, channels, rows_dev, rows, width,
                        offset, valid);
     HIP_CHECK(hipGetLastError());
@@ -612,20 +625,21 @@ void launch_activate(Device& d, float* x, const float* data, int data_width, int
 
 __global__ void output_kernel(float* __restrict__ dest, const float* __restrict__ out, int dest_width, int channels,
                               const int* __restrict__ rows, int R, int offset, int valid) {
-    const size_t total = size_t(valid) * R * channels;
-    for (size_t e = blockIdx.x * size_t(blockDim.x) + threadIdx.x; e < total; e += size_t(gridDim.x) * blockDim.x) {
-        const int c = int(e % channels);
-        const size_t pr = e / channels;
-        const int r = int(pr % R), p = int(pr / R);
-        dest[(size_t(rows[r]) * dest_width + offset + p) * channels + c] = out[e];
+    const int total = valid * R;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        const int p = e / R, r = e - p * R;
+        const float* src = out + size_t(e) * channels;
+        float* dst = dest + (size_t(rows[r]) * dest_width + offset + p) * channels;
+        for (int c = 0; c < channels; ++c) dst[c] = src[c];
     }
 }
 
 void launch_output(Device& d, float* dest, const float* out, int dest_width, int channels, const int* rows_dev,
                    int rows, int width, int offset, int valid) {
     (void)width;
-    const size_t total = size_t(valid) * rows * channels;
+    const size_t total = size_t(valid) * rows;
     if (!total) return;
+    require(total < (size_t(1) << 31), "chunk too large for one output copy");
     const int blocks = int(std::min<size_t>((total + 255) / 256, 4096));
     hipLaunchKernelGGL(output_kernel, blocks, 256, 0, d.stream, dest, out, dest_width, channels, rows_dev, rows, offset,
                        valid);
