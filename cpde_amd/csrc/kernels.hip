@@ -337,22 +337,31 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local,
     const float* __restrict__ G = a.G[t];
     const float* __restrict__ Y = a.Y[t];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = lane & 31, h = lane >> 5;
-    // staging: thread -> 4 consecutive columns at 4*(tid % (TILE/4)) of rows tid/(TILE/4) + RP*j
+    // staging: thread -> 4 consecutive columns at 4*(tid % (TILE/4)) of rows tid/(TILE/4) + RP*j;
+    // pointers advance by one chunk per step, bounds are per thread and fixed
     const int sc = 4 * (tid % (TILE / 4)), sr = tid / (TILE / 4);
-    const bool vecm = (M % 4) == 0, vecn = (N % 4) == 0;
-    auto load = [&](const float* src, int ld, int c0, int cmax, bool vec, int k) -> float4 {
+    const bool g_vec = (M % 4) == 0 && m0 + sc + 3 < M, y_vec = (N % 4) == 0 && n0 + sc + 3 < N;
+    const int g_cols = max(0, min(4, M - m0 - sc)), y_cols = max(0, min(4, N - n0 - sc));
+    const float* gp = G + size_t(kbegin + sr) * M + m0 + sc;
+    const float* yp = Y + size_t(kbegin + sr) * N + n0 + sc;
+    auto load = [](const float* p, bool vec, int cols) -> float4 {
+        if (vec) return *reinterpret_cast<const float4*>(p);
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (k < kend) {
-            const float* p = src + size_t(k) * ld + c0 + sc;
-            if (vec && c0 + sc + 3 < cmax) v = *reinterpret_cast<const float4*>(p);
-            else {
-                if (c0 + sc + 0 < cmax) v.x = p[0];
-                if (c0 + sc + 1 < cmax) v.y = p[1];
-                if (c0 + sc + 2 < cmax) v.z = p[2];
-                if (c0 + sc + 3 < cmax) v.w = p[3];
-            }
-        }
+        if (cols > 0) v.x = p[0];
+        if (cols > 1) v.y = p[1];
+        if (cols > 2) v.z = p[2];
+        if (cols > 3) v.w = p[3];
         return v;
+    };
+    auto stage = [&](float4* ga, float4* ya, int k0) {  // rows k0 + sr + RP*j of G and Y
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const bool in = k0 + sr + RP * j < kend;
+            ga[j] = in ? load(gp + size_t(RP) * j * M, g_vec, g_cols) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            ya[j] = in ? load(yp + size_t(RP) * j * N, y_vec, y_cols) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        gp += size_t(kWgKC) * M;
+        yp += size_t(kWgKC) * N;
     };
     floatx16 acc[WX][WX];
 #pragma unroll
@@ -362,13 +371,10 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local,
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[x][y][v] = 0.0f;
     float bias = 0.0f;  // tile column 0 blocks: thread tid < TILE sums G[k][m0+tid] over value rows
+    int value_col = (kbegin + a.R - 1) / a.R * a.R;  // next value-row column
     const int wm = (TILE / 2) * (wave & 1), wn = (TILE / 2) * (wave >> 1);
     float4 ga[J], ya[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        ga[j] = load(G, M, m0, M, vecm, kbegin + sr + RP * j);
-        ya[j] = load(Y, N, n0, N, vecn, kbegin + sr + RP * j);
-    }
+    stage(ga, ya, kbegin);
     int buf = 0;
     for (int k0 = kbegin; k0 < kend; k0 += kWgKC) {
 #pragma unroll
@@ -377,13 +383,7 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local,
             *reinterpret_cast<float4*>(&Bs[buf][sr + RP * j][sc]) = ya[j];
         }
         __syncthreads();
-        if (k0 + kWgKC < kend) {
-#pragma unroll
-            for (int j = 0; j < J; ++j) {
-                ga[j] = load(G, M, m0, M, vecm, k0 + kWgKC + sr + RP * j);
-                ya[j] = load(Y, N, n0, N, vecn, k0 + kWgKC + sr + RP * j);
-            }
-        }
+        if (k0 + kWgKC < kend) stage(ga, ya, k0 + kWgKC);
         __builtin_amdgcn_iglp_opt(0);  // interleave the LDS operand reads with the MFMAs
 #pragma unroll
         for (int kk = 0; kk < kWgKC; kk += 2) {
@@ -400,8 +400,8 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local,
                     acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[x], bv[y], acc[x][y], 0, 0, 0);
         }
         if (n0 == 0 && tid < TILE) {
-            const int first = (k0 + a.R - 1) / a.R * a.R;
-            for (int c = first; c < min(kend, k0 + kWgKC); c += a.R) bias += As[buf][c - k0][tid];
+            const int stop = min(kend, k0 + kWgKC);
+            for (; value_col < stop; value_col += a.R) bias += As[buf][value_col - k0][tid];
         }
         buf ^= 1;
     }
