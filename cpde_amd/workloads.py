@@ -324,6 +324,15 @@ class PoissonWorkload:
         from .wire import graph_bytes
         return graph_bytes([(1, 0, 0), (1, 1, 0), (3, 0, 1)], [0.0, 0.0, 0.0], 2)
 
+    @staticmethod
+    def value_dependent_graph():
+        """Root = leaf0 / leaf1 + log(leaf0) + leaf1 ** 1.5: every leaf multiplier
+        depends on the leaf values (scalar ops Leaf 1, Add 3, Div 6, Power 7,
+        Log 10, cuda/scalar_ops.cuh:5)."""
+        from .wire import graph_bytes
+        nodes = [(1, 0, 0), (1, 1, 0), (6, 0, 1), (10, 0, 0), (3, 2, 3), (7, 1, 0), (3, 4, 5)]
+        return graph_bytes(nodes, [0.0, 0.0, 0.0, 0.0, 0.0, 1.5, 0.0], 6)
+
     def upload(self, session):
         vschema = closed_schema(2, [])
         di = session.data(input_stack(self.interior, self.schema), self.schema)

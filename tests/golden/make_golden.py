@@ -172,6 +172,17 @@ def case_poisson(s):
     for leaf in range(2):
         v, _ = s.graph_eval(ids['net'], [ids['costs'][leaf]], SINGLE_LEAF, gradient=False)
         rec[f'leaf{leaf}'] = np.float64(v)
+    # a graph whose leaf multipliers depend on the leaf values (second backward
+    # pass, cuda/cpde_server.cu:279-316): leaf0 / leaf1 + log(leaf0) + leaf1 ** 1.5
+    graph = W.PoissonWorkload.value_dependent_graph()
+    value, grads = s.graph_eval(ids['net'], ids['costs'], graph, gradient=True)
+    rec['vgraph_loss'] = np.float64(value)
+    for t, g in enumerate(grads):
+        rec[f'vgraph_grad{t}'] = g
+    res = s.train(ids['net'], ids['costs'], 2, method=0, fresh=1, log=1, graph=graph)
+    rec['vgraph_reports'] = np.asarray([(e['completed'], e['updates'], e['after'], e['total'])
+                                        for e in res['events'] if e['kind'] == 6], np.float64)
+    rec['vgraph_state'] = np.frombuffer(s.snapshot(ids['net']), np.uint8)
     return rec
 
 

@@ -80,6 +80,35 @@ def test_expression_costs_and_graph(server):
     assert 'expression' in source
 
 
+def test_value_dependent_graph_multipliers(server):
+    """root = leaf0 / leaf1 + log(leaf0) + leaf1 ** 1.5: the leaf multipliers are
+    known only after the forward passes, so every leaf runs a second, backward
+    pass scaled by its multiplier (one leaf reusing its last forward chunk).
+    Objective, gradients, two training epochs' reports and the final state
+    against the reference server."""
+    from cpde_amd import workloads as W
+    g = load_golden('poisson')
+    pw = W.PoissonWorkload(radial=int(g['radial']), angular=int(g['angular']), boundary=int(g['boundary']))
+    graph = W.PoissonWorkload.value_dependent_graph()
+    ids = pw.upload(server)
+    value, grads = server.graph_eval(ids['net'], ids['costs'], graph, gradient=True)
+    print(f'[result] objective {value!r} reference {float(g["vgraph_loss"])!r}', flush=True)
+    assert abs(value / g['vgraph_loss'] - 1) < 1e-4
+    for t, grad in enumerate(grads):
+        assert rel_l2(grad, g[f'vgraph_grad{t}']) < 1e-3
+    res = server.train(ids['net'], ids['costs'], 2, method=0, fresh=1, log=1, graph=graph)
+    reports = np.asarray([(e['completed'], e['updates'], e['after'], e['total']) for e in res['events']
+                          if e['kind'] == 6])
+    assert reports.shape == g['vgraph_reports'].shape
+    np.testing.assert_array_equal(reports[:, :3], g['vgraph_reports'][:, :3])
+    np.testing.assert_allclose(reports[:, 3], g['vgraph_reports'][:, 3], rtol=1e-4)
+    ours = wire.decode_state(server.snapshot(ids['net']))
+    ref = wire.decode_state(bytes(g['vgraph_state']))
+    assert ours[0] == ref[0]
+    for a, b in zip(ours[1], ref[1]):
+        assert rel_l2(a['buffers'][0], b['buffers'][0]) < 1e-5
+
+
 def test_polynomial_cost(server):
     g = load_golden('polynomial')
     schema = g['schema']
