@@ -346,7 +346,7 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
             s = thin(t) ? 2 * d.compute_units : int(wgrad_blocks_per_cu() * d.compute_units / total_tiles + 0.5);
             s = std::max(1, std::min(s, std::max(1, K / 64)));
             int chunk = (K + s - 1) / s;
-            chunk = (chunk + 31) / 32 * 32;
+            chunk = (chunk + kWgradChunk - 1) / kWgradChunk * kWgradChunk;
             s = (K + chunk - 1) / chunk;
             g.wa.M[w] = M;
             g.wa.N[w] = N;

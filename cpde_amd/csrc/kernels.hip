@@ -310,11 +310,11 @@ void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, 
 // value-row columns), reduced in split order by reduce_grouped_kernel so the
 // result does not depend on scheduling.  Two block roles:
 //  * matrix-core tiles (M, N > 16): a 128x128 (or 64x64) tile, K staged
-//    through LDS in chunks of 32 columns (double-buffered, the next chunk's
+//    through LDS in chunks of 64 columns (double-buffered, the next chunk's
 //    global loads in flight during the current chunk's MFMAs);
 //  * thin transitions (M or N <= 16: the input and output layers): lanes
 //    stride the wide side and accumulate the narrow side in registers.
-constexpr int kWgKC = 32;                          // columns per LDS chunk
+constexpr int kWgKC = kWgradChunk;                 // columns per LDS chunk
 constexpr int kWgLds = 2 * 2 * kWgKC * (128 + 4);  // floats of LDS shared by the block roles
 
 // Matrix-core tile of one split: TILE x TILE of dW (TILE = 128, or 64 for
