@@ -43,7 +43,7 @@ PUBLISHED_POINTS_DERIVS_PER_S = 729 * 28 / 5.65e-3
 PEAK_FP32_MFMA = 157.3e12   # flop/s, dense
 PEAK_HBM = 8.0e12           # bytes/s
 MFMA_KINDS = {'gemm_forward', 'gemm_transposed', 'gemm_wgrad', 'fused_forward', 'fused_backward', 'network_forward',
-              'network_backward'}
+              'network_backward', 'network_epoch'}
 # CPU baseline sample: about this many multiply-adds of the linear steps
 # (rows x points x sum of n_in*n_out), ~12 s of the reference CPU server on
 # one core of the benchmark host.

@@ -131,6 +131,14 @@ static int guarded(F body) {
     }
 }
 
+// Re-raise the failure of a nested entry point with its own error class.
+[[noreturn]] static void throw_code(int code) {
+    const std::string message = last_error;
+    if (code == CPDE_EINVAL) throw invalid(message);
+    if (code == CPDE_ECOMPILE) throw compile_error(message);
+    throw device_error(message);
+}
+
 static const float* activations(const Net& net, int l) { return net.linear[l] ? net.z[l] : net.y[l]; }
 
 // Device copy of a host row map; re-uploaded only when it changes (the map is
@@ -221,6 +229,7 @@ static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const
     HIP_CHECK(hipModuleLoadData(&m->module, code.data()));
     HIP_CHECK(hipModuleGetFunction(&m->network_forward, m->module, "network_forward_k"));
     HIP_CHECK(hipModuleGetFunction(&m->network_backward, m->module, "network_backward_k"));
+    HIP_CHECK(hipModuleGetFunction(&m->network_epoch, m->module, "network_epoch_k"));
     HIP_CHECK(hipModuleGetFunction(&m->input_layer, m->module, "input_layer_k"));
     HIP_CHECK(hipModuleGetFunction(&m->output_backward, m->module, "output_backward_k"));
     const int L = int(neurons.size());
@@ -387,6 +396,66 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
 static void run_gradients(Device& d, const GradientPlan& g) {
     if (g.wa.transitions > 0) launch_wgrad_grouped(d, g.wa, g.flops);
     launch_reduce_grouped(d, g.ra);
+}
+
+// Host mirror of the one-pass epoch's matching arguments (fused.hip.in MatchArgs).
+struct MatchArgsHost {
+    const float* target;
+    const int* target_rows;
+    const float* weights;
+    CostStats* partials;
+    int target_width, weight_samples, offset, valid, collect;
+};
+
+// Forward, matching cost and backward of one chunk in one network-fused launch,
+// then the cost's fixed-order finish and the weight-gradient contraction.
+static void fused_epoch(Plan& p, const MatchArgsHost& match, int cost_index, bool accumulate) {
+    Net& n = *p.net;
+    Device& d = *n.dev;
+    FusedModule& fm = *p.fused;
+    const int L = n.layers;
+    int width = p.width;
+    const double cols = double(p.columns());
+    const int blocks = (width + fm.net_points_per_block - 1) / fm.net_points_per_block;
+    if (blocks > p.epoch_capacity) {
+        HIP_CHECK(hipStreamSynchronize(d.stream));
+        if (p.epoch_partials) HIP_CHECK(hipFree(p.epoch_partials));
+        p.epoch_partials = nullptr;
+        HIP_CHECK(hipMalloc(&p.epoch_partials, sizeof(CostStats) * size_t(blocks)));
+        p.epoch_capacity = blocks;
+    }
+    std::vector<int> external(L - 1, 0);
+    external[0] = external[L - 2] = blocks;
+    const GradientPlan g = plan_gradients(p, accumulate, external);
+    NetArgsHost a = net_args(n);
+    a.partial_in = n.partials + g.offset[0];
+    a.partial_out = n.partials + g.offset[L - 2];
+    MatchArgsHost m = match;
+    m.partials = p.epoch_partials;
+    {
+        // the backward half reads the row-major weight copies of every hidden
+        // transition, which no workgroup of the same launch may still be writing
+        std::vector<const float*> W;
+        std::vector<float*> WT;
+        std::vector<int> ni, no;
+        for (int t = 1; t + 2 < L; ++t) {
+            W.push_back(n.state[0][t]);
+            WT.push_back(n.wt[t]);
+            ni.push_back(n.neurons[t]);
+            no.push_back(n.neurons[t + 1]);
+        }
+        launch_transpose(d, W.data(), WT.data(), ni.data(), no.data(), int(W.size()));
+    }
+    void* args[] = {&a, &m, &width};
+    double flops = 0;
+    for (int t = 0; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
+    for (int t = 1; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
+    {
+        TraceScope trace(d, kTraceNetworkEpoch, flops);
+        launch_module(d, fm.network_epoch, unsigned(blocks), 1, args);
+    }
+    launch_finish_cost(d, p.epoch_partials, blocks, cost_index);
+    run_gradients(d, g);
 }
 
 static void weight_gradients(Plan& p, bool accumulate) {
@@ -659,6 +728,7 @@ int cpde_plan_destroy(cpde_plan* plan) {
         (void)hipStreamSynchronize(plan->net->dev->stream);
         (void)hipFree(plan->dev_tables);
         (void)hipFree(plan->dev_rows);
+        (void)hipFree(plan->epoch_partials);
         delete plan;
     });
 }
@@ -730,6 +800,35 @@ int cpde_cost_matching(cpde_plan* plan, const float* target, int target_width, c
         const int L = n.layers;
         launch_matching(d, *plan, n.z[L - 1], gradient ? n.g[L - 1] : nullptr, target, target_width, target_rows,
                         weights, weight_samples, offset, valid, cost_index, collect != 0, gradient != 0);
+    });
+}
+
+int cpde_epoch_matching(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
+                        const float* weights, int weight_samples, int offset, int valid, int cost_index, int collect,
+                        int accumulate) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
+        require(plan->backward, "plan has no adjoint storage");
+        require(valid >= 0 && valid <= plan->width && offset >= 0, "invalid chunk range");
+        // one launch where the whole chunk's workgroups are resident together (the
+        // saved kernel boundary matters); separate launches for long grids, where
+        // the forward keeps its own, higher occupancy
+        const bool one_pass = plan->fused && plan->network &&
+                              (plan->width + plan->fused->net_points_per_block - 1) / plan->fused->net_points_per_block <=
+                                  4 * d.compute_units;
+        if (!one_pass) {
+            if (int code = cpde_forward(plan)) throw_code(code);
+            if (int code = cpde_cost_matching(plan, target, target_width, target_rows, weights, weight_samples, offset,
+                                              valid, cost_index, collect, 1))
+                throw_code(code);
+            if (int code = cpde_backward(plan, accumulate)) throw_code(code);
+            return;
+        }
+        const MatchArgsHost m{target, target_rows, weights, nullptr, target_width, weight_samples, offset, valid,
+                              collect != 0};
+        fused_epoch(*plan, m, cost_index, accumulate != 0);
     });
 }
 
@@ -964,7 +1063,7 @@ const char* cpde_trace_name(int kind) {
         "compose_forward", "compose_adjoint", "gemm_forward",   "gemm_transposed", "gemm_wgrad",
         "split_reduce",    "bias_grad",       "activate",       "cost",            "reduce",
         "optimizer",       "other",           "fused_input",    "fused_forward",   "fused_backward",
-        "fused_output_backward", "network_forward", "network_backward"};
+        "fused_output_backward", "network_forward", "network_backward", "network_epoch"};
     return kind >= 0 && kind < kTraceKinds ? names[kind] : "";
 }
 

@@ -99,6 +99,8 @@ struct Plan {
     std::vector<int> host_rows;
     std::shared_ptr<FusedModule> fused;  // null: table-driven kernels
     bool network = false;                // fused: one network-wide kernel per pass
+    CostStats* epoch_partials = nullptr;  // one-pass epoch: one cost record per workgroup
+    int epoch_capacity = 0;
     size_t columns() const { return size_t(rows) * size_t(width); }
 };
 
@@ -116,7 +118,7 @@ enum TraceKind {
     kTraceComposeForward, kTraceComposeAdjoint, kTraceGemm, kTraceGemmTransposed, kTraceWgrad, kTraceSplitReduce,
     kTraceBiasGrad, kTraceActivate, kTraceCost, kTraceReduce, kTraceOptimizer, kTraceOther, kTraceFusedInput,
     kTraceFusedForward, kTraceFusedBackward, kTraceFusedOutput, kTraceNetworkForward, kTraceNetworkBackward,
-    kTraceKinds
+    kTraceNetworkEpoch, kTraceKinds
 };
 struct TraceRecord {
     int kind;
@@ -178,7 +180,7 @@ struct FusedModule {
     hipModule_t module = nullptr;
     hipFunction_t input_layer = nullptr, output_backward = nullptr;
     std::vector<hipFunction_t> hidden_forward, hidden_backward;  // per transition (index t)
-    hipFunction_t network_forward = nullptr, network_backward = nullptr;
+    hipFunction_t network_forward = nullptr, network_backward = nullptr, network_epoch = nullptr;
     int points_per_block = 2, net_points_per_block = 1;
     ~FusedModule();
 };
@@ -226,6 +228,11 @@ void launch_costs_begin(Device& d, int costs);
 // Statistics of `transitions` (<= kMaxTransitions) gradients into slots first_slot...
 void launch_grad_stats(Device& d, const float* const* g, const int* counts, int transitions, int first_slot);
 void launch_fill_grouped(Device& d, float* const* p, const int* counts, int buffers, float value);
+// WT[t][i + n_in*o] = W[t][o + n_out*i] for `count` blocks in one launch.
+void launch_transpose(Device& d, const float* const* W, float* const* WT, const int* n_in, const int* n_out,
+                      int count);
+// Fixed-order sum of `blocks` per-workgroup cost records into cost slot cost_index.
+void launch_finish_cost(Device& d, const CostStats* partials, int blocks, int cost_index);
 void launch_fill(Device& d, float* p, size_t count, float value);
 void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, int NI, int NO, int R, int columns);
 void launch_wgrad_grouped(Device& d, const WgradArgs& a, double flops);

@@ -345,31 +345,40 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
         if (G > 1) o << "#define CPDE_SPLIT" << G << " 1\n";
     o << compose_source(t, splits);
     o << kFusedSource;
-    // network-fused forward and backward, one call per layer with its widths
-    o << "\nextern \"C\" __global__ __launch_bounds__(256, " << tuning.forward_blocks << ") void network_forward_k(NetArgs a, int points) {\n"
-         "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
-         "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n"
-         "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n";
+    // network-fused forward and backward, one call per layer with its widths;
+    // the one-pass epoch runs both with the matching cost between them
+    std::ostringstream fwd, bwd;
+    fwd << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n";
     for (int t = 1; t + 2 < L; ++t)
-        o << "    net_transpose<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ");\n";
-    o << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
-         "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
-         "    __syncthreads();\n";
+        fwd << "    net_transpose<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ");\n";
+    fwd << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
+        << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
+        << "    __syncthreads();\n";
     for (int t = 1; t + 2 < L; ++t)
-        o << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
-    o << "    net_output<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2 << ", X, p0, npts);\n}\n";
+        fwd << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
+    fwd << "    net_output<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2 << ", X, p0, npts);\n";
+    bwd << "    net_output_backward<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2
+        << ", X, p0, npts);\n";
+    for (int t = L - 3; t >= 1; --t)
+        bwd << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
+    bwd << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
+    const char* tiles =
+        "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
+        "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n";
+    o << "\nextern \"C\" __global__ __launch_bounds__(256, " << tuning.forward_blocks
+      << ") void network_forward_k(NetArgs a, int points) {\n"
+      << tiles << fwd.str() << "}\n";
     o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
       << ") void network_backward_k(NetArgs a, int points) {\n"
-         "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
-         "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n"
-         "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
-         "    net_output_backward<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2
-      << ", X, p0, npts);\n";
-    for (int t = L - 3; t >= 1; --t)
-        o << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t
-          << ", X, T, p0, npts);\n";
-    o << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
-    o << "}\n";
+      << tiles << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n" << bwd.str() << "}\n";
+    // the one-pass epoch reads the row-major weight copies written before its launch
+    std::string fwd_epoch = fwd.str();
+    for (size_t at; (at = fwd_epoch.find("    net_transpose<")) != std::string::npos;)
+        fwd_epoch.erase(at, fwd_epoch.find('\n', at) - at + 1);
+    o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
+      << ") void network_epoch_k(NetArgs a, MatchArgs m, int points) {\n"
+      << tiles << fwd_epoch << "    __syncthreads();  // the output stack of the block's points is written\n"
+      << "    net_match<" << neurons[L - 1] << ">(a, m, " << L - 1 << ", T, p0, npts);\n" << bwd.str() << "}\n";
     o << "\nextern \"C\" __global__ __launch_bounds__(256) void input_layer_k(const float* W, const float* X, float* Z,"
          " float* Y, int points) { input_layer<"
       << neurons[0] << ", " << neurons[1] << ">(W, X, Z, Y, points); }\n";

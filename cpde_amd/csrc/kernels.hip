@@ -692,12 +692,33 @@ __global__ __launch_bounds__(kCostThreads) void cost_finish_kernel(const CostSta
 
 static int cost_blocks_for(int count) { return std::max(1, std::min(kMaxCostBlocks, (count + kCostThreads - 1) / kCostThreads)); }
 
-static void finish_cost(Device& d, int blocks, int cost_index) {
+// First stage for long record lists: block b combines records [b*per, (b+1)*per)
+// in order into out[b].
+__global__ __launch_bounds__(kCostThreads) void cost_stage_kernel(const CostStats* __restrict__ in, int count, int per,
+                                                                  CostStats* __restrict__ out) {
+    CostStats v = empty_cost();
+    const int begin = blockIdx.x * per, end = min(count, begin + per);
+    for (int i = begin + threadIdx.x; i < end; i += blockDim.x) v = combine(v, in[i]);
+    v = block_reduce_cost(v);
+    if (threadIdx.x == 0) out[blockIdx.x] = v;
+}
+
+void launch_finish_cost(Device& d, const CostStats* partials, int blocks, int cost_index) {
     TraceScope trace(d, kTraceReduce, double(sizeof(CostStats)) * (blocks + 2));
-    hipLaunchKernelGGL(cost_finish_kernel, 1, kCostThreads, 0, d.stream, d.cost_blocks, blocks,
+    if (blocks > kMaxCostBlocks) {
+        const int per = (blocks + kMaxCostBlocks - 1) / kMaxCostBlocks;
+        const int staged = (blocks + per - 1) / per;
+        hipLaunchKernelGGL(cost_stage_kernel, staged, kCostThreads, 0, d.stream, partials, blocks, per, d.cost_blocks);
+        HIP_CHECK(hipGetLastError());
+        partials = d.cost_blocks;
+        blocks = staged;
+    }
+    hipLaunchKernelGGL(cost_finish_kernel, 1, kCostThreads, 0, d.stream, partials, blocks,
                        d.cost_totals + cost_index);
     HIP_CHECK(hipGetLastError());
 }
+
+static void finish_cost(Device& d, int blocks, int cost_index) { launch_finish_cost(d, d.cost_blocks, blocks, cost_index); }
 
 __global__ void clear_costs_kernel(CostStats* c, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += blockDim.x * gridDim.x) c[i] = empty_cost();
@@ -968,6 +989,47 @@ void launch_grad_stats(Device& d, const float* const* g, const int* counts, int 
     HIP_CHECK(hipGetLastError());
     hipLaunchKernelGGL(grad_finish_kernel, transitions, 256, 0, d.stream, a, d.grad_blocks, d.grad_totals + first_slot);
     HIP_CHECK(hipGetLastError());
+}
+
+// Row-major copies WT[i + n_in*o] = W[o + n_out*i] of several weight blocks in
+// one launch (the network-fused backward's product operands).
+struct TransposeArgs {
+    const float* W[kMaxTransitions];
+    float* WT[kMaxTransitions];
+    int n_in[kMaxTransitions], n_out[kMaxTransitions];
+    int begin[kMaxTransitions + 1];
+    int transitions;
+};
+
+__global__ void transpose_kernel(TransposeArgs a) {
+    const int total = a.begin[a.transitions];
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += blockDim.x * gridDim.x) {
+        int t = 0;
+        while (t + 1 < a.transitions && e >= a.begin[t + 1]) ++t;
+        const int local = e - a.begin[t], ni = a.n_in[t];
+        const int o = local / ni, i = local - o * ni;
+        a.WT[t][local] = a.W[t][o + a.n_out[t] * i];
+    }
+}
+
+void launch_transpose(Device& d, const float* const* W, float* const* WT, const int* n_in, const int* n_out,
+                      int count) {
+    for (int first = 0; first < count; first += kMaxTransitions) {
+        TransposeArgs a{};
+        a.transitions = std::min(kMaxTransitions, count - first);
+        a.begin[0] = 0;
+        for (int k = 0; k < a.transitions; ++k) {
+            a.W[k] = W[first + k];
+            a.WT[k] = WT[first + k];
+            a.n_in[k] = n_in[first + k];
+            a.n_out[k] = n_out[first + k];
+            a.begin[k + 1] = a.begin[k] + n_in[first + k] * n_out[first + k];
+        }
+        if (!a.begin[a.transitions]) continue;
+        const int blocks = std::max(1, std::min(1024, (a.begin[a.transitions] + 255) / 256));
+        hipLaunchKernelGGL(transpose_kernel, blocks, 256, 0, d.stream, a);
+        HIP_CHECK(hipGetLastError());
+    }
 }
 
 // value into several buffers in one launch (buffer t holds begin[t+1]-begin[t] floats)

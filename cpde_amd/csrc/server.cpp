@@ -682,6 +682,15 @@ void Server::pass(NetRecord& n, CostRecord& c, int slot, bool& first, const Pass
             require(n.loaded == want, "forward context is no longer current");
         } else {
             activate(n, plan, c.input, c.rows, offset, valid);
+            if (c.kind == 0 && backward && !how.multiplier && c.has_components) {
+                // forward, cost and backward of this chunk in one pass
+                DataRecord& t = data(c.target);
+                call(cpde_epoch_matching(plan, t.values.as<float>(), t.samples, c.target_rows.as<int>(),
+                                         c.weights.as<float>(), c.weight_samples, offset, valid, slot, how.collect,
+                                         first ? 0 : 1));
+                first = false;
+                continue;
+            }
             if (c.has_components) call(cpde_forward(plan));
         }
         if (c.kind == 0) {

@@ -66,6 +66,7 @@ SIGNATURES = {
     'cpde_scale_adjoint': (i32, [vp, vp]),
     'cpde_backward': (i32, [vp, i32]),
     'cpde_inspect_gradients': (i32, [vp]),
+    'cpde_epoch_matching': (i32, [vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32]),
     'cpde_scalars_download': (i32, [vp, i32, vp, i32, vp]),
     'cpde_scalars_download_graph': (i32, [vp, i32, vp, i32, vp, vp, vp]),
     'cpde_rprop': (i32, [vp]),
@@ -309,6 +310,12 @@ class Plan:
         r = np.ascontiguousarray(rows, np.int32)
         check(load().cpde_output(self.handle, dest_buffer.ptr, dest_width, _ptr(r), offset, valid))
 
+    def epoch_matching(self, target, target_width, target_rows, weights, weight_samples, offset, valid, cost_index,
+                       collect=True, accumulate=False):
+        """forward + matching cost + backward of the activated chunk in one pass."""
+        check(load().cpde_epoch_matching(self.handle, target.ptr, target_width, target_rows.ptr, weights.ptr,
+                                         weight_samples, offset, valid, cost_index, int(collect), int(accumulate)))
+
     def matching(self, target, target_width, target_rows, weights, weight_samples, offset, valid, cost_index,
                  collect=True, gradient=True):
         check(load().cpde_cost_matching(self.handle, target.ptr, target_width, target_rows.ptr, weights.ptr,
@@ -348,9 +355,10 @@ class MatchingRun:
     """One matching cost on one plan: the unit of work of the benchmark step
     (forward + cost + weight gradient), driven through the C ABI."""
 
-    def __init__(self, device, workload, chunk=None):
+    def __init__(self, device, workload, chunk=None, one_pass=True):
         wl = workload
         self.device, self.wl = device, wl
+        self.one_pass = one_pass
         self.net = Net(device, wl.neurons, wl.linear, wl.init)
         self.samples = wl.size
         self.width = min(chunk or wl.chunk or wl.size, wl.size)
@@ -375,10 +383,14 @@ class MatchingRun:
             if self._loaded != (offset, valid):
                 self.plan.activate(self.data, self.samples, self.rows, offset, valid)
                 self._loaded = (offset, valid)
-            self.plan.forward()
-            self.plan.matching(self.target, self.samples, self.target_rows, self.weights, 1, offset, valid, 0,
-                               collect, True)
-            self.plan.backward(not first)
+            if self.one_pass:
+                self.plan.epoch_matching(self.target, self.samples, self.target_rows, self.weights, 1, offset, valid, 0,
+                                         collect, not first)
+            else:
+                self.plan.forward()
+                self.plan.matching(self.target, self.samples, self.target_rows, self.weights, 1, offset, valid, 0,
+                                   collect, True)
+                self.plan.backward(not first)
             first = False
 
     def loss(self):

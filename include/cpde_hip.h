@@ -143,6 +143,16 @@ int cpde_costs_begin(cpde_device* dev, int costs);
 int cpde_cost_matching(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
                        const float* weights, int weight_samples, int offset, int valid, int cost_index,
                        int collect, int gradient);
+/* One chunk of Server::pass for an array-matching cost with gradient
+ * (cuda/cpde_server.cu:223-257): cpde_forward, cpde_cost_matching(gradient=1)
+ * and cpde_backward(accumulate) with the same arguments.  The reference runs
+ * them as separate launches; on the network-fused kernels, when the chunk's
+ * workgroups fit on the device together, this is one launch (a point's
+ * matching terms depend on that point alone), the cost's finish and the
+ * weight-gradient contraction.  The input chunk must be activated. */
+int cpde_epoch_matching(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
+                        const float* weights, int weight_samples, int offset, int valid, int cost_index, int collect,
+                        int accumulate);
 /* Sparse linear/quadratic residual cost (cuda/cost_kernels.cuh:37-90); all device. */
 int cpde_cost_polynomial(cpde_plan* plan, const cpde_poly_term* terms, int term_count, const float* coefficients,
                          const float* rhs, const float* weights, int equations, int samples, int offset, int valid,

@@ -86,3 +86,24 @@ def test_chunked_epoch_against_reference_server(device, path):
     for t, grad in enumerate(run.gradients()):
         assert rel_l2(grad, g[f'chunk7_grad{t}']) < 1e-3
     run.close()
+
+
+@pytest.mark.parametrize('name', ['fourier_order6', 'large_reduced'])
+def test_one_pass_epoch_matches_separate_launches(device, path, name):
+    """forward + matching + backward in one launch (cpde_epoch_matching) against
+    the three separate entry points: the same output adjoint and backward, so
+    bit-identical gradients; the loss differs only in its fp64 summation order."""
+    g = load_golden(name)
+    wl = golden_workload(g)
+    results = []
+    for one_pass in (True, False):
+        run = hip.MatchingRun(device, wl, one_pass=one_pass)
+        run.step()
+        device.synchronize()
+        results.append((run.loss(), run.gradients()))
+        run.close()
+    (l1, g1), (l2, g2) = results
+    print(f'[result] one-pass loss {l1!r} separate {l2!r}', flush=True)
+    assert abs(l1 / l2 - 1) < 1e-12
+    for a, b in zip(g1, g2):
+        np.testing.assert_array_equal(a, b)
