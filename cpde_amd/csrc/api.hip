@@ -424,6 +424,7 @@ static void fused_epoch(Plan& p, const MatchArgsHost& match, int cost_index, boo
         HIP_CHECK(hipMalloc(&p.epoch_partials, sizeof(CostStats) * size_t(blocks)));
         p.epoch_capacity = blocks;
     }
+
     std::vector<int> external(L - 1, 0);
     external[0] = external[L - 2] = blocks;
     const GradientPlan g = plan_gradients(p, accumulate, external);
@@ -914,7 +915,11 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
             HIP_CHECK(hipMemcpyAsync(dev->host_summary, summary, sizeof(cpde_graph_summary), hipMemcpyDeviceToHost,
                                      dev->stream));
         HIP_CHECK(hipStreamSynchronize(dev->stream));
-        if (costs && cost_out) std::memcpy(cost_out, dev->host_costs, sizeof(CostStats) * costs);
+        if (costs && cost_out) {
+            std::memcpy(cost_out, dev->host_costs, sizeof(CostStats) * costs);
+            for (int i = 0; i < costs && i < int(dev->slot_fresh.size()); ++i)
+                if (dev->slot_fresh[i]) cost_out[i] = cpde_cost_stats{0.0, INT32_MAX, INT32_MAX};
+        }
         if (layers && gradient_out) std::memcpy(gradient_out, dev->host_grads, sizeof(GradStats) * layers);
         if (summary) *summary_out = *dev->host_summary;
     });

@@ -149,6 +149,14 @@ struct Device {
     void fold_trace();
     // fused modules compiled on this device, by source text
     std::vector<std::pair<std::string, std::shared_ptr<FusedModule>>> fused_modules;
+    // Cost slots cleared by cpde_costs_begin and not yet written: the first
+    // finish into a slot overwrites it instead of accumulating.
+    std::vector<char> slot_fresh;
+    bool take_fresh(int slot) {
+        const bool fresh = slot < int(slot_fresh.size()) && slot_fresh[slot];
+        if (fresh) slot_fresh[slot] = 0;
+        return fresh;
+    }
     void reserve_costs(int costs);
     void reserve_grads(int layers);
 };
@@ -233,6 +241,8 @@ void launch_transpose(Device& d, const float* const* W, float* const* WT, const 
                       int count);
 // Fixed-order sum of `blocks` per-workgroup cost records into cost slot cost_index.
 void launch_finish_cost(Device& d, const CostStats* partials, int blocks, int cost_index);
+// Zero the slots among [0, count) still marked fresh (before something reads them on the device).
+void launch_clear_fresh(Device& d, int count);
 void launch_fill(Device& d, float* p, size_t count, float value);
 void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, int NI, int NO, int R, int columns);
 void launch_wgrad_grouped(Device& d, const WgradArgs& a, double flops);

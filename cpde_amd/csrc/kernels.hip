@@ -683,11 +683,11 @@ __device__ CostStats block_reduce_cost(CostStats v) {
 }
 
 __global__ __launch_bounds__(kCostThreads) void cost_finish_kernel(const CostStats* __restrict__ blocks, int count,
-                                                                   CostStats* __restrict__ total) {
+                                                                   CostStats* __restrict__ total, int overwrite) {
     CostStats v = empty_cost();
     for (int i = threadIdx.x; i < count; i += blockDim.x) v = combine(v, blocks[i]);
     v = block_reduce_cost(v);
-    if (threadIdx.x == 0) *total = combine(*total, v);
+    if (threadIdx.x == 0) *total = overwrite ? v : combine(*total, v);
 }
 
 static int cost_blocks_for(int count) { return std::max(1, std::min(kMaxCostBlocks, (count + kCostThreads - 1) / kCostThreads)); }
@@ -714,7 +714,7 @@ void launch_finish_cost(Device& d, const CostStats* partials, int blocks, int co
         blocks = staged;
     }
     hipLaunchKernelGGL(cost_finish_kernel, 1, kCostThreads, 0, d.stream, partials, blocks,
-                       d.cost_totals + cost_index);
+                       d.cost_totals + cost_index, int(d.take_fresh(cost_index)));
     HIP_CHECK(hipGetLastError());
 }
 
@@ -724,10 +724,20 @@ __global__ void clear_costs_kernel(CostStats* c, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += blockDim.x * gridDim.x) c[i] = empty_cost();
 }
 
+// Workspace::begin (cuda/reduction_kernels.cuh:149-152) without a launch: the
+// slots are marked fresh and the first finish into each overwrites it.
 void launch_costs_begin(Device& d, int costs) {
     d.reserve_costs(costs);
-    hipLaunchKernelGGL(clear_costs_kernel, 1, 256, 0, d.stream, d.cost_totals, costs);
-    HIP_CHECK(hipGetLastError());
+    if (int(d.slot_fresh.size()) < costs) d.slot_fresh.resize(costs, 0);
+    std::fill(d.slot_fresh.begin(), d.slot_fresh.begin() + costs, 1);
+}
+
+void launch_clear_fresh(Device& d, int count) {
+    for (int i = 0; i < count && i < int(d.slot_fresh.size()); ++i)
+        if (d.take_fresh(i)) {
+            hipLaunchKernelGGL(clear_costs_kernel, 1, 64, 0, d.stream, d.cost_totals + i, 1);
+            HIP_CHECK(hipGetLastError());
+        }
 }
 
 // Array-matching squared loss (cuda/cost_kernels.cuh:6-35) on the output stack
@@ -1291,6 +1301,7 @@ __global__ void graph_kernel(const cpde_scalar_node* __restrict__ nodes, int cou
 
 void launch_graph(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,
                   double* adjoints, double* multipliers, int* active, cpde_graph_summary* summary, bool gradient) {
+    launch_clear_fresh(d, leaves);
     hipLaunchKernelGGL(graph_kernel, 1, 1, 0, d.stream, nodes, count, root, d.cost_totals, leaves, values, adjoints,
                        multipliers, active, summary, int(gradient));
     HIP_CHECK(hipGetLastError());
