@@ -40,6 +40,9 @@ METRIC = 'ms/epoch (fwd+cost+wgrad) at order 6, 729 pts; points·derivs/s; % roo
 # The reference's published order-6 figure for this workload shape: 5.65 ms/epoch
 # on an RTX 3090, i.e. 729*28/5.65e-3 points*derivs/s (README.md:63).
 PUBLISHED_POINTS_DERIVS_PER_S = 729 * 28 / 5.65e-3
+# The reference's published ms/epoch of the same 729-point 2->128x4->1 epoch
+# (forward, loss, weight gradient) per derivative order (README.md:57-63).
+PUBLISHED_MS = {0: 0.41, 1: 0.68, 2: 1.10, 3: 1.72, 4: 2.40, 5: 3.59, 6: 5.65}
 PEAK_FP32_MFMA = 157.3e12   # flop/s, dense
 PEAK_HBM = 8.0e12           # bytes/s
 MFMA_KINDS = {'gemm_forward', 'gemm_transposed', 'gemm_wgrad', 'fused_forward', 'fused_backward', 'network_forward',
@@ -72,8 +75,7 @@ class Spec:
 
 
 WORKLOADS = {
-    'fourier_fit_order6': Spec(lambda: workloads.fourier_fit(6), 500, 50, 20, (20, 100, 7)),
-    'fourier_fit_order2': Spec(lambda: workloads.fourier_fit(2), 500, 50, 20, (20, 100, 7)),
+    **{f'fourier_fit_order{k}': Spec(lambda k=k: workloads.fourier_fit(k), 500, 50, 20, (20, 100, 7)) for k in range(7)},
     'poisson_disk_order2': Spec(lambda: workloads.PoissonWorkload(), 500, 50, 20, None, server=True),
     'fourier_3d_order4': Spec(lambda: workloads.fourier_3d(), 30, 3, 3, (3, 10, 3)),
     'fourier_large_order6': Spec(lambda: workloads.fourier_large(), 10, 2, 2, (2, 3, 3)),
@@ -127,6 +129,14 @@ def roofline(report, workload):
             'work_per_launch': work / launches}
 
 
+def published_ratio(wl, ms):
+    """Published reference ms/epoch over ours for the 729-point Fourier fits."""
+    for order, ref in PUBLISHED_MS.items():
+        if wl.name == f'fourier_fit_order{order}' and wl.size == 729:
+            return {'reference_ms': ref, 'speedup': round(ref / ms, 2)}
+    return None
+
+
 def server_op90(wl, warm, iterations, batches):
     """The reference's own timing scope through the protocol server (op 90:
     forward + cost + weight gradient, no optimizer; C++ host, no Python in the
@@ -140,7 +150,7 @@ def server_op90(wl, warm, iterations, batches):
     wall, gpu = float(np.median(r['wall_ms'])), float(np.median(r['gpu_ms']))
     return {'ms_per_epoch_wall': round(wall, 5), 'ms_per_epoch_device': round(gpu, 5),
             'points_derivs_per_s': round(wl.size * wl.rows / (wall / 1e3), 1),
-            'vs_published_5.65ms': round(5.65 / wall, 2) if wl.name == 'fourier_fit_order6' else None,
+            'vs_published': published_ratio(wl, wall),
             'loss': r['loss'], 'scope': f'op 90: {batches} batches x {iterations} epochs after {warm} warm-ups'}
 
 
