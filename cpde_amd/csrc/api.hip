@@ -737,8 +737,12 @@ int cpde_plan_destroy(cpde_plan* plan) {
 int cpde_plan_stack(cpde_plan* plan, int layer, int kind, float** device_ptr) {
     return guarded([&] {
         Net& n = *plan->net;
-        require(layer >= 0 && layer < n.layers && kind >= 0 && kind <= 2, "invalid stack");
-        float* p = kind == 0 ? n.z[layer] : kind == 1 ? n.y[layer] : n.g[layer];
+        require(layer >= 0 && layer < n.layers && kind >= 0 && kind <= 3, "invalid stack");
+        // network-fused plans keep u (the jet of sigma'(z)) where the others keep z
+        const bool keeps_u = plan->fused && plan->network && !n.linear[layer];
+        require(!(kind == 0 && keeps_u), "this plan keeps u, not z, for a sigmoid layer (stack kind 3)");
+        require(!(kind == 3 && !keeps_u), "u is kept only by network-fused plans for sigmoid layers");
+        float* p = kind == 0 || kind == 3 ? n.z[layer] : kind == 1 ? n.y[layer] : n.g[layer];
         require(p != nullptr, "stack not present for this layer");
         *device_ptr = p;
     });

@@ -77,12 +77,13 @@ void emit_sigma(std::ostringstream& o, int highest) {
         o << "    const float s7 = (5.0f * s1) * (0.2f - (8.4f * s1) * (3.0f - 4.0f * (5.0f * s1 + 5.0f * s3)));\n";
 }
 
-// sum_m s_{m+shift} M_m for row r, M_m = sum_terms c * prod(block rows).
+// sum_m s_{m+shift} M_m for row r, M_m = sum_terms c * prod(block rows).  With
+// `prime`, also sum_m s_{m+1} M_m (the row of the jet of sigma') into *prime.
 std::string emit_partition_sum(std::ostringstream& o, Products& P, const Tables& t, int r, int shift,
-                               const std::string& name) {
+                               const std::string& name, std::string* prime = nullptr) {
     int pos = t.fwd_offset[r];
     const int k = t.words[pos++];
-    std::string acc;
+    std::string acc, pacc;
     for (int m = 1; m <= k; ++m) {
         const int count = t.words[pos++];
         std::string M = "0.0f";
@@ -105,12 +106,25 @@ std::string emit_partition_sum(std::ostringstream& o, Products& P, const Tables&
                 M = tmp;
             }
         }
+        if (prime) {  // M is used twice
+            const std::string tmp = name + "_M" + std::to_string(m);
+            o << "    const float " << tmp << " = " << M << ";\n";
+            M = tmp;
+        }
         const std::string s = "s" + std::to_string(m + shift);
         acc = m == 1 ? s + " * " + M : "fmaf(" + s + ", " + M + ", " + acc + ")";
         const std::string tmp = name + "_a" + std::to_string(m);
         o << "    const float " << tmp << " = " << acc << ";\n";
         acc = tmp;
+        if (prime) {
+            const std::string sp = "s" + std::to_string(m + shift + 1);
+            pacc = m == 1 ? sp + " * " + M : "fmaf(" + sp + ", " + M + ", " + pacc + ")";
+            const std::string ptmp = name + "_u" + std::to_string(m);
+            o << "    const float " << ptmp << " = " << pacc << ";\n";
+            pacc = ptmp;
+        }
     }
+    if (prime) *prime = pacc;
     return acc;
 }
 
@@ -159,6 +173,24 @@ void emit_forward(std::ostringstream& o, const Tables& t, const std::string& nam
     o << "}\n";
 }
 
+// The same rows of y and of u, the jet of sigma'(z) (u[0] = sigma'(z0)): the
+// partition sums M_m of a row serve both, y = sum s_m M_m and u = sum s_{m+1} M_m.
+void emit_forward_prime(std::ostringstream& o, const Tables& t, const std::string& name,
+                        const std::vector<char>& owned) {
+    o << "__device__ __forceinline__ void " << name
+      << "(const float* __restrict__ z, float* __restrict__ y, float* __restrict__ u) {\n";
+    emit_sigma(o, t.max_order + 1);
+    if (owned[0]) o << "    y[0] = 1.0f / (1.0f + expf(-z[0]));\n    u[0] = s1;\n";
+    Products P{o, {}};
+    for (int r = 1; r < t.rows; ++r) {
+        if (!owned[r]) continue;
+        std::string prime;
+        const std::string v = emit_partition_sum(o, P, t, r, 0, "f" + std::to_string(r), &prime);
+        o << "    y[" << r << "] = " << v << ";\n    u[" << r << "] = " << prime << ";\n";
+    }
+    o << "}\n";
+}
+
 // compose_adjoint outputs gz[i] where owned[i]; the others are left untouched.
 void emit_adjoint(std::ostringstream& o, const Tables& t, const std::string& name, const std::vector<char>& owned) {
     o << "__device__ __forceinline__ void " << name << "(const float* __restrict__ z, const float* __restrict__ gy,"
@@ -193,17 +225,47 @@ void emit_adjoint(std::ostringstream& o, const Tables& t, const std::string& nam
     o << "}\n";
 }
 
+// The adjoint from the jet of sigma' kept by the forward:
+// gz_i = u_0 gy_i + sum over pairs C(alpha_j, alpha_i) gy_j u_(alpha_j - alpha_i)
+// (back_step, cuda/derivative_kernels_v4.cu:349-380, with DPlus = u).
+void emit_adjoint_prime(std::ostringstream& o, const Tables& t, const std::string& name,
+                        const std::vector<char>& owned) {
+    o << "__device__ __forceinline__ void " << name << "(const float* __restrict__ u, const float* __restrict__ gy,"
+         " float* __restrict__ gz) {\n";
+    for (int i = 0; i < t.rows; ++i) {
+        if (!owned[i]) continue;
+        int pos = t.pair_offset[i];
+        const int count = t.words[pos++];
+        o << "    { float acc = u[0] * gy[" << i << "];\n";
+        for (int q = 0; q < count; ++q, pos += 3) {
+            const int j = t.words[pos], dn = t.words[pos + 1];
+            require(dn > 0, "adjoint pair refers to the value row");
+            const float c = word_float(t.words[pos + 2]);
+            if (c == 1.0f)
+                o << "      acc = fmaf(gy[" << j << "], u[" << dn << "], acc);\n";
+            else
+                o << "      acc = fmaf(" << flit(c) << " * gy[" << j << "], u[" << dn << "], acc);\n";
+        }
+        o << "      gz[" << i << "] = acc; }\n";
+    }
+    o << "}\n";
+}
+
 }  // namespace
 
-// compose_forward / compose_adjoint for all rows, and for each G in `splits`
-// the G partial versions compose_forward_G<G>_<g> / compose_adjoint_G<G>_<g>
-// plus the row-to-group tables kForwardGroup<G>[R] / kAdjointGroup<G>[R].
+// compose_forward / compose_adjoint (from z) and compose_forward_prime /
+// compose_adjoint_prime (keeping and contracting the jet of sigma') for all
+// rows, and for each G in `splits` the G partial versions of the latter,
+// compose_forward_G<G>_<g> / compose_adjoint_G<G>_<g>, plus the row-to-group
+// tables kForwardGroup<G>[R] / kAdjointGroup<G>[R].
 std::string compose_source(const Tables& t, const std::vector<int>& splits) {
     std::ostringstream o;
     o << "#define CPDE_R " << t.rows << "\n";
     const std::vector<char> all(t.rows, 1);
     emit_forward(o, t, "compose_forward", all);
     emit_adjoint(o, t, "compose_adjoint", all);
+    emit_forward_prime(o, t, "compose_forward_prime", all);
+    emit_adjoint_prime(o, t, "compose_adjoint_prime", all);
     std::vector<int> fcost(t.rows), acost(t.rows);
     for (int r = 0; r < t.rows; ++r) {
         fcost[r] = forward_terms(t, r) + 1;
@@ -223,8 +285,8 @@ std::string compose_source(const Tables& t, const std::vector<int>& splits) {
                 for (int r = 0; r < t.rows; ++r) owned[r] = grp[r] == g;
                 const std::string name = std::string(which ? "compose_adjoint_G" : "compose_forward_G") +
                                          std::to_string(G) + "_" + std::to_string(g);
-                if (which) emit_adjoint(o, t, name, owned);
-                else emit_forward(o, t, name, owned);
+                if (which) emit_adjoint_prime(o, t, name, owned);
+                else emit_forward_prime(o, t, name, owned);
             }
         }
     }

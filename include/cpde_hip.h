@@ -120,7 +120,10 @@ int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, i
                      cpde_plan** out);
 int cpde_plan_destroy(cpde_plan* plan);
 /* Device pointer of a plan's stack: kind 0 = z (layer 0: the input), 1 = y
- * (sigmoid activations), 2 = adjoint dE/dz.  Layout [point][row][neuron]. */
+ * (sigmoid activations), 2 = adjoint dE/dz, 3 = u, the jet of sigma'(z) (the
+ * reference's DPlus rows, cuda/derivative_kernels_v4.cu:12-380, with u[0] =
+ * sigma'(z0)).  Network-fused plans keep u instead of z for sigmoid layers
+ * (their adjoint needs only u); other plans keep z.  Layout [point][row][neuron]. */
 int cpde_plan_stack(cpde_plan* plan, int layer, int kind, float** device_ptr);
 
 /* ---- hot path ---------------------------------------------------------------------- */

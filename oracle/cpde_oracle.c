@@ -142,6 +142,22 @@ int orc_compose(int R, int V, const int* table, long count, const float* z, floa
     return 0;
 }
 
+/* Jet of sigma'(z): u[0] = sigma'(z0), u[r] = d^{alpha_r} sigma'(z(x)) -- the
+ * reference's DPlus rows (cuda/derivative_kernels_v4.cu:12-380, the shift-1
+ * partition sums), here for every row. */
+int orc_compose_prime(int R, int V, const int* table, long count, const float* z, float* u) {
+    if (check_schema(R, V, table)) return -1;
+    row_parts_t* rp = build_parts(R, V, table);
+    for (long e = 0; e < count; ++e) {
+        float s[8];
+        sigma_derivs(z[e], s);
+        u[e] = s[1];
+        for (int r = 1; r < R; ++r) u[(long)r * count + e] = partition_sum(&rp[r], z, count, e, s, 1);
+    }
+    free(rp);
+    return 0;
+}
+
 /* back_step (cuda/derivative_kernels_v4.cu:349-380): ascending i, in place, so each
  * g_j (j>i) is still the incoming dE/dy_j.  DPlus depends only on the difference
  * row, so it is evaluated once per row and element (identical floats). */

@@ -8,6 +8,7 @@
  * It restates the reference's arithmetic in plain C, fp32 like the reference:
  *   - derivative schema tables          cuda/cpde_engine.cuh:391-498
  *   - forward sigmoid composition        cuda/derivative_kernels_v4.cu:382-745
+ *   - sigma' composition (DPlus rows)    cuda/derivative_kernels_v4.cu:12-380
  *   - adjoint composition (back_step)    cuda/derivative_kernels_v4.cu:12-380
  *   - serial column-major BLAS order     cpu/include/cublas_v2.h:34-40,51-53,64-71
  *   - network forward / backward         cuda/cpde_engine.cuh:889-913,947-991
@@ -37,6 +38,8 @@ int orc_pair_tables(int R, int V, const int* table, int* dtab, int* crs);
 
 /* y[r][e] = d^{alpha_r} sigma(z)[e] for count independent elements. */
 int orc_compose(int R, int V, const int* table, long count, const float* z, float* y);
+/* u[r][e] = d^{alpha_r} sigma'(z)[e]: the jet of sigma' the adjoint contracts with. */
+int orc_compose_prime(int R, int V, const int* table, long count, const float* z, float* u);
 /* In place: g holds dE/dy on entry and dE/dz on exit. */
 int orc_compose_adjoint(int R, int V, const int* table, long count, const float* z, float* g);
 

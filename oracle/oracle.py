@@ -38,6 +38,7 @@ def _load():
     lib.orc_pair_tables.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, _i32p, _i32p]
     lib.orc_compose.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, ctypes.c_long, _f32p, _f32p]
     lib.orc_compose_adjoint.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, ctypes.c_long, _f32p, _f32p]
+    lib.orc_compose_prime.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, ctypes.c_long, _f32p, _f32p]
     lib.orc_gemm.argtypes = [ctypes.c_int] * 5 + [ctypes.c_float, _f32p, ctypes.c_int, _f32p, ctypes.c_int,
                                                   ctypes.c_float, _f32p, ctypes.c_int]
     lib.orc_matching.restype = ctypes.c_double
@@ -91,6 +92,16 @@ def compose(table, z):
     if lib().orc_compose(t.shape[0], t.shape[1] - 1, t, z.shape[1], z, y):
         raise ValueError('invalid schema')
     return y
+
+
+def compose_prime(table, z):
+    """z: (R, count) float32 -> u (R, count): the jet of sigma'(z)."""
+    t = _table(table)
+    z = np.ascontiguousarray(z, np.float32)
+    u = np.zeros_like(z)
+    if lib().orc_compose_prime(t.shape[0], t.shape[1] - 1, t, z.shape[1], z, u):
+        raise ValueError('invalid schema')
+    return u
 
 
 def compose_adjoint(table, z, gy):

@@ -87,6 +87,15 @@ def compose_stack(schema, z):
     return j.to_stack(schema, j.sigmoid(j.from_stack(schema, z)))
 
 
+def compose_prime_stack(schema, z):
+    """d^alpha sigma'(z(x)) for every schema row: sigma' = sigma (1 - sigma) as series."""
+    schema = np.asarray(schema)
+    V, K = schema.shape[1] - 1, int(schema[:, 0].max())
+    j = Jet(V, K, np.complex128 if np.iscomplexobj(z) else np.float64)
+    y = j.sigmoid(j.from_stack(schema, z))
+    return j.to_stack(schema, y - j.mul(y, y))
+
+
 def compose_jacobian(schema, z, h=1e-30):
     """J[i, j] = d y_i / d z_j by complex step (exact to rounding)."""
     R = len(schema)

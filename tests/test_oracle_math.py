@@ -4,6 +4,8 @@
   composition (tests/jet.py), for 1-3 variables through order 6 and a
   non-full (Poisson) closure; the single-variable rows also against the closed
   forms of sigma^(k);
+* the jet of sigma'(z): against sigma(1-sigma) as a series and against
+  d y / d z_0 from the complex-step Jacobian;
 * adjoint: against J^T g with J the complex-step Jacobian of the jet
   composition -- a dropped pair, a wrong binomial or a transposed index fails;
 * products: the serial column-major SGEMM against a float64 matmul;
@@ -18,7 +20,7 @@ import pytest
 
 import oracle
 from cpde_amd import workloads as W
-from jet import compose_jacobian, compose_stack
+from jet import compose_jacobian, compose_prime_stack, compose_stack
 
 SCHEMAS = {
     '1var_order6': W.full_schema(1, 6),
@@ -47,6 +49,22 @@ def test_composition_against_taylor_jet(name):
         scale = np.maximum(np.abs(want), np.sqrt(np.mean(want ** 2)))
         err = np.max(np.abs(y[:, e] - want) / scale)
         assert err < 2e-5, (name, e, err)
+
+
+@pytest.mark.parametrize('name', list(SCHEMAS))
+def test_sigma_prime_jet(name):
+    """The jet of sigma'(z) (what the adjoint contracts with) against sigma(1-sigma)
+    composed as a float64 series, and against the first column of the
+    complex-step Jacobian of the composition (d y_alpha / d z_0)."""
+    schema = SCHEMAS[name]
+    z = random_stacks(schema, 4, 5)
+    u = oracle.compose_prime(schema, z)
+    for e in range(z.shape[1]):
+        zz = z[:, e].astype(np.float64)
+        for want in (compose_prime_stack(schema, zz), compose_jacobian(schema, zz)[:, 0]):
+            scale = np.maximum(np.abs(want), np.sqrt(np.mean(want ** 2)))
+            err = np.max(np.abs(u[:, e] - want) / scale)
+            assert err < 2e-5, (name, e, err)
 
 
 def test_sigma_closed_forms():
