@@ -208,7 +208,9 @@ static FusedTuning tuning(int rows, int width, int compute_units) {
     }
     t.points_per_block = std::max(1, env_int("CPDE_FUSED_POINTS", t.points_per_block));
     t.net_points_per_block = std::max(1, env_int("CPDE_NET_POINTS", npb));
-    t.max_split = std::max(1, env_int("CPDE_NET_SPLIT", t.max_split));
+    // a composition split over lanes pays off while a point's rows fit one
+    // matrix-core tile; with two tiles (R > 32) whole compositions per lane are faster
+    t.max_split = std::max(1, env_int("CPDE_NET_SPLIT", rows > 32 ? 1 : t.max_split));
     t.max_split_adjoint = std::max(1, env_int("CPDE_NET_SPLIT_ADJOINT", t.max_split_adjoint));
     t.forward_blocks = std::max(1, env_int("CPDE_NET_FWD_OCC", t.forward_blocks));
     t.backward_blocks = std::max(1, env_int("CPDE_NET_BWD_OCC", t.backward_blocks));
