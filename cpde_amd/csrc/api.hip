@@ -323,8 +323,9 @@ struct GradientPlan {
 };
 
 // Weight-gradient tiles per compute unit the split-K decomposition aims for
-// (CPDE_WGRAD_OCC; two keep a second wave on every SIMD to cover stalls).
-static double wgrad_blocks_per_cu() { return std::max(1, env_int("CPDE_WGRAD_OCC", 1)); }
+// (CPDE_WGRAD_OCC; two, the kernel's occupancy, keep a second wave on every
+// SIMD to cover the other's loads and barriers).
+static int wgrad_blocks_per_cu() { return std::max(1, env_int("CPDE_WGRAD_OCC", 2)); }
 
 static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<int>& external_splits) {
     Net& n = *p.net;
@@ -338,9 +339,11 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
         const int T0 = tile_of(t);
         return ((n.neurons[t + 1] + T0 - 1) / T0) * ((n.neurons[t] + T0 - 1) / T0);
     };
-    double total_tiles = 0;
+    int total_tiles = 0;
     for (int t = 0; t < T; ++t)
         if (!thin(t) && !external_splits[t]) total_tiles += tiles_of(t);
+    // whole waves of tiles: a partial last wave would run alone for a whole split
+    const int tile_splits = std::max(1, wgrad_blocks_per_cu() * d.compute_units / std::max(1, total_tiles));
     g.wa.K = K;
     g.wa.R = p.rows;
     g.wa.block_begin[0] = 0;
@@ -354,8 +357,8 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
         int s = external_splits[t];
         if (!s) {
             const int tiles = thin(t) ? 1 : tiles_of(t);
-            s = thin(t) ? 2 * d.compute_units : int(wgrad_blocks_per_cu() * d.compute_units / total_tiles + 0.5);
-            s = std::max(1, std::min(s, std::max(1, K / 64)));
+            s = thin(t) ? 2 * d.compute_units : tile_splits;
+            s = std::max(1, std::min(s, std::max(1, K / kWgradChunk)));
             int chunk = (K + s - 1) / s;
             chunk = (chunk + kWgradChunk - 1) / kWgradChunk * kWgradChunk;
             s = (K + chunk - 1) / chunk;

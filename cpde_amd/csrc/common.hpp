@@ -36,7 +36,7 @@ constexpr int kMaxRows = 255;      // row indices are stored in 8 bits in the te
 constexpr int kMaxTransitions = 32;  // per fused optimizer launch
 constexpr int kCostThreads = 256;
 constexpr int kMaxCostBlocks = 1024;
-constexpr int kWgradChunk = 64;  // columns per LDS chunk of the weight-gradient tiles
+constexpr int kWgradChunk = 32;  // columns per LDS chunk of the weight-gradient tiles
 
 // Device-side mirrors of the public reduction structs.
 struct CostStats {

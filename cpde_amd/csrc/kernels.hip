@@ -310,7 +310,7 @@ void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, 
 // value-row columns), reduced in split order by reduce_grouped_kernel so the
 // result does not depend on scheduling.  Two block roles:
 //  * matrix-core tiles (M, N > 16): a 128x128 (or 64x64) tile, K staged
-//    through LDS in chunks of 64 columns (double-buffered, the next chunk's
+//    through LDS in chunks of 32 columns (double-buffered, the next chunk's
 //    global loads in flight during the current chunk's MFMAs);
 //  * thin transitions (M or N <= 16: the input and output layers): lanes
 //    stride the wide side and accumulate the narrow side in registers.
@@ -506,12 +506,24 @@ __device__ __forceinline__ void wgrad_thin(const WgradArgs& a, int t, int split,
     }
 }
 
-__global__ __launch_bounds__(256) void wgrad_grouped_kernel(WgradArgs a) {
+// Workgroups go to the eight XCDs round-robin (workgroup b on XCD b % 8), each
+// XCD with its own L2.  This renumbering gives every XCD a contiguous range of
+// work items, so that the tiles of one split, which read the same rows of G
+// or Y, run under one L2.  It is a permutation of [0, n) for any n.
+__device__ __forceinline__ int xcd_grouped(int b, int n) {
+    const int x = b & 7, q = b >> 3, per = (n + 7) >> 3, full = (n & 7) ? (n & 7) : 8;
+    return x < full ? x * per + q : full * per + (x - full) * (per - 1) + q;
+}
+
+// Two workgroups per CU (LDS 2 x 67.6 KB): one's chunk loads and barriers
+// overlap the other's MFMAs.
+__global__ __launch_bounds__(256, 2) void wgrad_grouped_kernel(WgradArgs a) {
     __shared__ __attribute__((aligned(16))) float lds[kWgLds];
     static_assert(256 * 17 <= kWgLds, "thin-transition scratch exceeds the shared LDS");
+    const int b = xcd_grouped(int(blockIdx.x), int(gridDim.x));
     int t = 0;
-    while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
-    const int local = int(blockIdx.x) - a.block_begin[t];
+    while (t + 1 < a.transitions && b >= a.block_begin[t + 1]) ++t;
+    const int local = b - a.block_begin[t];
     if (a.M[t] <= 16 || a.N[t] <= 16) wgrad_thin(a, t, local, lds);
     else if (a.tile[t] == 64) wgrad_tile<64>(a, t, local, lds);
     else wgrad_tile<128>(a, t, local, lds);
