@@ -283,6 +283,7 @@ static void fused_forward(Plan& p) {
         TraceScope trace(d, kTraceNetworkForward, flops);
         launch_module(d, fm.network_forward, unsigned((width + fm.net_points_per_block - 1) / fm.net_points_per_block),
                       1, args);
+        n.wt_current = true;  // written by the forward's side job
         return;
     }
     {
@@ -438,9 +439,10 @@ static void fused_epoch(Plan& p, const MatchArgsHost& match, int cost_index, boo
     a.partial_out = n.partials + g.offset[L - 2];
     MatchArgsHost m = match;
     m.partials = p.epoch_partials;
-    {
+    if (!n.wt_current) {
         // the backward half reads the row-major weight copies of every hidden
-        // transition, which no workgroup of the same launch may still be writing
+        // transition, which no workgroup of the same launch may still be
+        // writing; RPROP and Adam keep them current between epochs
         std::vector<const float*> W;
         std::vector<float*> WT;
         std::vector<int> ni, no;
@@ -451,6 +453,7 @@ static void fused_epoch(Plan& p, const MatchArgsHost& match, int cost_index, boo
             no.push_back(n.neurons[t + 1]);
         }
         launch_transpose(d, W.data(), WT.data(), ni.data(), no.data(), int(W.size()));
+        n.wt_current = true;
     }
     void* args[] = {&a, &m, &width};
     double flops = 0;
@@ -677,6 +680,7 @@ int cpde_net_destroy(cpde_net* net) {
 int cpde_net_state(cpde_net* net, int transition, int buffer, float** device_ptr, int* count) {
     return guarded([&] {
         require(transition >= 0 && transition < net->layers - 1 && buffer >= 0 && buffer < 4, "invalid state buffer");
+        if (buffer == 0) net->wt_current = false;  // the caller may write the weights
         if (device_ptr) *device_ptr = net->state[buffer][transition];
         if (count) *count = net->param_count(transition);
     });

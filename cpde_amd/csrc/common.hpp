@@ -77,8 +77,12 @@ struct Net {
     std::vector<float*> state[4];
     std::vector<int> active;  // 1 or 2 per transition
     // Per transition: n_t x n_{t+1} row-major copy of the weights (without the
-    // bias), refreshed by every network-fused forward for the backward's products.
+    // bias) for the backward's products.  Written by every network-fused
+    // forward and by the optimizer launches; the one-pass epoch transposes
+    // first only when wt_current is false (a new network, or the weights'
+    // device pointer handed out by cpde_net_state).
     std::vector<float*> wt;
+    bool wt_current = false;
     // Stack arena shared by every plan of the network (contexts are views,
     // the reference's layer banks, cuda/cpde_engine.cuh:661-693).
     std::vector<float*> z, y, g;      // per layer

@@ -1106,9 +1106,17 @@ struct OptimizerArgs {
     float* S[kMaxTransitions];   // RPROP step / Adam first moment
     float* Ga[kMaxTransitions];  // active gradient
     float* Gi[kMaxTransitions];  // inactive gradient / Adam second moment
+    float* WT[kMaxTransitions];  // row-major copy of the weights, kept current by RPROP and Adam
+    int NO[kMaxTransitions], NI[kMaxTransitions];
     int begin[kMaxTransitions + 1];
     int transitions;
 };
+
+// Entry j = o + NO*i of a weight block into its row-major copy (bias column i = NI excluded).
+__device__ __forceinline__ void copy_transposed(const OptimizerArgs& a, int t, int j, float w) {
+    const int i = j / a.NO[t], o = j - i * a.NO[t];
+    if (i < a.NI[t]) a.WT[t][i + a.NI[t] * o] = w;
+}
 
 __device__ __forceinline__ int find_transition(const OptimizerArgs& a, int i) {
     int t = 0;
@@ -1142,6 +1150,7 @@ __global__ void rprop_kernel(OptimizerArgs a) {
             }
         }
         *step = s;
+        copy_transposed(a, t, j, *W);
     }
 }
 
@@ -1159,6 +1168,7 @@ __global__ void adam_kernel(OptimizerArgs a, float lr, float beta1, float beta2,
         const float mh = m / (1 - beta1t), vh = v / (1 - beta2t);
         const float nW = float(double(a.W[t][j]) - double(lr * mh) / (double(sqrtf(vh)) + 1e-8));
         if (fabsf(nW) <= 20.0f) a.W[t][j] = nW;
+        copy_transposed(a, t, j, a.W[t][j]);
     }
 }
 
@@ -1189,6 +1199,9 @@ static void for_transition_groups(Net& net, F launch) {
             a.S[k] = net.state[3][t];
             a.Ga[k] = net.state[act][t];
             a.Gi[k] = net.state[inact][t];
+            a.WT[k] = net.wt[t];
+            a.NO[k] = net.neurons[t + 1];
+            a.NI[k] = net.neurons[t];
             a.begin[k + 1] = a.begin[k] + net.param_count(t);
         }
         const int blocks = std::max(1, std::min(1024, (a.begin[a.transitions] + 255) / 256));
@@ -1203,6 +1216,7 @@ void launch_rprop(Device& d, Net& net) {
         HIP_CHECK(hipGetLastError());
     });
     for (auto& act : net.active) act = act == 1 ? 2 : 1;
+    net.wt_current = true;
 }
 
 void launch_adam(Device& d, Net& net, int step, float lr) {
@@ -1212,6 +1226,7 @@ void launch_adam(Device& d, Net& net, int step, float lr) {
         hipLaunchKernelGGL(adam_kernel, blocks, 256, 0, d.stream, a, lr, b1, b2, b1t, b2t);
         HIP_CHECK(hipGetLastError());
     });
+    net.wt_current = true;
 }
 
 void launch_set_steps(Device& d, Net& net, float value) {

@@ -102,7 +102,11 @@ int cpde_net_create(cpde_device* dev, int layers, const int* neurons, const int*
                     const float* const* initial, cpde_net** out);
 int cpde_net_destroy(cpde_net* net);
 /* Device pointer and element count of state buffer b of transition t:
- * 0 weights, 1 and 2 the gradient ping-pong pair, 3 RPROP step / Adam first moment. */
+ * 0 weights, 1 and 2 the gradient ping-pong pair, 3 RPROP step / Adam first moment.
+ * Weights written through a buffer-0 pointer are seen by the next library call
+ * on the network: write them before that call, or ask for the pointer again
+ * after writing (the library keeps a transposed copy of the weights, which it
+ * rebuilds after the pointer has been handed out). */
 int cpde_net_state(cpde_net* net, int transition, int buffer, float** device_ptr, int* count);
 /* The active gradient buffer (1 or 2) of a transition (weights::act_grad). */
 int cpde_net_active(cpde_net* net, int transition);

@@ -107,3 +107,40 @@ def test_one_pass_epoch_matches_separate_launches(device, path, name):
     assert abs(l1 / l2 - 1) < 1e-12
     for a, b in zip(g1, g2):
         np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize('optimizer', ['rprop', 'adam'])
+def test_one_pass_epochs_across_updates(device, optimizer):
+    """Four epochs with an optimizer update after each: the one-pass epoch reads
+    the row-major weight copy that RPROP and Adam keep current, and must track
+    the separate launches (which transpose in the forward) bit for bit.  Then
+    weights written through the state pointer must be seen by the next epoch."""
+    g = load_golden('fourier_order6')
+    wl = golden_workload(g)
+    runs = [hip.MatchingRun(device, wl, one_pass=one_pass) for one_pass in (True, False)]
+    for epoch in range(4):
+        for run in runs:
+            run.step()
+            if optimizer == 'rprop':
+                run.net.rprop()
+            else:
+                run.net.adam(epoch + 1, 0.01)
+        device.synchronize()
+        for t in range(len(wl.neurons) - 1):
+            np.testing.assert_array_equal(runs[0].net.state(t, 0), runs[1].net.state(t, 0))
+    print(f'[case] {optimizer}: 4 epochs, weights identical', flush=True)
+    fresh = wl.init
+    for run in runs:
+        for t, w in enumerate(fresh):
+            run.net.set_state(t, 0, w)
+        run.step()
+    device.synchronize()
+    ref = hip.MatchingRun(device, wl, one_pass=True)
+    ref.step()
+    device.synchronize()
+    for run in runs:
+        assert abs(run.loss() / ref.loss() - 1) < 1e-12
+        for a, b in zip(run.gradients(), ref.gradients()):
+            np.testing.assert_array_equal(a, b)
+    for run in runs + [ref]:
+        run.close()
