@@ -433,7 +433,7 @@ static void fused_epoch(Plan& p, const MatchArgsHost& match, int cost_index, boo
 
     std::vector<int> external(L - 1, 0);
     external[0] = external[L - 2] = blocks;
-    const GradientPlan g = plan_gradients(p, accumulate, external);
+    GradientPlan g = plan_gradients(p, accumulate, external);
     NetArgsHost a = net_args(n);
     a.partial_in = n.partials + g.offset[0];
     a.partial_out = n.partials + g.offset[L - 2];
@@ -463,7 +463,14 @@ static void fused_epoch(Plan& p, const MatchArgsHost& match, int cost_index, boo
         TraceScope trace(d, kTraceNetworkEpoch, flops);
         launch_module(d, fm.network_epoch, unsigned(blocks), 1, args);
     }
-    launch_finish_cost(d, p.epoch_partials, blocks, cost_index);
+    if (blocks <= kMaxCostBlocks) {  // the cost's finish rides in the gradient reduction launch
+        g.ra.cost_partials = p.epoch_partials;
+        g.ra.cost_total = d.cost_totals + cost_index;
+        g.ra.cost_count = blocks;
+        g.ra.cost_overwrite = d.take_fresh(cost_index) ? 1 : 0;
+    } else {
+        launch_finish_cost(d, p.epoch_partials, blocks, cost_index);
+    }
     run_gradients(d, g);
 }
 

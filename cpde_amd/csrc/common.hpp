@@ -183,6 +183,11 @@ struct ReduceArgs {
     int block_begin[kMaxTransitions + 1];  // first block of each transition
     int split_minor[kMaxTransitions];      // partial layout: 0 [split][entry], 1 [entry][split]
     int transitions, accumulate;
+    // optional: one more block finishes a cost from its per-block records
+    // (cost_count > 0, at most kMaxCostBlocks), as launch_finish_cost would
+    const CostStats* cost_partials;
+    CostStats* cost_total;
+    int cost_count, cost_overwrite;
 };
 // Blocks reduce_grouped_kernel uses for a transition of `count` entries.
 inline int reduce_blocks(int count, bool split_minor) { return split_minor ? (count + 3) / 4 : (count + 63) / 64; }

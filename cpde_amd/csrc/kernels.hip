@@ -537,8 +537,15 @@ __global__ __launch_bounds__(256, 2) void wgrad_grouped_kernel(WgradArgs a) {
 // l + 64u (+ 256i) into running sum u (four, combined in a fixed order), then a
 // fixed shuffle tree.  Either way the summation order is fixed whatever the
 // scheduling.
+__device__ void finish_cost_records(const CostStats* __restrict__ records, int count, CostStats* __restrict__ total,
+                                    int overwrite);
+
 __global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
     __shared__ float part[4][64];
+    if (a.cost_count && int(blockIdx.x) == a.block_begin[a.transitions]) {
+        finish_cost_records(a.cost_partials, a.cost_count, a.cost_total, a.cost_overwrite);
+        return;
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int t = 0;
     while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
@@ -599,8 +606,10 @@ void launch_reduce_grouped(Device& d, const ReduceArgs& a) {
     double bytes = 0;
     for (int t = 0; t < a.transitions; ++t)
         bytes += 4.0 * (a.begin[t + 1] - a.begin[t]) * (a.splits[t] + (a.accumulate ? 2 : 1));
+    if (a.cost_count) bytes += double(sizeof(CostStats)) * (a.cost_count + 2);
     TraceScope trace(d, kTraceSplitReduce, bytes);
-    hipLaunchKernelGGL(reduce_grouped_kernel, a.block_begin[a.transitions], 256, 0, d.stream, a);
+    hipLaunchKernelGGL(reduce_grouped_kernel, a.block_begin[a.transitions] + (a.cost_count ? 1 : 0), 256, 0, d.stream,
+                       a);
     HIP_CHECK(hipGetLastError());
 }
 
@@ -694,12 +703,19 @@ __device__ CostStats block_reduce_cost(CostStats v) {
     return r;
 }
 
-__global__ __launch_bounds__(kCostThreads) void cost_finish_kernel(const CostStats* __restrict__ blocks, int count,
-                                                                   CostStats* __restrict__ total, int overwrite) {
+// One block of kCostThreads lanes: lane l combines records l, l + 256, ... in
+// order, then the fixed block reduction; the result overwrites or joins *total.
+__device__ void finish_cost_records(const CostStats* __restrict__ records, int count, CostStats* __restrict__ total,
+                                    int overwrite) {
     CostStats v = empty_cost();
-    for (int i = threadIdx.x; i < count; i += blockDim.x) v = combine(v, blocks[i]);
+    for (int i = threadIdx.x; i < count; i += blockDim.x) v = combine(v, records[i]);
     v = block_reduce_cost(v);
     if (threadIdx.x == 0) *total = overwrite ? v : combine(*total, v);
+}
+
+__global__ __launch_bounds__(kCostThreads) void cost_finish_kernel(const CostStats* __restrict__ blocks, int count,
+                                                                   CostStats* __restrict__ total, int overwrite) {
+    finish_cost_records(blocks, count, total, overwrite);
 }
 
 static int cost_blocks_for(int count) { return std::max(1, std::min(kMaxCostBlocks, (count + kCostThreads - 1) / kCostThreads)); }
