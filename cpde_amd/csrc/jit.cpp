@@ -433,14 +433,32 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
       << ") void network_backward_k(NetArgs a, int points) {\n"
       << tiles << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n" << bwd.str() << "}\n";
-    // the one-pass epoch reads the row-major weight copies written before its launch
-    std::string fwd_epoch = fwd.str();
-    for (size_t at; (at = fwd_epoch.find("    net_transpose<")) != std::string::npos;)
-        fwd_epoch.erase(at, fwd_epoch.find('\n', at) - at + 1);
-    o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
-      << ") void network_epoch_k(NetArgs a, MatchArgs m, int points) {\n"
-      << tiles << fwd_epoch << "    __syncthreads();  // the output stack of the block's points is written\n"
-      << "    net_match<" << neurons[L - 1] << ">(a, m, " << L - 1 << ", T, p0, npts);\n" << bwd.str() << "}\n";
+    // The one-pass epoch: the row-major weight copies are written before its
+    // launch; the output values and the output adjoint of the block's columns
+    // stay in LDS (O) between the output layer, the match and the backward.
+    {
+        const int NO = neurons[L - 1];
+        std::ostringstream ep;
+        ep << "    __shared__ __attribute__((aligned(16))) float O[2 * kNNC * " << NO << "];\n"
+           << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
+           << "    const MatchTerm pre = match_prefetch<" << NO << ">(m, p0, npts);\n"
+           << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
+           << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
+           << "    __syncthreads();\n";
+        for (int t = 1; t + 2 < L; ++t)
+            ep << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
+        ep << "    net_output<" << neurons[L - 2] << ", " << NO << ">(a, " << L - 2 << ", X, p0, npts, O);\n"
+           << "    __syncthreads();  // the output values of the block's columns are in O\n"
+           << "    net_match<" << NO << ">(a, m, " << L - 1 << ", T, p0, npts, O, O + kNNC * " << NO << ", pre);\n"
+           << "    net_output_backward<" << neurons[L - 2] << ", " << NO << ", true>(a, " << L - 2
+           << ", X, p0, npts, O + kNNC * " << NO << ");\n";
+        for (int t = L - 3; t >= 1; --t)
+            ep << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t
+               << ", X, T, p0, npts);\n";
+        ep << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
+        o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
+          << ") void network_epoch_k(NetArgs a, MatchArgs m, int points) {\n" << tiles << ep.str() << "}\n";
+    }
     o << "\nextern \"C\" __global__ __launch_bounds__(256) void input_layer_k(const float* W, const float* X, float* Z,"
          " float* Y, int points) { input_layer<"
       << neurons[0] << ", " << neurons[1] << ">(W, X, Z, Y, points); }\n";
