@@ -335,16 +335,30 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
     GradientPlan g;
     g.offset.assign(T, 0);
     auto thin = [&](int t) { return n.neurons[t + 1] <= 16 || n.neurons[t] <= 16; };
-    auto tile_of = [&](int t) { return n.neurons[t + 1] <= 64 && n.neurons[t] <= 64 ? 64 : 128; };
+    // 128x128 tiles, or 64x64 when both widths are at most 64 -- or when the
+    // 128x128 splits would be short (fewer than kWgradMinColumns columns each):
+    // then four times the tiles give each split four times the columns, and
+    // the split partials the reduction reads shrink fourfold
+    bool small_tiles = false;
+    auto tile_of = [&](int t) { return small_tiles || (n.neurons[t + 1] <= 64 && n.neurons[t] <= 64) ? 64 : 128; };
     auto tiles_of = [&](int t) {
         const int T0 = tile_of(t);
         return ((n.neurons[t + 1] + T0 - 1) / T0) * ((n.neurons[t] + T0 - 1) / T0);
     };
-    int total_tiles = 0;
-    for (int t = 0; t < T; ++t)
-        if (!thin(t) && !external_splits[t]) total_tiles += tiles_of(t);
+    auto count_tiles = [&] {
+        int total = 0;
+        for (int t = 0; t < T; ++t)
+            if (!thin(t) && !external_splits[t]) total += tiles_of(t);
+        return total;
+    };
     // whole waves of tiles: a partial last wave would run alone for a whole split
-    const int tile_splits = std::max(1, wgrad_blocks_per_cu() * d.compute_units / std::max(1, total_tiles));
+    auto splits_for = [&](int tiles) { return std::max(1, wgrad_blocks_per_cu() * d.compute_units / std::max(1, tiles)); };
+    int total_tiles = count_tiles();
+    if (total_tiles > 0 && K / splits_for(total_tiles) < kWgradMinColumns) {
+        small_tiles = true;
+        total_tiles = count_tiles();
+    }
+    const int tile_splits = splits_for(total_tiles);
     g.wa.K = K;
     g.wa.R = p.rows;
     g.wa.block_begin[0] = 0;

@@ -36,7 +36,8 @@ constexpr int kMaxRows = 255;      // row indices are stored in 8 bits in the te
 constexpr int kMaxTransitions = 32;  // per fused optimizer launch
 constexpr int kCostThreads = 256;
 constexpr int kMaxCostBlocks = 1024;
-constexpr int kWgradChunk = 32;  // columns per LDS chunk of the weight-gradient tiles
+constexpr int kWgradChunk = 32;         // columns per LDS chunk of the weight-gradient tiles
+constexpr int kWgradMinColumns = 1024;  // shorter 128x128 splits switch to 64x64 tiles
 
 // Device-side mirrors of the public reduction structs.
 struct CostStats {
