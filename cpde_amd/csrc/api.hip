@@ -3,6 +3,7 @@
 #include <hip/hiprtc.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -154,6 +155,10 @@ static const int* plan_rows(Plan& p, const int* rows) {
 }
 
 FusedModule::~FusedModule() {
+    if (module) (void)hipModuleUnload(module);
+}
+
+ExpressionEpoch::~ExpressionEpoch() {
     if (module) (void)hipModuleUnload(module);
 }
 
@@ -427,16 +432,31 @@ struct MatchArgsHost {
     int target_width, weight_samples, offset, valid, collect;
 };
 
-// Forward, matching cost and backward of one chunk in one network-fused launch,
-// then the cost's fixed-order finish and the weight-gradient contraction.
-static void fused_epoch(Plan& p, const MatchArgsHost& match, int cost_index, bool accumulate) {
-    Net& n = *p.net;
-    Device& d = *n.dev;
-    FusedModule& fm = *p.fused;
-    const int L = n.layers;
-    int width = p.width;
-    const double cols = double(p.columns());
-    const int blocks = (width + fm.net_points_per_block - 1) / fm.net_points_per_block;
+// Host mirror of the one-pass epoch's expression arguments (fused.hip.in ExpressionArgs).
+struct ExpressionArgsHost {
+    const double* fields;
+    const double* weights;
+    const double* multiplier;
+    CostStats* partials;
+    int samples, offset, valid, collect;
+};
+
+static int epoch_blocks(const Plan& p) {
+    return (p.width + p.fused->net_points_per_block - 1) / p.fused->net_points_per_block;
+}
+
+// Whether the one-pass epoch applies: a network-fused plan whose chunk's
+// workgroups are resident together (the saved kernel boundary matters); long
+// grids keep separate launches, where the forward has its own, higher occupancy.
+// CPDE_ONE_PASS=0 forces the separate launches (same kernels otherwise).
+static bool one_pass_fits(const Plan& p) {
+    return env_int("CPDE_ONE_PASS", 1) && p.fused && p.network && epoch_blocks(p) <= 4 * p.net->dev->compute_units;
+}
+
+// The per-workgroup cost records of a one-pass epoch.
+static CostStats* epoch_records(Plan& p) {
+    Device& d = *p.net->dev;
+    const int blocks = epoch_blocks(p);
     if (blocks > p.epoch_capacity) {
         HIP_CHECK(hipStreamSynchronize(d.stream));
         if (p.epoch_partials) HIP_CHECK(hipFree(p.epoch_partials));
@@ -444,15 +464,25 @@ static void fused_epoch(Plan& p, const MatchArgsHost& match, int cost_index, boo
         HIP_CHECK(hipMalloc(&p.epoch_partials, sizeof(CostStats) * size_t(blocks)));
         p.epoch_capacity = blocks;
     }
+    return p.epoch_partials;
+}
 
+// Forward, cost and backward of one chunk in one network-fused launch of
+// `kernel` (arguments: the network, `cost_args`, the chunk width), then the
+// cost's fixed-order finish and the weight-gradient contraction.
+static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, int cost_index, bool accumulate) {
+    Net& n = *p.net;
+    Device& d = *n.dev;
+    const int L = n.layers;
+    int width = p.width;
+    const double cols = double(p.columns());
+    const int blocks = epoch_blocks(p);
     std::vector<int> external(L - 1, 0);
     external[0] = external[L - 2] = blocks;
     GradientPlan g = plan_gradients(p, accumulate, external);
     NetArgsHost a = net_args(n);
     a.partial_in = n.partials + g.offset[0];
     a.partial_out = n.partials + g.offset[L - 2];
-    MatchArgsHost m = match;
-    m.partials = p.epoch_partials;
     if (!n.wt_current) {
         // the backward half reads the row-major weight copies of every hidden
         // transition, which no workgroup of the same launch may still be
@@ -469,13 +499,13 @@ static void fused_epoch(Plan& p, const MatchArgsHost& match, int cost_index, boo
         launch_transpose(d, W.data(), WT.data(), ni.data(), no.data(), int(W.size()));
         n.wt_current = true;
     }
-    void* args[] = {&a, &m, &width};
+    void* args[] = {&a, cost_args, &width};
     double flops = 0;
     for (int t = 0; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
     for (int t = 1; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
     {
         TraceScope trace(d, kTraceNetworkEpoch, flops);
-        launch_module(d, fm.network_epoch, unsigned(blocks), 1, args);
+        launch_module(d, kernel, unsigned(blocks), 1, args);
     }
     if (blocks <= kMaxCostBlocks) {  // the cost's finish rides in the gradient reduction launch
         g.ra.cost_partials = p.epoch_partials;
@@ -486,6 +516,30 @@ static void fused_epoch(Plan& p, const MatchArgsHost& match, int cost_index, boo
         launch_finish_cost(d, p.epoch_partials, blocks, cost_index);
     }
     run_gradients(d, g);
+}
+
+// The plan's one-pass epoch kernel for an expression program: the program's
+// source compiled together with the plan's network kernels (cached on disk and
+// per device by source text, per plan by program id).
+static hipFunction_t expression_epoch(Plan& p, const Program& program) {
+    for (auto& kv : p.expression_epochs)
+        if (kv.first == program.id) return kv.second->function;
+    Device& d = *p.net->dev;
+    const FusedTuning tune = tuning(p.tables.rows, p.width, d.compute_units);
+    const std::string src = expression_epoch_source(p.tables, p.net->neurons, tune, program.source);
+    std::shared_ptr<ExpressionEpoch> e;
+    for (auto& kv : d.expression_epochs)
+        if (kv.first == src) e = kv.second;
+    if (!e) {
+        std::string log;
+        const std::vector<char> code = compile_module(src, device_arch(d.ordinal), &log);
+        e = std::make_shared<ExpressionEpoch>();
+        HIP_CHECK(hipModuleLoadData(&e->module, code.data()));
+        HIP_CHECK(hipModuleGetFunction(&e->function, e->module, "network_epoch_expression_k"));
+        d.expression_epochs.emplace_back(src, e);
+    }
+    p.expression_epochs.emplace_back(program.id, e);
+    return e->function;
 }
 
 static void weight_gradients(Plan& p, bool accumulate) {
@@ -847,13 +901,7 @@ int cpde_epoch_matching(cpde_plan* plan, const float* target, int target_width, 
         require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
         require(plan->backward, "plan has no adjoint storage");
         require(valid >= 0 && valid <= plan->width && offset >= 0, "invalid chunk range");
-        // one launch where the whole chunk's workgroups are resident together (the
-        // saved kernel boundary matters); separate launches for long grids, where
-        // the forward keeps its own, higher occupancy
-        const bool one_pass = plan->fused && plan->network &&
-                              (plan->width + plan->fused->net_points_per_block - 1) / plan->fused->net_points_per_block <=
-                                  4 * d.compute_units;
-        if (!one_pass) {
+        if (!one_pass_fits(*plan)) {
             if (int code = cpde_forward(plan)) throw_code(code);
             if (int code = cpde_cost_matching(plan, target, target_width, target_rows, weights, weight_samples, offset,
                                               valid, cost_index, collect, 1))
@@ -861,9 +909,9 @@ int cpde_epoch_matching(cpde_plan* plan, const float* target, int target_width, 
             if (int code = cpde_backward(plan, accumulate)) throw_code(code);
             return;
         }
-        const MatchArgsHost m{target, target_rows, weights, nullptr, target_width, weight_samples, offset, valid,
-                              collect != 0};
-        fused_epoch(*plan, m, cost_index, accumulate != 0);
+        MatchArgsHost m{target, target_rows, weights, epoch_records(*plan), target_width, weight_samples, offset, valid,
+                        collect != 0};
+        one_pass_epoch(*plan, plan->fused->network_epoch, &m, cost_index, accumulate != 0);
     });
 }
 
@@ -1003,32 +1051,21 @@ int cpde_reset_optimizer(cpde_net* net) {
 int cpde_program_compile(cpde_device* dev, const char* source, cpde_program** out, char* log, size_t log_capacity) {
     return guarded([&] {
         require(source && out, "null argument");
-        hiprtcProgram prog;
-        if (hiprtcCreateProgram(&prog, source, "cpde_expression.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
-            throw compile_error("hiprtcCreateProgram failed");
-        hipDeviceProp_t prop;
-        HIP_CHECK(hipGetDeviceProperties(&prop, dev->ordinal));
-        std::string arch = std::string("--offload-arch=") + prop.gcnArchName;
-        const char* options[] = {arch.c_str(), "-O3", "-std=c++17"};
-        const hiprtcResult result = hiprtcCompileProgram(prog, 3, options);
-        size_t size = 0;
-        hiprtcGetProgramLogSize(prog, &size);
-        std::string text(size, '\0');
-        if (size) hiprtcGetProgramLog(prog, &text[0]);
-        while (!text.empty() && text.back() == '\0') text.pop_back();
-        if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
-        if (result != HIPRTC_SUCCESS) {
-            hiprtcDestroyProgram(&prog);
+        static std::atomic<uint64_t> next_id{1};
+        std::string text;
+        std::vector<char> code;
+        try {
+            code = compile_module(source, device_arch(dev->ordinal), &text);
+        } catch (const compile_error&) {
+            if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
             throw compile_error("expression compile failed: " + text);
         }
-        size_t code_size = 0;
-        hiprtcGetCodeSize(prog, &code_size);
-        std::vector<char> code(code_size);
-        hiprtcGetCode(prog, code.data());
-        hiprtcDestroyProgram(&prog);
+        if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
         auto p = std::make_unique<cpde_program>();
         p->dev = dev;
         p->log = text;
+        p->source = source;
+        p->id = next_id++;
         HIP_CHECK(hipModuleLoadData(&p->module, code.data()));
         HIP_CHECK(hipModuleGetFunction(&p->function, p->module, "expression"));
         *out = p.release();
@@ -1064,6 +1101,33 @@ int cpde_cost_expression(cpde_plan* plan, cpde_program* program, const double* f
         HIP_CHECK(hipModuleLaunchKernel(program->function, blocks, 1, 1, kCostThreads, 1, 1, 0, d.stream, args,
                                         nullptr));
         launch_sample_reduce(d, loss, bad, valid, offset, cost_index);
+    });
+}
+
+int cpde_epoch_expression(cpde_plan* plan, cpde_program* program, const double* fields,
+                          const double* quadrature_weights, int samples, int offset, int valid, const double* multiplier,
+                          void* scratch, int cost_index, int collect, int accumulate) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        require(program, "null argument");
+        require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
+        require(plan->backward, "plan has no adjoint storage");
+        require(valid >= 0 && valid <= plan->width && offset >= 0, "invalid chunk range");
+        const bool one_pass =
+            one_pass_fits(*plan) && program->source.find("cpde_expression_point") != std::string::npos;
+        if (!one_pass) {
+            if (int code = cpde_forward(plan)) throw_code(code);
+            if (int code = cpde_cost_expression(plan, program, fields, quadrature_weights, samples, offset, valid,
+                                                multiplier, scratch, cost_index, collect, 1))
+                throw_code(code);
+            if (int code = cpde_backward(plan, accumulate)) throw_code(code);
+            return;
+        }
+        const hipFunction_t kernel = expression_epoch(*plan, *program);
+        ExpressionArgsHost e{fields, quadrature_weights, multiplier, epoch_records(*plan), samples, offset, valid,
+                             collect != 0};
+        one_pass_epoch(*plan, kernel, &e, cost_index, accumulate != 0);
     });
 }
 

@@ -69,6 +69,7 @@ Tables build_tables(int rows, int variables, const int* table);
 
 struct Device;
 struct FusedModule;
+struct ExpressionEpoch;
 
 struct Net {
     Device* dev = nullptr;
@@ -106,6 +107,8 @@ struct Plan {
     bool network = false;                // fused: one network-wide kernel per pass
     CostStats* epoch_partials = nullptr;  // one-pass epoch: one cost record per workgroup
     int epoch_capacity = 0;
+    // one-pass expression epochs of this plan, by program id
+    std::vector<std::pair<uint64_t, std::shared_ptr<ExpressionEpoch>>> expression_epochs;
     size_t columns() const { return size_t(rows) * size_t(width); }
 };
 
@@ -114,6 +117,8 @@ struct Program {
     hipModule_t module = nullptr;
     hipFunction_t function = nullptr;
     std::string log;
+    std::string source;  // kept for the one-pass epoch, which compiles it into the network module
+    uint64_t id = 0;     // unique per compiled program
 };
 
 // Per-launch device timing (HIP events on the library's stream), grouped by
@@ -154,6 +159,7 @@ struct Device {
     void fold_trace();
     // fused modules compiled on this device, by source text
     std::vector<std::pair<std::string, std::shared_ptr<FusedModule>>> fused_modules;
+    std::vector<std::pair<std::string, std::shared_ptr<ExpressionEpoch>>> expression_epochs;
     // Cost slots cleared by cpde_costs_begin and not yet written: the first
     // finish into a slot overwrites it instead of accumulating.
     std::vector<char> slot_fresh;
@@ -212,6 +218,14 @@ struct FusedTuning {
     int forward_blocks = 2, backward_blocks = 2;  // blocks per CU the register budget must allow
 };
 std::string fused_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning);
+std::string expression_epoch_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning,
+                                    const std::string& program);
+// The one-pass epoch kernel of one expression program on one network module.
+struct ExpressionEpoch {
+    hipModule_t module = nullptr;
+    hipFunction_t function = nullptr;
+    ~ExpressionEpoch();
+};
 std::vector<char> compile_module(const std::string& source, const std::string& arch, std::string* log);
 
 // Brackets one launch with events when tracing is on.

@@ -381,10 +381,11 @@ std::vector<char> compile_module(const std::string& source, const std::string& a
     return code;
 }
 
-// Full source of the fused module for a schema and architecture.
-std::string fused_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning) {
+// Tuning macros, the generated compositions and the fused kernels' device code
+// for a schema and architecture.
+static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<int>& neurons,
+                          const FusedTuning& tuning) {
     const int points_per_block = tuning.points_per_block, net_points_per_block = tuning.net_points_per_block;
-    std::ostringstream o;
     const int L = int(neurons.size());
     int widest = 0;
     for (int l = 1; l + 1 < L; ++l) widest = std::max(widest, neurons[l]);
@@ -407,6 +408,39 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
         if (G > 1) o << "#define CPDE_SPLIT" << G << " 1\n";
     o << compose_source(t, splits);
     o << kFusedSource;
+}
+
+// Body of a one-pass epoch kernel: the forward of the workgroup's points, the
+// output values and the output adjoint of its columns kept in LDS (O), the
+// cost stage `cost` between them (it fills O's second half), then the
+// backward.  The row-major weight copies are written before the launch.
+static std::string epoch_body(const std::vector<int>& neurons, const std::string& prefetch, const std::string& cost) {
+    const int L = int(neurons.size()), NO = neurons[L - 1];
+    std::ostringstream ep;
+    ep << "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
+       << "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n"
+       << "    __shared__ __attribute__((aligned(16))) float O[2 * kNNC * " << NO << "];\n"
+       << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
+       << prefetch << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
+       << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
+       << "    __syncthreads();\n";
+    for (int t = 1; t + 2 < L; ++t)
+        ep << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
+    ep << "    net_output<" << neurons[L - 2] << ", " << NO << ">(a, " << L - 2 << ", X, p0, npts, O);\n"
+       << "    __syncthreads();  // the output values of the block's columns are in O\n"
+       << cost << "    net_output_backward<" << neurons[L - 2] << ", " << NO << ", true>(a, " << L - 2
+       << ", X, p0, npts, O + kNNC * " << NO << ");\n";
+    for (int t = L - 3; t >= 1; --t)
+        ep << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
+    ep << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
+    return ep.str();
+}
+
+// Full source of the fused module for a schema and architecture.
+std::string fused_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning) {
+    std::ostringstream o;
+    const int L = int(neurons.size());
+    emit_prologue(o, t, neurons, tuning);
     // network-fused forward and backward, one call per layer with its widths;
     // the one-pass epoch runs both with the matching cost between them
     std::ostringstream fwd, bwd;
@@ -433,31 +467,15 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
       << ") void network_backward_k(NetArgs a, int points) {\n"
       << tiles << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n" << bwd.str() << "}\n";
-    // The one-pass epoch: the row-major weight copies are written before its
-    // launch; the output values and the output adjoint of the block's columns
-    // stay in LDS (O) between the output layer, the match and the backward.
     {
         const int NO = neurons[L - 1];
-        std::ostringstream ep;
-        ep << "    __shared__ __attribute__((aligned(16))) float O[2 * kNNC * " << NO << "];\n"
-           << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
-           << "    const MatchTerm pre = match_prefetch<" << NO << ">(m, p0, npts);\n"
-           << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
-           << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
-           << "    __syncthreads();\n";
-        for (int t = 1; t + 2 < L; ++t)
-            ep << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
-        ep << "    net_output<" << neurons[L - 2] << ", " << NO << ">(a, " << L - 2 << ", X, p0, npts, O);\n"
-           << "    __syncthreads();  // the output values of the block's columns are in O\n"
-           << "    net_match<" << NO << ">(a, m, " << L - 1 << ", T, p0, npts, O, O + kNNC * " << NO << ", pre);\n"
-           << "    net_output_backward<" << neurons[L - 2] << ", " << NO << ", true>(a, " << L - 2
-           << ", X, p0, npts, O + kNNC * " << NO << ");\n";
-        for (int t = L - 3; t >= 1; --t)
-            ep << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t
-               << ", X, T, p0, npts);\n";
-        ep << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
+        const std::string prefetch =
+            "    const MatchTerm pre = match_prefetch<" + std::to_string(NO) + ">(m, p0, npts);\n";
+        const std::string cost = "    net_match<" + std::to_string(NO) + ">(a, m, " + std::to_string(L - 1) +
+                                 ", T, p0, npts, O, O + kNNC * " + std::to_string(NO) + ", pre);\n";
         o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
-          << ") void network_epoch_k(NetArgs a, MatchArgs m, int points) {\n" << tiles << ep.str() << "}\n";
+          << ") void network_epoch_k(NetArgs a, MatchArgs m, int points) {\n" << epoch_body(neurons, prefetch, cost)
+          << "}\n";
     }
     o << "\nextern \"C\" __global__ __launch_bounds__(256) void input_layer_k(const float* W, const float* X, float* Z,"
          " float* Y, int points) { input_layer<"
@@ -473,6 +491,23 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     o << "extern \"C\" __global__ __launch_bounds__(256) void output_backward_k(const float* W, const float* G,"
          " const float* Zl, float* Gl, int points) { output_backward<"
       << neurons[L - 2] << ", " << neurons[L - 1] << ">(W, G, Zl, Gl, points); }\n";
+    return o.str();
+}
+
+// The one-pass epoch of an expression cost: the expression program (which
+// defines cpde_expression_point) compiled together with the network kernels of
+// a schema and architecture.
+std::string expression_epoch_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning,
+                                    const std::string& program) {
+    std::ostringstream o;
+    const int L = int(neurons.size()), NO = neurons[L - 1];
+    o << "// generated: one-pass epoch of an expression cost\n" << program << "\n#define CPDE_EXPRESSION_EPOCH 1\n";
+    emit_prologue(o, t, neurons, tuning);
+    const std::string cost = "    net_expression<" + std::to_string(NO) + ">(a, e, " + std::to_string(L - 1) +
+                             ", T, p0, npts, O, O + kNNC * " + std::to_string(NO) + ");\n";
+    o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
+      << ") void network_epoch_expression_k(NetArgs a, ExpressionArgs e, int points) {\n" << epoch_body(neurons, "", cost)
+      << "}\n";
     return o.str();
 }
 

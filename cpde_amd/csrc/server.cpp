@@ -261,20 +261,25 @@ std::string number(double x) {
     return t;
 }
 
+// The program of an expression cost (cuda/cost_kernels.cuh expression costs,
+// cpde/_expressions.py IR): a per-sample device function
+// cpde_expression_point(yp, gp, ...) -- value, non-finite flag and, with
+// `gradient`, d(loss)/d(output component) scaled by the multiplier into gp --
+// and the kernel `expression` that applies it to every sample of a chunk.  The
+// library's one-pass epoch compiles the same function into the network module
+// and applies it to the output values a workgroup holds in LDS.
 std::string expression_source(const std::vector<ExpressionNode>& nodes) {
     std::ostringstream s;
-    s << "extern \"C\" __global__ __launch_bounds__(256) void expression(const float* __restrict__ y, float* g,\n"
-         "    const double* __restrict__ fields, const double* __restrict__ weights, double* loss, int* bad,\n"
-         "    int outputs, int rows, int samples, int width, int offset, int valid, const double* multiplier,\n"
-         "    int collect, int gradient) {\n"
-         "  const int comps = rows * outputs;\n"
-         "  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < width; p += blockDim.x * gridDim.x) {\n"
-         "    loss[p] = 0; bad[p] = -2;\n"
-         "    if (gradient) for (int c = 0; c < comps; ++c) g[(size_t)p * comps + c] = 0.0f;\n"
-         "    if (p >= valid || weights[offset + p] == 0) continue;\n"
-         "    const double scale = multiplier ? *multiplier : 1.0;\n"
-         "    if (gradient && scale == 0 && !collect) continue;\n"
-         "    const float* yp = y + (size_t)p * comps;\n";
+    s << "__device__ __forceinline__ void cpde_expression_point(const float* __restrict__ yp, float* __restrict__ gp,\n"
+         "    const double* __restrict__ fields, const double* __restrict__ weights, int comps, int samples, int offset,\n"
+         "    int p, int valid, double scale, int collect, int gradient, double* loss_out, int* bad_out) {\n"
+         "  *loss_out = 0; *bad_out = -2;\n"
+         "  if (gradient) for (int c = 0; c < comps; ++c) gp[c] = 0.0f;\n"
+         "  if (p >= valid || weights[offset + p] == 0) return;\n"
+         "  if (gradient && scale == 0 && !collect) return;\n"
+         "  int bad = -2;\n"
+         "  double lossv = 0;\n"
+         "  {\n";
     std::vector<bool> active;
     for (size_t i = 0; i < nodes.size(); ++i) {
         const ExpressionNode& n = nodes[i];
@@ -302,16 +307,17 @@ std::string expression_source(const std::vector<ExpressionNode>& nodes) {
         case kTanh: e = "tanh(" + a + ")"; break;
         default: throw Rejected("invalid expression node");
         }
-        s << "    const double v" << i << " = " << e << "; if (!isfinite(v" << i << ")) bad[p] = -1;\n";
+        s << "    const double v" << i << " = " << e << "; if (!isfinite(v" << i << ")) bad = -1;\n";
         const bool act = n.op == kComponent ? n.b == 0
                                             : (n.op <= kField ? false
                                                               : active[n.a] || (n.op >= kAdd && n.op <= kDiv && active[n.b]));
         active.push_back(act);
     }
     const size_t last = nodes.size() - 1;
-    s << "    if (collect) loss[p] = weights[offset + p] * v" << last << ";\n"
-      << "    if (!isfinite(loss[p])) bad[p] = -1;\n"
-      << "    if (!gradient || scale == 0 || bad[p] != -2) continue;\n";
+    s << "    if (collect) lossv = weights[offset + p] * v" << last << ";\n"
+      << "    if (!isfinite(lossv)) bad = -1;\n"
+      << "    *loss_out = lossv; *bad_out = bad;\n"
+      << "    if (!gradient || scale == 0 || bad != -2) return;\n";
     for (size_t i = 0; i < nodes.size(); ++i) s << "    double d" << i << " = " << (i == last ? "1" : "0") << ";\n";
     for (int i = int(nodes.size()) - 1; i >= 0; --i) {
         const ExpressionNode& n = nodes[i];
@@ -349,10 +355,20 @@ std::string expression_source(const std::vector<ExpressionNode>& nodes) {
     for (const auto& kv : comps) {
         s << "    { double t = 0";
         for (size_t i : kv.second) s << " + d" << i;
-        s << "; const float out = (float)(t * weights[offset + p] * scale); g[(size_t)p * comps + " << kv.first
-          << "] = out; if (!isfinite(out)) bad[p] = " << kv.first << "; }\n";
+        s << "; const float out = (float)(t * weights[offset + p] * scale); gp[" << kv.first
+          << "] = out; if (!isfinite(out)) *bad_out = " << kv.first << "; }\n";
     }
-    s << "  }\n}\n";
+    s << "  }\n}\n"
+         "extern \"C\" __global__ __launch_bounds__(256) void expression(const float* __restrict__ y, float* g,\n"
+         "    const double* __restrict__ fields, const double* __restrict__ weights, double* loss, int* bad,\n"
+         "    int outputs, int rows, int samples, int width, int offset, int valid, const double* multiplier,\n"
+         "    int collect, int gradient) {\n"
+         "  const int comps = rows * outputs;\n"
+         "  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < width; p += blockDim.x * gridDim.x) {\n"
+         "    const double scale = multiplier ? *multiplier : 1.0;\n"
+         "    cpde_expression_point(y + (size_t)p * comps, gradient ? g + (size_t)p * comps : nullptr, fields, weights,\n"
+         "                          comps, samples, offset, p, valid, scale, collect, gradient, &loss[p], &bad[p]);\n"
+         "  }\n}\n";
     return s.str();
 }
 
@@ -682,6 +698,15 @@ void Server::pass(NetRecord& n, CostRecord& c, int slot, bool& first, const Pass
             require(n.loaded == want, "forward context is no longer current");
         } else {
             activate(n, plan, c.input, c.rows, offset, valid);
+            if (c.kind == 2 && backward && c.has_components) {
+                // forward, cost and backward of this chunk in one pass (the
+                // multiplier, if any, is final before the pass starts)
+                call(cpde_epoch_expression(plan, c.program, c.fields.as<double>(), c.quadrature.as<double>(), c.samples,
+                                           offset, valid, how.multiplier, c.scratch.ptr, slot, how.collect,
+                                           first ? 0 : 1));
+                first = false;
+                continue;
+            }
             if (c.kind == 0 && backward && !how.multiplier && c.has_components) {
                 // forward, cost and backward of this chunk in one pass
                 DataRecord& t = data(c.target);

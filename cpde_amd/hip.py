@@ -78,6 +78,7 @@ SIGNATURES = {
     'cpde_program_compile': (i32, [vp, ctypes.c_char_p, ctypes.POINTER(vp), ctypes.c_char_p, ctypes.c_size_t]),
     'cpde_program_destroy': (i32, [vp]),
     'cpde_cost_expression': (i32, [vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, i32]),
+    'cpde_epoch_expression': (i32, [vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, i32]),
     'cpde_graph_execute': (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, i32]),
     'cpde_jit_prepare': (i32, [i32, i32, vp, i32, vp, i32, i32, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     'cpde_trace_enable': (i32, [vp, i32]),

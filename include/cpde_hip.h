@@ -199,7 +199,10 @@ int cpde_zero_gradient(cpde_net* net);
 int cpde_reset_optimizer(cpde_net* net);
 
 /* ---- scalar-expression costs: generated source compiled with hipRTC for gfx950
- *      (cuda/expression_program.hpp:96-131 used NVRTC) and the scalar cost graph. */
+ *      (cuda/expression_program.hpp:96-131 used NVRTC) and the scalar cost graph.
+ * The source defines the kernel `expression` (arguments as cpde_cost_expression
+ * passes them) and may define the per-sample function cpde_expression_point
+ * that cpde_epoch_expression compiles into the network kernels. */
 int cpde_program_compile(cpde_device* dev, const char* source, cpde_program** out, char* log, size_t log_capacity);
 int cpde_program_destroy(cpde_program* program);
 /* Per-sample expression over the plan's output stack, then its deterministic
@@ -209,6 +212,18 @@ int cpde_program_destroy(cpde_program* program);
 int cpde_cost_expression(cpde_plan* plan, cpde_program* program, const double* fields,
                          const double* quadrature_weights, int samples, int offset, int valid,
                          const double* multiplier, void* scratch, int cost_index, int collect, int gradient);
+/* One chunk of Server::pass for an expression cost with gradient
+ * (cuda/cpde_server.cu:223-257): cpde_forward, cpde_cost_expression(gradient=1)
+ * and cpde_backward(accumulate) with the same arguments.  On the network-fused
+ * kernels, when the chunk's workgroups fit on the device together and the
+ * program defines cpde_expression_point, this is one launch (a sample's value
+ * and adjoint depend on that sample alone; the program is compiled into the
+ * network module on first use), the cost's finish and the weight-gradient
+ * contraction.  The multiplier must be final when the call is made.  The input
+ * chunk must be activated. */
+int cpde_epoch_expression(cpde_plan* plan, cpde_program* program, const double* fields,
+                          const double* quadrature_weights, int samples, int offset, int valid,
+                          const double* multiplier, void* scratch, int cost_index, int collect, int accumulate);
 /* cost_graph::execute (cuda/cost_graph.cuh:6-27) on one lane: reads cost slots,
  * writes values/adjoints/multipliers/active (device) and the summary (device). */
 int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int count, int root, int leaves,

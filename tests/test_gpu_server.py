@@ -80,6 +80,37 @@ def test_expression_costs_and_graph(server):
     assert 'expression' in source
 
 
+def test_one_pass_expression_epoch_matches_separate_launches(server):
+    """The Poisson objective and gradient with the one-pass expression epoch
+    (forward, per-sample expression and backward in one launch per leaf) against
+    a second server that runs them as separate launches (CPDE_ONE_PASS=0): the
+    same adjoint and backward, so bit-identical gradients; the objective
+    differs only in its fp64 summation order.  Then three RPROP epochs on each,
+    whose weights must stay bit-identical."""
+    import os
+    from cpde_amd import workloads as W
+    g = load_golden('poisson')
+    pw = W.PoissonWorkload(radial=int(g['radial']), angular=int(g['angular']), boundary=int(g['boundary']))
+    separate = wire.Session(SERVER, env=dict(os.environ, CPDE_ONE_PASS='0'))
+    try:
+        results = []
+        for s in (server, separate):
+            ids = pw.upload(s)
+            value, grads = s.graph_eval(ids['net'], ids['costs'], pw.graph(), gradient=True)
+            s.train(ids['net'], ids['costs'], 3, method=0, fresh=1, log=1, graph=pw.graph())
+            results.append((value, grads, wire.decode_state(s.snapshot(ids['net']))))
+    finally:
+        separate.close()
+    (v1, g1, st1), (v2, g2, st2) = results
+    print(f'[result] one-pass objective {v1!r} separate {v2!r}', flush=True)
+    assert abs(v1 / v2 - 1) < 1e-12
+    for a, b in zip(g1, g2):
+        np.testing.assert_array_equal(a, b)
+    assert st1[0] == st2[0]
+    for a, b in zip(st1[1], st2[1]):
+        np.testing.assert_array_equal(a['buffers'][0], b['buffers'][0])
+
+
 def test_value_dependent_graph_multipliers(server):
     """root = leaf0 / leaf1 + log(leaf0) + leaf1 ** 1.5: the leaf multipliers are
     known only after the forward passes, so every leaf runs a second, backward
