@@ -140,7 +140,12 @@ static int guarded(F body) {
     throw device_error(message);
 }
 
-static const float* activations(const Net& net, int l) { return net.linear[l] ? net.z[l] : net.y[l]; }
+// Layer l's values as the next transition reads them: the plan's activated
+// input at layer 0, z of a linear layer, y otherwise.
+static const float* activations(const Plan& p, int l) {
+    const Net& net = *p.net;
+    return l == 0 ? p.input : (net.linear[l] ? net.z[l] : net.y[l]);
+}
 
 // Device copy of a host row map; re-uploaded only when it changes (the map is
 // fixed for a cost, so a training loop uploads it once).
@@ -255,7 +260,8 @@ static void launch_module(Device& d, hipFunction_t f, unsigned gx, unsigned gy, 
     HIP_CHECK(hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, d.stream, args, nullptr));
 }
 
-static NetArgsHost net_args(Net& n) {
+static NetArgsHost net_args(const Plan& p) {
+    const Net& n = *p.net;
     NetArgsHost a{};
     for (int t = 0; t + 1 < n.layers; ++t) {
         a.W[t] = n.state[0][t];
@@ -266,7 +272,8 @@ static NetArgsHost net_args(Net& n) {
         a.Y[l] = n.y[l];
         a.G[l] = n.g[l];
     }
-    a.X = n.z[0];
+    a.X = p.input;
+    a.Z[0] = p.input;
     return a;
 }
 
@@ -281,7 +288,7 @@ static void fused_forward(Plan& p) {
     int width = p.width;
     const double cols = double(p.columns());
     if (p.network) {
-        NetArgsHost a = net_args(n);
+        NetArgsHost a = net_args(p);
         void* args[] = {&a, &width};
         double flops = 0;
         for (int t = 0; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
@@ -293,7 +300,7 @@ static void fused_forward(Plan& p) {
     }
     {
         const float* W = n.state[0][0];
-        const float* X = n.z[0];
+        const float* X = p.input;
         float* Z = n.z[1];
         float* Y = n.y[1];
         void* args[] = {&W, &X, &Z, &Y, &width};
@@ -388,7 +395,7 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
             g.wa.tile[w] = tile_of(t);
             g.wa.block_begin[w + 1] = g.wa.block_begin[w] + tiles * s;
             g.wa.G[w] = n.g[t + 1];
-            g.wa.Y[w] = n.linear[t] ? n.z[t] : n.y[t];
+            g.wa.Y[w] = activations(p, t);
             g.flops += 2.0 * M * N * double(K);
             ++w;
         }
@@ -480,7 +487,7 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, int c
     std::vector<int> external(L - 1, 0);
     external[0] = external[L - 2] = blocks;
     GradientPlan g = plan_gradients(p, accumulate, external);
-    NetArgsHost a = net_args(n);
+    NetArgsHost a = net_args(p);
     a.partial_in = n.partials + g.offset[0];
     a.partial_out = n.partials + g.offset[L - 2];
     if (!n.wt_current) {
@@ -558,7 +565,7 @@ static void fused_backward(Plan& p, bool accumulate) {
         std::vector<int> external(L - 1, 0);
         external[0] = external[L - 2] = blocks;
         const GradientPlan g = plan_gradients(p, accumulate, external);
-        NetArgsHost a = net_args(n);
+        NetArgsHost a = net_args(p);
         a.partial_in = n.partials + g.offset[0];
         a.partial_out = n.partials + g.offset[L - 2];
         void* args[] = {&a, &width};
@@ -795,6 +802,8 @@ int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, i
         blob.insert(blob.end(), p->tables.fwd_offset.begin(), p->tables.fwd_offset.end());
         HIP_CHECK(hipMalloc(&p->dev_tables, blob.size() * sizeof(int)));
         HIP_CHECK(hipMalloc(&p->dev_rows, size_t(rows) * sizeof(int)));
+        HIP_CHECK(hipMalloc(&p->input, p->columns() * net->neurons[0] * sizeof(float)));
+        launch_fill(*net->dev, p->input, p->columns() * net->neurons[0], 0.0f);
         HIP_CHECK(hipMemcpyAsync(p->dev_tables, blob.data(), blob.size() * sizeof(int), hipMemcpyHostToDevice,
                                  net->dev->stream));
         reserve_arena(*net, *p);
@@ -814,6 +823,7 @@ int cpde_plan_destroy(cpde_plan* plan) {
         (void)hipFree(plan->dev_tables);
         (void)hipFree(plan->dev_rows);
         (void)hipFree(plan->epoch_partials);
+        (void)hipFree(plan->input);
         delete plan;
     });
 }
@@ -826,7 +836,7 @@ int cpde_plan_stack(cpde_plan* plan, int layer, int kind, float** device_ptr) {
         const bool keeps_u = plan->fused && plan->network && !n.linear[layer];
         require(!(kind == 0 && keeps_u), "this plan keeps u, not z, for a sigmoid layer (stack kind 3)");
         require(!(kind == 3 && !keeps_u), "u is kept only by network-fused plans for sigmoid layers");
-        float* p = kind == 0 || kind == 3 ? n.z[layer] : kind == 1 ? n.y[layer] : n.g[layer];
+        float* p = kind == 0 || kind == 3 ? (layer == 0 ? plan->input : n.z[layer]) : kind == 1 ? n.y[layer] : n.g[layer];
         require(p != nullptr, "stack not present for this layer");
         *device_ptr = p;
     });
@@ -840,7 +850,7 @@ int cpde_activate(cpde_plan* plan, const float* data, int data_width, const int*
         require(valid >= 0 && valid <= plan->width && offset >= 0 && offset + valid <= data_width,
                 "invalid chunk range");
         reserve_arena(n, *plan);
-        launch_activate(d, n.z[0], data, data_width, n.neurons[0], plan_rows(*plan, rows), plan->rows, plan->width,
+        launch_activate(d, plan->input, data, data_width, n.neurons[0], plan_rows(*plan, rows), plan->rows, plan->width,
                         offset, valid);
     });
 }
@@ -858,7 +868,7 @@ int cpde_forward(cpde_plan* plan) {
             const int ni = n.neurons[t], no = n.neurons[t + 1];
             if (!n.linear[t]) launch_compose_forward(d, *plan, n.z[t], n.y[t], ni);
             const float* W = n.state[0][t];
-            launch_gemm(d, no, cols, ni, W, no, false, activations(n, t), ni, false, n.z[t + 1], no,
+            launch_gemm(d, no, cols, ni, W, no, false, activations(*plan, t), ni, false, n.z[t + 1], no,
                         W + size_t(no) * ni, plan->rows);
         }
     });

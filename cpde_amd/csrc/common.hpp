@@ -103,6 +103,9 @@ struct Plan {
     int* dev_tables = nullptr;  // device copy of tables.words, then tables.fwd_offset
     int* dev_rows = nullptr;    // device row map of the last activate/output
     std::vector<int> host_rows;
+    // the plan's activated chunk [point][row][channel] (layer 0): its own, so
+    // that plans of one network keep their inputs between epochs
+    float* input = nullptr;
     std::shared_ptr<FusedModule> fused;  // null: table-driven kernels
     bool network = false;                // fused: one network-wide kernel per pass
     CostStats* epoch_partials = nullptr;  // one-pass epoch: one cost record per workgroup

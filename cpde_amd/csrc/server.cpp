@@ -210,6 +210,17 @@ struct NetRecord {
                    offset == o.offset && valid == o.valid && rows == o.rows;
         }
     } loaded;
+    // the chunk in each plan's own input stack: re-activation is skipped while
+    // it is unchanged, even when another plan's forward ran in between
+    struct Input {
+        uint64_t data = 0, version = 0;
+        int offset = -1, valid = -1;
+        std::vector<int> rows;
+        bool operator==(const Input& o) const {
+            return data == o.data && version == o.version && offset == o.offset && valid == o.valid && rows == o.rows;
+        }
+    };
+    std::map<cpde_plan*, Input> inputs;
     int transitions() const { return int(neurons.size()) - 1; }
     ~NetRecord() {
         for (auto& kv : plans) cpde_plan_destroy(kv.second);
@@ -674,7 +685,12 @@ void Server::activate(NetRecord& n, cpde_plan* plan, uint64_t data_id, const std
     DataRecord& d = data(data_id);
     NetRecord::Loaded want{plan, data_id, d.version, cpde_net_generation(n.net), offset, valid, rows};
     if (n.loaded == want) return;
-    call(cpde_activate(plan, d.values.as<float>(), d.samples, rows.data(), offset, valid));
+    const NetRecord::Input in{data_id, d.version, offset, valid, rows};
+    auto it = n.inputs.find(plan);
+    if (it == n.inputs.end() || !(it->second == in)) {
+        call(cpde_activate(plan, d.values.as<float>(), d.samples, rows.data(), offset, valid));
+        n.inputs[plan] = in;
+    }
     want.generation = cpde_net_generation(n.net);
     n.loaded = want;
 }
@@ -1075,16 +1091,16 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
             require(n.adam_step < uint64_t(INT_MAX), "Adam counter exceeds supported range");
             call(cpde_adam(n.net, int(++n.adam_step), n.learning_rate));
         }
-        call(cpde_device_synchronize(dev_));
+        // The reference synchronises here (cuda/cpde_server.cu:409) only to
+        // surface errors; every later host read (the next epoch's scalar
+        // download, evaluation, snapshots, outputs) synchronises itself, so the
+        // next epoch's launches queue behind the update instead.
         ++completed;
         ++n.updates;
         ++n.stage_done;
         n.remaining = epochs - completed;
         // the absolute update count survives short calls and checkpoints
-        if (restore_every && n.updates % restore_every == 0) {
-            call(cpde_restore_steps(n.net, restore_step));
-            call(cpde_device_synchronize(dev_));
-        }
+        if (restore_every && n.updates % restore_every == 0) call(cpde_restore_steps(n.net, restore_step));
         const bool last = completed == epochs || stop.load();
         if (collect) report(0);
         if (eval && (completed % eval == 0 || last)) {
