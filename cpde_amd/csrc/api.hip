@@ -63,26 +63,35 @@ void Device::fold_trace() {
 
 void Device::reserve_costs(int costs) {
     require(costs >= 0, "invalid cost count");
-    if (costs <= cost_capacity) return;
-    HIP_CHECK(hipStreamSynchronize(stream));
-    if (cost_totals) HIP_CHECK(hipFree(cost_totals));
-    if (host_costs) HIP_CHECK(hipHostFree(host_costs));
-    cost_totals = nullptr;
-    host_costs = nullptr;
-    HIP_CHECK(hipMalloc(&cost_totals, sizeof(CostStats) * costs));
-    HIP_CHECK(hipHostMalloc(&host_costs, sizeof(CostStats) * costs, hipHostMallocDefault));
-    cost_capacity = costs;
+    reserve_scalars(costs, grad_capacity);
 }
 
-void Device::reserve_grads(int layers) {
-    if (layers <= grad_capacity) return;
+void Device::reserve_grads(int layers) { reserve_scalars(cost_capacity, layers); }
+
+// Grow the scalar block; slots already written keep their values.
+void Device::reserve_scalars(int costs, int layers) {
+    costs = std::max(costs, cost_capacity);
+    layers = std::max(layers, grad_capacity);
+    if (costs == cost_capacity && layers == grad_capacity && scalar_block) return;
     HIP_CHECK(hipStreamSynchronize(stream));
-    if (grad_totals) HIP_CHECK(hipFree(grad_totals));
-    if (host_grads) HIP_CHECK(hipHostFree(host_grads));
-    grad_totals = nullptr;
-    host_grads = nullptr;
-    HIP_CHECK(hipMalloc(&grad_totals, sizeof(GradStats) * layers));
-    HIP_CHECK(hipHostMalloc(&host_grads, sizeof(GradStats) * layers, hipHostMallocDefault));
+    const size_t cost_bytes = (sizeof(CostStats) * size_t(costs) + 255) / 256 * 256;
+    const size_t bytes = cost_bytes + sizeof(GradStats) * size_t(layers);
+    void *block = nullptr, *host = nullptr;
+    HIP_CHECK(hipMalloc(&block, bytes));
+    HIP_CHECK(hipHostMalloc(&host, bytes, hipHostMallocDefault));
+    CostStats* c = static_cast<CostStats*>(block);
+    GradStats* g = reinterpret_cast<GradStats*>(static_cast<char*>(block) + cost_bytes);
+    if (cost_capacity) HIP_CHECK(hipMemcpy(c, cost_totals, sizeof(CostStats) * cost_capacity, hipMemcpyDeviceToDevice));
+    if (grad_capacity) HIP_CHECK(hipMemcpy(g, grad_totals, sizeof(GradStats) * grad_capacity, hipMemcpyDeviceToDevice));
+    if (scalar_block) HIP_CHECK(hipFree(scalar_block));
+    if (host_block) HIP_CHECK(hipHostFree(host_block));
+    scalar_block = block;
+    host_block = host;
+    cost_totals = c;
+    grad_totals = g;
+    host_costs = static_cast<CostStats*>(host);
+    host_grads = reinterpret_cast<GradStats*>(static_cast<char*>(host) + cost_bytes);
+    cost_capacity = costs;
     grad_capacity = layers;
 }
 
@@ -625,8 +634,7 @@ int cpde_device_open(int ordinal, cpde_device** out) {
         HIP_CHECK(hipMalloc(&d->cost_blocks, sizeof(CostStats) * kMaxCostBlocks));
         HIP_CHECK(hipMalloc(&d->grad_blocks, sizeof(GradStats) * kMaxCostBlocks));
         for (auto& e : d->marks) HIP_CHECK(hipEventCreate(&e));
-        d->reserve_costs(8);
-        d->reserve_grads(8);
+        d->reserve_scalars(8, 8);
         HIP_CHECK(hipHostMalloc(&d->host_summary, sizeof(cpde_graph_summary), hipHostMallocDefault));
         *out = d.release();
     });
@@ -640,10 +648,8 @@ int cpde_device_close(cpde_device* dev) {
         for (auto& e : dev->event_pool) (void)hipEventDestroy(e);
         (void)hipFree(dev->cost_blocks);
         (void)hipFree(dev->grad_blocks);
-        (void)hipFree(dev->cost_totals);
-        (void)hipFree(dev->grad_totals);
-        (void)hipHostFree(dev->host_costs);
-        (void)hipHostFree(dev->host_grads);
+        (void)hipFree(dev->scalar_block);
+        (void)hipHostFree(dev->host_block);
         (void)hipHostFree(dev->host_summary);
         (void)hipStreamDestroy(dev->stream);
         delete dev;
@@ -997,12 +1003,17 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
     return guarded([&] {
         require(costs <= dev->cost_capacity && layers <= dev->grad_capacity, "scalar slots out of range");
         require((summary == nullptr) == (summary_out == nullptr), "graph summary source and destination go together");
-        if (costs)
+        if (costs && layers) {  // one copy over both (the block keeps them in this order)
+            const size_t bytes = size_t(reinterpret_cast<char*>(dev->grad_totals + layers) -
+                                        static_cast<char*>(dev->scalar_block));
+            HIP_CHECK(hipMemcpyAsync(dev->host_block, dev->scalar_block, bytes, hipMemcpyDeviceToHost, dev->stream));
+        } else if (costs) {
             HIP_CHECK(hipMemcpyAsync(dev->host_costs, dev->cost_totals, sizeof(CostStats) * costs,
                                      hipMemcpyDeviceToHost, dev->stream));
-        if (layers)
+        } else if (layers) {
             HIP_CHECK(hipMemcpyAsync(dev->host_grads, dev->grad_totals, sizeof(GradStats) * layers,
                                      hipMemcpyDeviceToHost, dev->stream));
+        }
         if (summary)
             HIP_CHECK(hipMemcpyAsync(dev->host_summary, summary, sizeof(cpde_graph_summary), hipMemcpyDeviceToHost,
                                      dev->stream));

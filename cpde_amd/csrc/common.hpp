@@ -145,10 +145,14 @@ struct Device {
     hipStream_t stream = nullptr;
     // reduction workspace (cuda/reduction_kernels.cuh:101-178)
     CostStats* cost_blocks = nullptr;   // kMaxCostBlocks
-    CostStats* cost_totals = nullptr;   // cost_capacity
     GradStats* grad_blocks = nullptr;   // kMaxCostBlocks
-    GradStats* grad_totals = nullptr;   // grad_capacity
-    CostStats* host_costs = nullptr;
+    // cost and gradient totals in one device block, [cost_capacity] then
+    // [grad_capacity], mirrored by one pinned host block: one copy downloads both
+    void* scalar_block = nullptr;
+    void* host_block = nullptr;
+    CostStats* cost_totals = nullptr;   // cost_capacity, in scalar_block
+    GradStats* grad_totals = nullptr;   // grad_capacity, in scalar_block
+    CostStats* host_costs = nullptr;    // in host_block
     GradStats* host_grads = nullptr;
     cpde_graph_summary* host_summary = nullptr;  // pinned: one graph summary
     int cost_capacity = 0, grad_capacity = 0;
@@ -173,6 +177,7 @@ struct Device {
     }
     void reserve_costs(int costs);
     void reserve_grads(int layers);
+    void reserve_scalars(int costs, int layers);
 };
 
 // Grouped weight-gradient launch (one entry per transition).

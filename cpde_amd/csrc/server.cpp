@@ -816,7 +816,16 @@ void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
     int reuse = -1, last_offset = 0;
     double best_work = -1;
     if (backward) {
-        call(cpde_zero_gradient(n.net));
+        // The reference zeroes the gradient here (cuda/cpde_server.cu:278).  The
+        // first backward pass overwrites all of it (accumulate 0), so the zero
+        // fill is needed only when no leaf will run one.
+        bool written = false;
+        for (size_t i = 0; i < ids.size() && !written; ++i) {
+            CostRecord& c = cost(ids[i]);
+            const bool runs = !graph.schedule[i].known || graph.schedule[i].value != 0;
+            written = runs && c.input && c.has_gradient && data(c.input).samples > 0;
+        }
+        if (!written) call(cpde_zero_gradient(n.net));
         // run the most expensive leaf with an unknown multiplier last so its
         // final forward can be reused by its backward (a work estimate)
         for (size_t i = 0; i < ids.size(); ++i) {

@@ -111,6 +111,24 @@ def test_one_pass_expression_epoch_matches_separate_launches(server):
         np.testing.assert_array_equal(a['buffers'][0], b['buffers'][0])
 
 
+def test_graph_without_leaf_dependence_zeroes_the_gradient(server):
+    """A root that depends on no leaf: every multiplier is known to be 0, no
+    leaf runs a backward pass, and the gradient must come back zero although
+    the previous evaluation left a nonzero one (the only case in which the
+    server still zero-fills before the passes)."""
+    from cpde_amd import workloads as W
+    g = load_golden('poisson')
+    pw = W.PoissonWorkload(radial=int(g['radial']), angular=int(g['angular']), boundary=int(g['boundary']))
+    ids = pw.upload(server)
+    _, grads = server.graph_eval(ids['net'], ids['costs'], pw.graph(), gradient=True)
+    assert all(np.abs(x).max() > 0 for x in grads)
+    constant = wire.graph_bytes([(1, 0, 0), (1, 1, 0), (0, 0, 0)], [0.0, 0.0, 5.0], 2)
+    value, grads = server.graph_eval(ids['net'], ids['costs'], constant, gradient=True)
+    assert value == 5.0
+    for x in grads:
+        np.testing.assert_array_equal(x, np.zeros_like(x))
+
+
 def test_value_dependent_graph_multipliers(server):
     """root = leaf0 / leaf1 + log(leaf0) + leaf1 ** 1.5: the leaf multipliers are
     known only after the forward passes, so every leaf runs a second, backward
