@@ -233,6 +233,7 @@ static FusedTuning tuning(int rows, int width, int compute_units) {
     t.max_split_adjoint = std::max(1, env_int("CPDE_NET_SPLIT_ADJOINT", t.max_split_adjoint));
     t.forward_blocks = std::max(1, env_int("CPDE_NET_FWD_OCC", t.forward_blocks));
     t.backward_blocks = std::max(1, env_int("CPDE_NET_BWD_OCC", t.backward_blocks));
+    t.col_tile = env_int("CPDE_NET_COLTILE", 0);
     return t;
 }
 

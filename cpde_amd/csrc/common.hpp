@@ -224,6 +224,7 @@ struct FusedTuning {
     int max_split = 4;             // lanes per composition, at most
     int max_split_adjoint = 1;     // lanes per adjoint composition, at most
     int forward_blocks = 2, backward_blocks = 2;  // blocks per CU the register budget must allow
+    int col_tile = 0;              // column tile of the network products: 16, 32, or 0 (chosen per shape)
 };
 std::string fused_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning);
 std::string expression_epoch_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning,

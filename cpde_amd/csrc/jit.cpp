@@ -392,6 +392,20 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
     o << "// generated: cPDE layer-fused kernels\n#define CPDE_POINTS " << points_per_block << "\n";
     o << "#define CPDE_NET_POINTS " << net_points_per_block << "\n";
     o << "#define CPDE_STRIDE " << ((widest + 7) / 8 * 8 + 4) << "\n";
+    // Column tile of the network products: 16 (v_mfma_f32_16x16x4f32) when a
+    // block holds one point and every hidden width is a multiple of 16; else 32
+    // (v_mfma_f32_32x32x2f32).  Measured on 2->128^4->1 at 729 points, epoch
+    // kernel: one point per block (orders 5, 6; 21 and 28 rows) 16 is 6 and 2 %
+    // faster, and 35 rows pad to 48 columns instead of 64 (3D order 4: 11 %);
+    // several points per block (orders 2-4) 32 is 5-15 % faster.
+    {
+        bool hidden16 = true;
+        for (int l = 1; l + 1 < L; ++l) hidden16 = hidden16 && neurons[l] % 16 == 0;
+        int col_tile = net_points_per_block == 1 ? 16 : 32;
+        if (tuning.col_tile == 16 || tuning.col_tile == 32) col_tile = tuning.col_tile;
+        if (!hidden16) col_tile = 32;
+        o << "#define CPDE_COL_TILE " << col_tile << "\n";
+    }
     o << "#define CPDE_MAX_SPLIT " << tuning.max_split << "\n";
     o << "#define CPDE_MAX_SPLIT_ADJOINT " << tuning.max_split_adjoint << "\n";
     // row splits of the compositions used by the network-fused kernels

@@ -58,6 +58,29 @@ def test_epoch_against_reference_server(device, path, name):
     run.close()
 
 
+@pytest.mark.parametrize('col_tile', [16, 32])
+@pytest.mark.parametrize('name', ['fourier_order6', 'fourier3d_reduced', 'large_reduced'])
+def test_network_products_column_tiles(device, monkeypatch, name, col_tile):
+    """The network-fused products on 16-column (v_mfma_f32_16x16x4f32) and
+    32-column (v_mfma_f32_32x32x2f32) tiles, each forced on shapes where the
+    other is the default (28 rows: 32 columns either way; 35 rows: 48 or 64),
+    against the reference server's epoch at the order-6 bars."""
+    monkeypatch.setenv('CPDE_FUSED', '2')
+    monkeypatch.setenv('CPDE_NET_COLTILE', str(col_tile))
+    g = load_golden(name)
+    wl = golden_workload(g)
+    print(f'[case] {name} col_tile={col_tile} R={wl.rows} P={wl.size}', flush=True)
+    run = hip.MatchingRun(device, wl)
+    run.step()
+    device.synchronize()
+    assert abs(run.loss() / g['loss'] - 1) < 1e-4
+    for t, grad in enumerate(run.gradients()):
+        assert check_gradient(g, t, grad, 1e-3) < 1e-3
+    out = outputs_of(device, run, wl)
+    assert max(rel_l2(out[r], g['outputs'][r]) for r in range(wl.rows)) < 1e-3
+    run.close()
+
+
 @pytest.mark.parametrize('name', ['tiny_order6', 'tiny_3var_order4'])
 def test_first_rprop_step_against_reference_server(device, path, name):
     g = load_golden(name)
