@@ -87,7 +87,8 @@ def warm_jit():
                                   (W.full_schema(3, 4), [3, 128, 128, 128, 128, 128, 1], 32768),
                                   (W.full_schema(2, 6), [2, 256, 256, 256, 256, 1], 65536),
                                   (W.closed_schema(2, [(2, 0), (0, 2)]), [2, 64, 64, 64, 1], 4096),
-                                  (W.closed_schema(2, []), [2, 64, 64, 64, 1], 256)]:
+                                  (W.closed_schema(2, []), [2, 64, 64, 64, 1], 256),
+                                  (W.full_schema(2, 6), [2, 32, 32, 1], 40)]:  # __graft_entry__.smoke
         hip.jit_prepare(table, neurons, width, 256, ARCH)
 
 
