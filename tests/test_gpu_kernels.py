@@ -151,3 +151,60 @@ def test_epoch_matches_oracle(device, path, order, neurons, points, chunk):
         print(f'[result] transition {t} gradient rel-L2 {e:.3e}', flush=True)
         assert e < 1e-3
     run.close()
+
+
+@pytest.mark.parametrize('order,neurons,points,chunk,one_pass', [
+    (4, [2, 32, 24, 3], 45, 0, True),
+    (4, [2, 32, 24, 3], 45, 20, False),
+    (3, [3, 16, 16, 2], 33, 16, True),
+    (6, [2, 32, 32, 8], 20, 0, True),
+    (6, [3, 24, 16, 2], 10, 0, True),     # 84 rows: beyond the network kernels' 64
+])
+def test_multi_output_epoch_matches_oracle(device, path, order, neurons, points, chunk, one_pass):
+    """Networks with several outputs (up to the eight the output layer takes):
+    per-channel targets and row weights in the wire layouts [row][sample][channel]
+    and [row][weight sample][channel], ragged last chunks, one-pass and separate
+    launches."""
+    print(f'[case] multi-output path={path} order={order} neurons={neurons} points={points} chunk={chunk} '
+          f'one_pass={one_pass}', flush=True)
+    V, n_out = neurons[0], neurons[-1]
+    schema = W.full_schema(V, order)
+    R = len(schema)
+    pts = np.random.default_rng(11).uniform(0, 1, (points, V))
+    target = np.stack([W.fourier_target(pts, schema, *W.fourier_modes(V, 3, 2, 40 + c)) for c in range(n_out)],
+                      axis=2).astype(np.float32)                                   # (R, points, n_out)
+    row_weights = (1.0 / target.var(axis=1, dtype=np.float64))[:, None, :].astype(np.float32)   # (R, 1, n_out)
+    x = np.ascontiguousarray(W.input_stack(pts, schema).transpose(0, 2, 1), np.float32)      # (R, points, V)
+    init = W.xavier_weights(neurons, 21)
+    width = chunk or points
+    net = hip.Net(device, neurons, W.linear_flags(neurons), init)
+    plan = hip.Plan(net, schema, width, True)
+    bufs = [hip.Buffer.of(device, a) for a in
+            (x, target, np.arange(R, dtype=np.int32), row_weights)]
+    data, tbuf, trows, wts = bufs
+    rows = np.arange(R, dtype=np.int32)
+    device.costs_begin(1)
+    for offset in range(0, points, width):
+        valid = min(width, points - offset)
+        plan.activate(data, points, rows, offset, valid)
+        if one_pass:
+            plan.epoch_matching(tbuf, points, trows, wts, 1, offset, valid, 0, True, offset > 0)
+        else:
+            plan.forward()
+            plan.matching(tbuf, points, trows, wts, 1, offset, valid, 0, True, True)
+            plan.backward(offset > 0)
+    device.synchronize()
+    loss = device.scalars(1, 0)[0][0].value
+    grads = [net.gradient(t) for t in range(len(neurons) - 1)]
+    ref_loss, ref_grads, _ = oracle.matching_epoch(neurons, W.linear_flags(neurons), init, schema, x, target,
+                                                   row_weights, chunk=chunk)
+    print(f'[result] loss {loss!r} oracle {ref_loss!r}', flush=True)
+    assert abs(loss / ref_loss - 1) < 1e-4
+    for t, (g, r) in enumerate(zip(grads, ref_grads)):
+        e = rel_l2(g, r)
+        print(f'[result] transition {t} gradient rel-L2 {e:.3e}', flush=True)
+        assert e < 1e-3
+    for b in bufs:
+        b.free()
+    plan.destroy()
+    net.destroy()
