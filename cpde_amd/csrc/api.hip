@@ -75,14 +75,20 @@ void Device::reserve_scalars(int costs, int layers) {
     if (costs == cost_capacity && layers == grad_capacity && scalar_block) return;
     HIP_CHECK(hipStreamSynchronize(stream));
     const size_t cost_bytes = (sizeof(CostStats) * size_t(costs) + 255) / 256 * 256;
-    const size_t bytes = cost_bytes + sizeof(GradStats) * size_t(layers);
+    const size_t grad_bytes = (sizeof(GradStats) * size_t(layers) + 255) / 256 * 256;
+    const size_t bytes = cost_bytes + grad_bytes + sizeof(cpde_graph_summary);
     void *block = nullptr, *host = nullptr;
     HIP_CHECK(hipMalloc(&block, bytes));
     HIP_CHECK(hipHostMalloc(&host, bytes, hipHostMallocDefault));
     CostStats* c = static_cast<CostStats*>(block);
     GradStats* g = reinterpret_cast<GradStats*>(static_cast<char*>(block) + cost_bytes);
+    auto* summary = reinterpret_cast<cpde_graph_summary*>(static_cast<char*>(block) + cost_bytes + grad_bytes);
     if (cost_capacity) HIP_CHECK(hipMemcpy(c, cost_totals, sizeof(CostStats) * cost_capacity, hipMemcpyDeviceToDevice));
     if (grad_capacity) HIP_CHECK(hipMemcpy(g, grad_totals, sizeof(GradStats) * grad_capacity, hipMemcpyDeviceToDevice));
+    const cpde_graph_summary none{0.0, -1, 0};
+    if (graph_summary)
+        HIP_CHECK(hipMemcpy(summary, graph_summary, sizeof(cpde_graph_summary), hipMemcpyDeviceToDevice));
+    else HIP_CHECK(hipMemcpy(summary, &none, sizeof(cpde_graph_summary), hipMemcpyHostToDevice));
     if (scalar_block) HIP_CHECK(hipFree(scalar_block));
     if (host_block) HIP_CHECK(hipHostFree(host_block));
     scalar_block = block;
@@ -91,6 +97,9 @@ void Device::reserve_scalars(int costs, int layers) {
     grad_totals = g;
     host_costs = static_cast<CostStats*>(host);
     host_grads = reinterpret_cast<GradStats*>(static_cast<char*>(host) + cost_bytes);
+    graph_summary = summary;
+    host_graph_summary = reinterpret_cast<cpde_graph_summary*>(static_cast<char*>(host) + cost_bytes + grad_bytes);
+    scalar_bytes = bytes;
     cost_capacity = costs;
     grad_capacity = layers;
 }
@@ -633,7 +642,6 @@ int cpde_device_open(int ordinal, cpde_device** out) {
         d->compute_units = prop.multiProcessorCount;
         HIP_CHECK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
         HIP_CHECK(hipMalloc(&d->cost_blocks, sizeof(CostStats) * kMaxCostBlocks));
-        HIP_CHECK(hipMalloc(&d->grad_blocks, sizeof(GradStats) * kMaxCostBlocks));
         for (auto& e : d->marks) HIP_CHECK(hipEventCreate(&e));
         d->reserve_scalars(8, 8);
         HIP_CHECK(hipHostMalloc(&d->host_summary, sizeof(cpde_graph_summary), hipHostMallocDefault));
@@ -648,7 +656,6 @@ int cpde_device_close(cpde_device* dev) {
         for (auto& e : dev->marks) (void)hipEventDestroy(e);
         for (auto& e : dev->event_pool) (void)hipEventDestroy(e);
         (void)hipFree(dev->cost_blocks);
-        (void)hipFree(dev->grad_blocks);
         (void)hipFree(dev->scalar_block);
         (void)hipHostFree(dev->host_block);
         (void)hipHostFree(dev->host_summary);
@@ -1003,8 +1010,12 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
                                 cpde_graph_summary* summary_out) {
     return guarded([&] {
         require(costs <= dev->cost_capacity && layers <= dev->grad_capacity, "scalar slots out of range");
-        require((summary == nullptr) == (summary_out == nullptr), "graph summary source and destination go together");
-        if (costs && layers) {  // one copy over both (the block keeps them in this order)
+        require(summary == nullptr || summary_out != nullptr, "graph summary without a destination");
+        const bool own_summary = summary == nullptr && summary_out != nullptr;
+        if (own_summary) {  // one copy over the whole block: costs, gradient totals and the summary slot
+            HIP_CHECK(hipMemcpyAsync(dev->host_block, dev->scalar_block, dev->scalar_bytes, hipMemcpyDeviceToHost,
+                                     dev->stream));
+        } else if (costs && layers) {  // one copy over both (the block keeps them in this order)
             const size_t bytes = size_t(reinterpret_cast<char*>(dev->grad_totals + layers) -
                                         static_cast<char*>(dev->scalar_block));
             HIP_CHECK(hipMemcpyAsync(dev->host_block, dev->scalar_block, bytes, hipMemcpyDeviceToHost, dev->stream));
@@ -1026,6 +1037,7 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
         }
         if (layers && gradient_out) std::memcpy(gradient_out, dev->host_grads, sizeof(GradStats) * layers);
         if (summary) *summary_out = *dev->host_summary;
+        if (own_summary) *summary_out = *dev->host_graph_summary;
     });
 }
 
@@ -1158,7 +1170,8 @@ int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int coun
                        int gradient) {
     return guarded([&] {
         require(leaves <= dev->cost_capacity, "graph leaves exceed cost slots");
-        launch_graph(*dev, nodes, count, root, leaves, values, adjoints, multipliers, active, summary, gradient != 0);
+        launch_graph(*dev, nodes, count, root, leaves, values, adjoints, multipliers, active,
+                     summary ? summary : dev->graph_summary, gradient != 0);
     });
 }
 

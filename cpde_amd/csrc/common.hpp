@@ -145,9 +145,9 @@ struct Device {
     hipStream_t stream = nullptr;
     // reduction workspace (cuda/reduction_kernels.cuh:101-178)
     CostStats* cost_blocks = nullptr;   // kMaxCostBlocks
-    GradStats* grad_blocks = nullptr;   // kMaxCostBlocks
     // cost and gradient totals in one device block, [cost_capacity] then
-    // [grad_capacity], mirrored by one pinned host block: one copy downloads both
+    // [grad_capacity] then the graph-summary slot, mirrored by one pinned host
+    // block: one copy downloads them
     void* scalar_block = nullptr;
     void* host_block = nullptr;
     CostStats* cost_totals = nullptr;   // cost_capacity, in scalar_block
@@ -155,6 +155,11 @@ struct Device {
     CostStats* host_costs = nullptr;    // in host_block
     GradStats* host_grads = nullptr;
     cpde_graph_summary* host_summary = nullptr;  // pinned: one graph summary
+    // the device's own graph-summary slot, after the gradient totals in
+    // scalar_block (and its mirror in host_block): one copy downloads all three
+    cpde_graph_summary* graph_summary = nullptr;
+    cpde_graph_summary* host_graph_summary = nullptr;
+    size_t scalar_bytes = 0;
     int cost_capacity = 0, grad_capacity = 0;
     hipEvent_t marks[8] = {};
     // tracing

@@ -954,7 +954,7 @@ __device__ __forceinline__ GradStats combine_grad(GradStats a, const GradStats& 
 }
 
 __device__ GradStats block_reduce_grad(GradStats v) {
-    __shared__ GradStats waves[4];
+    __shared__ GradStats waves[16];
     for (int off = 32; off > 0; off >>= 1) {
         GradStats o;
         o.squared_norm = __shfl_down(v.squared_norm, off, 64);
@@ -972,23 +972,24 @@ __device__ GradStats block_reduce_grad(GradStats v) {
     return r;
 }
 
-// Statistics of several transitions' gradients in two launches: blocks
-// [block_begin[t], block_begin[t+1]) stride transition t's entries, then one
-// block per transition combines its partials in block order.
+// Statistics of several transitions' gradients in one launch (a host round
+// trip per launch is what an epoch of small costs waits on): block t strides
+// transition t's entries with 1,024 lanes, each lane in index order, then the
+// fixed block reduction -- one order whatever the scheduling.
 struct GradGroupArgs {
     const float* g[kMaxTransitions];
     int count[kMaxTransitions];
-    int block_begin[kMaxTransitions + 1];
     int transitions;
 };
 
-__global__ __launch_bounds__(256) void grad_blocks_kernel(GradGroupArgs a, GradStats* __restrict__ partials) {
-    int t = 0;
-    while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
-    const int local = int(blockIdx.x) - a.block_begin[t], blocks = a.block_begin[t + 1] - a.block_begin[t];
+constexpr int kGradThreads = 1024;
+
+__global__ __launch_bounds__(kGradThreads) void grad_stats_kernel(GradGroupArgs a, GradStats* __restrict__ totals) {
+    const int t = blockIdx.x;
     const float* __restrict__ g = a.g[t];
     GradStats acc{0.0, 0.0, 0ull, INT_MAX, 0};
-    for (int i = local * blockDim.x + threadIdx.x; i < a.count[t]; i += blockDim.x * blocks) {
+#pragma unroll 4
+    for (int i = threadIdx.x; i < a.count[t]; i += kGradThreads) {
         const double v = g[i];
         if (!isfinite(v)) {
             ++acc.nonfinite;
@@ -1000,32 +1001,17 @@ __global__ __launch_bounds__(256) void grad_blocks_kernel(GradGroupArgs a, GradS
         }
     }
     acc = block_reduce_grad(acc);
-    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
-}
-
-__global__ __launch_bounds__(256) void grad_finish_kernel(GradGroupArgs a, const GradStats* __restrict__ partials,
-                                                          GradStats* __restrict__ totals) {
-    const int t = blockIdx.x;
-    GradStats v{0.0, 0.0, 0ull, INT_MAX, 0};
-    for (int i = a.block_begin[t] + threadIdx.x; i < a.block_begin[t + 1]; i += blockDim.x)
-        v = combine_grad(v, partials[i]);
-    v = block_reduce_grad(v);
-    if (threadIdx.x == 0) totals[t] = v;
+    if (threadIdx.x == 0) totals[t] = acc;
 }
 
 void launch_grad_stats(Device& d, const float* const* g, const int* counts, int transitions, int first_slot) {
     GradGroupArgs a{};
     a.transitions = transitions;
-    a.block_begin[0] = 0;
-    const int cap = std::max(1, kMaxCostBlocks / transitions);
     for (int t = 0; t < transitions; ++t) {
         a.g[t] = g[t];
         a.count[t] = counts[t];
-        a.block_begin[t + 1] = a.block_begin[t] + std::min(cap, cost_blocks_for(counts[t]));
     }
-    hipLaunchKernelGGL(grad_blocks_kernel, a.block_begin[transitions], 256, 0, d.stream, a, d.grad_blocks);
-    HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(grad_finish_kernel, transitions, 256, 0, d.stream, a, d.grad_blocks, d.grad_totals + first_slot);
+    hipLaunchKernelGGL(grad_stats_kernel, transitions, kGradThreads, 0, d.stream, a, d.grad_totals + first_slot);
     HIP_CHECK(hipGetLastError());
 }
 

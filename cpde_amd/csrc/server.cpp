@@ -503,7 +503,9 @@ struct GraphRecord {
     std::vector<cpde_scalar_node> nodes;
     int root = 0, leaves = 0;
     std::vector<Known> schedule;
-    DeviceBuffer dev_nodes, values, adjoints, multipliers, active, summary, fixed;
+    // the summary is written into the device's own slot (cpde_graph_execute with
+    // a null summary) and arrives with the scalar download
+    DeviceBuffer dev_nodes, values, adjoints, multipliers, active, fixed;
     cpde_graph_summary host{0, -1, 0};
 
     void read(cpde_device* dev, Frame& b, int leaf_count) {
@@ -530,7 +532,6 @@ struct GraphRecord {
         adjoints.reset(dev, nodes.size() * sizeof(double));
         active.reset(dev, nodes.size() * sizeof(int));
         multipliers.reset(dev, std::max(1, leaves) * sizeof(double));
-        summary.upload(dev, std::vector<cpde_graph_summary>{host});
         schedule = schedule_leaves(nodes, root, leaves);
         std::vector<double> f(std::max(1, leaves), 0.0);
         for (int i = 0; i < leaves; ++i)
@@ -785,7 +786,7 @@ void Server::download(int costs, int layers, std::vector<cpde_cost_stats>& cs, s
     gs.resize(std::max(layers, 1));
     if (graph)
         call(cpde_scalars_download_graph(dev_, costs, cs.data(), layers, gs.data(),
-                                         graph->summary.as<cpde_graph_summary>(), &graph->host));
+                                         nullptr, &graph->host));
     else
         call(cpde_scalars_download(dev_, costs, cs.data(), layers, gs.data()));
     cs.resize(costs);
@@ -860,7 +861,7 @@ void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
     call(cpde_graph_execute(dev_, graph.dev_nodes.as<cpde_scalar_node>(), int(graph.nodes.size()), graph.root,
                             int(ids.size()), graph.values.as<double>(), graph.adjoints.as<double>(),
                             graph.multipliers.as<double>(), graph.active.as<int>(),
-                            graph.summary.as<cpde_graph_summary>(), backward ? 1 : 0));
+                            nullptr, backward ? 1 : 0));
     if (backward) {
         if (reuse >= 0)
             pass(n, cost(ids[reuse]), reuse, first,

@@ -180,7 +180,9 @@ int cpde_scalars_download(cpde_device* dev, int costs, cpde_cost_stats* cost_out
 /* The same, plus a scalar graph's summary (device, written by cpde_graph_execute)
  * in the same synchronisation: one host round trip per graph epoch, as the
  * reference queues the graph copy before its scalar download
- * (cuda/cpde_server.cu:317, cuda/reduction_kernels.cuh:171-177). */
+ * (cuda/cpde_server.cu:317, cuda/reduction_kernels.cuh:171-177).  summary NULL
+ * (summary_out not NULL): the device's own summary slot, downloaded in the same
+ * copy as the cost and gradient slots. */
 int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
                                 cpde_gradient_stats* gradient_out, const cpde_graph_summary* summary,
                                 cpde_graph_summary* summary_out);
@@ -225,7 +227,8 @@ int cpde_epoch_expression(cpde_plan* plan, cpde_program* program, const double* 
                           const double* quadrature_weights, int samples, int offset, int valid,
                           const double* multiplier, void* scratch, int cost_index, int collect, int accumulate);
 /* cost_graph::execute (cuda/cost_graph.cuh:6-27) on one lane: reads cost slots,
- * writes values/adjoints/multipliers/active (device) and the summary (device). */
+ * writes values/adjoints/multipliers/active (device) and the summary (device;
+ * NULL: the device's own summary slot, see cpde_scalars_download_graph). */
 int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int count, int root, int leaves,
                        double* values, double* adjoints, double* multipliers, int* active,
                        cpde_graph_summary* summary, int gradient);
