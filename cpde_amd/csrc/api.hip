@@ -812,6 +812,12 @@ int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, i
         p->tables = build_tables(rows, variables, table);
         for (int l = 0; l < net->layers; ++l)
             require(double(width) * rows * net->neurons[l] < double(1ull << 40), "context exceeds device capacity");
+        // kernels index a chunk's (point, row) and (point, neuron) pairs, and
+        // the weight gradient its R x width columns, in 32 bits
+        require(double(width) * rows < double(1 << 30), "chunk too large: rows x width must stay below 2^30");
+        for (int l = 0; l < net->layers; ++l)
+            require(double(width) * net->neurons[l] < double(1 << 30),
+                    "chunk too large: width x neurons must stay below 2^30");
         std::vector<int> blob = p->tables.words;
         blob.insert(blob.end(), p->tables.fwd_offset.begin(), p->tables.fwd_offset.end());
         HIP_CHECK(hipMalloc(&p->dev_tables, blob.size() * sizeof(int)));

@@ -1111,8 +1111,11 @@ struct OptimizerArgs {
     float* WT[kMaxTransitions];  // row-major copy of the weights, kept current by RPROP and Adam
     int NO[kMaxTransitions], NI[kMaxTransitions];
     int begin[kMaxTransitions + 1];
+    int block_begin[kMaxTransitions + 1];  // blocks of kOptimizerThreads entries, per transition
     int transitions;
 };
+
+constexpr int kOptimizerThreads = 256;
 
 // Entry j = o + NO*i of a weight block into its row-major copy (bias column i = NI excluded).
 __device__ __forceinline__ void copy_transposed(const OptimizerArgs& a, int t, int j, float w) {
@@ -1120,17 +1123,19 @@ __device__ __forceinline__ void copy_transposed(const OptimizerArgs& a, int t, i
     if (i < a.NI[t]) a.WT[t][i + a.NI[t] * o] = w;
 }
 
-__device__ __forceinline__ int find_transition(const OptimizerArgs& a, int i) {
-    int t = 0;
-    while (t + 1 < a.transitions && i >= a.begin[t + 1]) ++t;
-    return t;
+// Entry j of transition t for this lane: each block lies within one
+// transition, so t and its pointers are uniform (scalar loads).
+__device__ __forceinline__ bool entry_of(const OptimizerArgs& a, int& t, int& j) {
+    t = 0;
+    while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
+    j = (int(blockIdx.x) - a.block_begin[t]) * kOptimizerThreads + int(threadIdx.x);
+    return j < a.begin[t + 1] - a.begin[t];
 }
 
 // Resile_k (cuda/derivative_kernels_v4.cu:752-778), sign tests on float products.
-__global__ void rprop_kernel(OptimizerArgs a) {
-    const int total = a.begin[a.transitions];
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += blockDim.x * gridDim.x) {
-        const int t = find_transition(a, i), j = i - a.begin[t];
+__global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs a) {
+    int t, j;
+    if (entry_of(a, t, j)) {
         float* W = a.W[t] + j;
         float* step = a.S[t] + j;
         float* ga = a.Ga[t] + j;
@@ -1139,28 +1144,31 @@ __global__ void rprop_kernel(OptimizerArgs a) {
         const float prod = __fmul_rn(g, gi);
         float s = *step;
         if (prod > 0) s *= 1.2f;
-        const float nW = *W - copysignf(s, g);
+        const float w = *W;
+        const float nW = w - copysignf(s, g);
+        float kept = w;
         if (prod < 0) {
-            *W = *W + copysignf(s, gi);
+            kept = w + copysignf(s, gi);
             s *= 0.5f;
             *ga = 0.0f;
         } else if (g != 0.0f) {
-            if (fabsf(nW) <= 20.0f) *W = nW;
+            if (fabsf(nW) <= 20.0f) kept = nW;
             else {
                 s = 0.1f;
                 *ga = 0.0f;
             }
         }
+        *W = kept;
         *step = s;
-        copy_transposed(a, t, j, *W);
+        copy_transposed(a, t, j, kept);
     }
 }
 
 // ADAM_k (cuda/derivative_kernels_v4.cu:780-799); M in S, V in the inactive buffer.
-__global__ void adam_kernel(OptimizerArgs a, float lr, float beta1, float beta2, float beta1t, float beta2t) {
-    const int total = a.begin[a.transitions];
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += blockDim.x * gridDim.x) {
-        const int t = find_transition(a, i), j = i - a.begin[t];
+__global__ __launch_bounds__(kOptimizerThreads) void adam_kernel(OptimizerArgs a, float lr, float beta1, float beta2,
+                                                                  float beta1t, float beta2t) {
+    int t, j;
+    if (entry_of(a, t, j)) {
         const float g = a.Ga[t][j];
         float m = a.S[t][j], v = a.Gi[t][j];
         m = __fadd_rn(__fmul_rn(beta1, m), __fmul_rn(1 - beta1, g));
@@ -1168,17 +1176,18 @@ __global__ void adam_kernel(OptimizerArgs a, float lr, float beta1, float beta2,
         a.S[t][j] = m;
         a.Gi[t][j] = v;
         const float mh = m / (1 - beta1t), vh = v / (1 - beta2t);
-        const float nW = float(double(a.W[t][j]) - double(lr * mh) / (double(sqrtf(vh)) + 1e-8));
-        if (fabsf(nW) <= 20.0f) a.W[t][j] = nW;
-        copy_transposed(a, t, j, a.W[t][j]);
+        const float w = a.W[t][j];
+        const float nW = float(double(w) - double(lr * mh) / (double(sqrtf(vh)) + 1e-8));
+        const float kept = fabsf(nW) <= 20.0f ? nW : w;
+        a.W[t][j] = kept;
+        copy_transposed(a, t, j, kept);
     }
 }
 
 // Set_Resile_k / Reset_Resile_k (cuda/derivative_kernels_v4.cu:801-832).
-__global__ void steps_kernel(OptimizerArgs a, float value, int floor_mode) {
-    const int total = a.begin[a.transitions];
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += blockDim.x * gridDim.x) {
-        const int t = find_transition(a, i), j = i - a.begin[t];
+__global__ __launch_bounds__(kOptimizerThreads) void steps_kernel(OptimizerArgs a, float value, int floor_mode) {
+    int t, j;
+    if (entry_of(a, t, j)) {
         if (!floor_mode || a.S[t][j] < value) {
             a.S[t][j] = value;
             a.Ga[t][j] = 0.0f;
@@ -1194,6 +1203,7 @@ static void for_transition_groups(Net& net, F launch) {
         OptimizerArgs a{};
         a.transitions = std::min(kMaxTransitions, T - first);
         a.begin[0] = 0;
+        a.block_begin[0] = 0;
         for (int k = 0; k < a.transitions; ++k) {
             const int t = first + k;
             const int act = net.active[t], inact = act == 1 ? 2 : 1;
@@ -1205,16 +1215,16 @@ static void for_transition_groups(Net& net, F launch) {
             a.NO[k] = net.neurons[t + 1];
             a.NI[k] = net.neurons[t];
             a.begin[k + 1] = a.begin[k] + net.param_count(t);
+            a.block_begin[k + 1] = a.block_begin[k] + (net.param_count(t) + kOptimizerThreads - 1) / kOptimizerThreads;
         }
-        const int blocks = std::max(1, std::min(1024, (a.begin[a.transitions] + 255) / 256));
-        launch(a, blocks);
+        launch(a, a.block_begin[a.transitions]);
     }
 }
 
 void launch_rprop(Device& d, Net& net) {
     for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
         TraceScope trace(d, kTraceOptimizer, 28.0 * a.begin[a.transitions]);  // 4 reads, 3 writes per entry
-        hipLaunchKernelGGL(rprop_kernel, blocks, 256, 0, d.stream, a);
+        hipLaunchKernelGGL(rprop_kernel, blocks, kOptimizerThreads, 0, d.stream, a);
         HIP_CHECK(hipGetLastError());
     });
     for (auto& act : net.active) act = act == 1 ? 2 : 1;
@@ -1225,7 +1235,7 @@ void launch_adam(Device& d, Net& net, int step, float lr) {
     const float b1 = 0.9f, b2 = 0.999f;
     const float b1t = std::pow(b1, float(step)), b2t = std::pow(b2, float(step));
     for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
-        hipLaunchKernelGGL(adam_kernel, blocks, 256, 0, d.stream, a, lr, b1, b2, b1t, b2t);
+        hipLaunchKernelGGL(adam_kernel, blocks, kOptimizerThreads, 0, d.stream, a, lr, b1, b2, b1t, b2t);
         HIP_CHECK(hipGetLastError());
     });
     net.wt_current = true;
@@ -1233,14 +1243,14 @@ void launch_adam(Device& d, Net& net, int step, float lr) {
 
 void launch_set_steps(Device& d, Net& net, float value) {
     for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
-        hipLaunchKernelGGL(steps_kernel, blocks, 256, 0, d.stream, a, value, 0);
+        hipLaunchKernelGGL(steps_kernel, blocks, kOptimizerThreads, 0, d.stream, a, value, 0);
         HIP_CHECK(hipGetLastError());
     });
 }
 
 void launch_restore_steps(Device& d, Net& net, float floor_value) {
     for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
-        hipLaunchKernelGGL(steps_kernel, blocks, 256, 0, d.stream, a, floor_value, 1);
+        hipLaunchKernelGGL(steps_kernel, blocks, kOptimizerThreads, 0, d.stream, a, floor_value, 1);
         HIP_CHECK(hipGetLastError());
     });
 }

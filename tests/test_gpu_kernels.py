@@ -208,3 +208,16 @@ def test_multi_output_epoch_matches_oracle(device, path, order, neurons, points,
         b.free()
     plan.destroy()
     net.destroy()
+
+
+def test_oversized_chunk_is_rejected(device):
+    """A chunk whose (point, row) pairs would overflow the kernels' 32-bit
+    indexing is refused at plan creation, before any allocation, and the
+    network stays usable."""
+    neurons = [2, 8, 1]
+    net = hip.Net(device, neurons, W.linear_flags(neurons), W.xavier_weights(neurons, 1))
+    with pytest.raises(hip.CpdeError, match='chunk too large'):
+        hip.Plan(net, W.full_schema(2, 6), 1 << 26, True)
+    plan = hip.Plan(net, W.full_schema(2, 6), 64, True)
+    plan.destroy()
+    net.destroy()
