@@ -159,6 +159,8 @@ def test_epoch_matches_oracle(device, path, order, neurons, points, chunk):
     (3, [3, 16, 16, 2], 33, 16, True),
     (6, [2, 32, 32, 8], 20, 0, True),
     (6, [3, 24, 16, 2], 10, 0, True),     # 84 rows: beyond the network kernels' 64
+    (2, [2, 320, 2], 20, 0, True),        # hidden width beyond the network kernels' 256
+    (1, [2, 1040, 1], 8, 0, True),        # and beyond the layer-fused kernels' 1024
 ])
 def test_multi_output_epoch_matches_oracle(device, path, order, neurons, points, chunk, one_pass):
     """Networks with several outputs (up to the eight the output layer takes):
