@@ -223,16 +223,32 @@ struct NetArgsHost {
 };
 
 // Tuning of the fused kernels for a schema of `rows` derivative rows over chunks
-// of `width` points (0: unknown) on `compute_units` CUs.  The network-fused
-// kernels put as many points in a workgroup as fill one 32-column matrix-core
-// tile (one point when the rows alone need a tile or more), but no more than
-// spread the chunk over about one workgroup per CU.
-static FusedTuning tuning(int rows, int width, int compute_units) {
+// of `width` points (0: unknown) on `compute_units` CUs, for a network of
+// `neurons`.  The network-fused kernels put as many points in a workgroup as
+// fill one 32-column matrix-core tile (one point when the rows alone need a
+// tile or more), but no more than spread the chunk over about one workgroup
+// per CU.  Long grids of many-row points take two points per workgroup
+// instead: each weight load feeds both, 2R rows pad to whole 16-column tiles
+// (35 rows: 80 columns for two points against 48 for one), and the product
+// tile is written over its operand tile, so a workgroup needs no more LDS
+// than one point did.  That needs whole columns per composition lane (hidden
+// widths above 64) and hidden widths that are multiples of 16.  Measured:
+// 3->128^5->1 over 32,768 points 6.87 -> 5.79 ms per epoch, 2->256^4->1 over
+// 65,536-point chunks 102.8 -> 95.4 ms; at 729 points (config 2, under one
+// workgroup per CU either way) two points per workgroup were slower.
+static FusedTuning tuning(int rows, int width, int compute_units, const std::vector<int>& neurons) {
     FusedTuning t;
     int npb = rows <= 16 ? 32 / rows : 1;
     if (width > 0) {
         const int spread = std::max(1, env_int("CPDE_NET_MIN_BLOCKS", compute_units));
         npb = std::max(1, std::min(npb, (width + spread - 1) / spread));
+        bool paired = rows > 16 && width >= 16 * compute_units && neurons.size() >= 3;
+        for (size_t l = 1; l + 1 < neurons.size(); ++l) paired = paired && neurons[l] > 64 && neurons[l] % 16 == 0;
+        if (paired) {
+            npb = 2;
+            t.alias = 1;
+            t.col_tile = 16;
+        }
     }
     t.points_per_block = std::max(1, env_int("CPDE_FUSED_POINTS", t.points_per_block));
     t.net_points_per_block = std::max(1, env_int("CPDE_NET_POINTS", npb));
@@ -242,13 +258,14 @@ static FusedTuning tuning(int rows, int width, int compute_units) {
     t.max_split_adjoint = std::max(1, env_int("CPDE_NET_SPLIT_ADJOINT", t.max_split_adjoint));
     t.forward_blocks = std::max(1, env_int("CPDE_NET_FWD_OCC", t.forward_blocks));
     t.backward_blocks = std::max(1, env_int("CPDE_NET_BWD_OCC", t.backward_blocks));
-    t.col_tile = env_int("CPDE_NET_COLTILE", 0);
+    t.col_tile = env_int("CPDE_NET_COLTILE", t.col_tile);
+    t.alias = env_int("CPDE_NET_ALIAS", t.alias);
     return t;
 }
 
 static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const std::vector<int>& neurons,
                                                int width) {
-    const FusedTuning tune = tuning(t.rows, width, d.compute_units);
+    const FusedTuning tune = tuning(t.rows, width, d.compute_units, neurons);
     const std::string src = fused_source(t, neurons, tune);
     for (auto& kv : d.fused_modules)
         if (kv.first == src) return kv.second;
@@ -551,7 +568,7 @@ static hipFunction_t expression_epoch(Plan& p, const Program& program) {
     for (auto& kv : p.expression_epochs)
         if (kv.first == program.id) return kv.second->function;
     Device& d = *p.net->dev;
-    const FusedTuning tune = tuning(p.tables.rows, p.width, d.compute_units);
+    const FusedTuning tune = tuning(p.tables.rows, p.width, d.compute_units, p.net->neurons);
     const std::string src = expression_epoch_source(p.tables, p.net->neurons, tune, program.source);
     std::shared_ptr<ExpressionEpoch> e;
     for (auto& kv : d.expression_epochs)
@@ -1220,9 +1237,8 @@ int cpde_jit_prepare(int rows, int variables, const int* table, int layers, cons
         const Tables t = build_tables(rows, variables, table);
         std::string text;
         try {
-            compile_module(fused_source(t, std::vector<int>(neurons, neurons + layers),
-                                        tuning(t.rows, width, compute_units)),
-                           arch, &text);
+            const std::vector<int> n(neurons, neurons + layers);
+            compile_module(fused_source(t, n, tuning(t.rows, width, compute_units, n)), arch, &text);
         } catch (...) {
             if (log && log_capacity) std::snprintf(log, log_capacity, "%s", text.c_str());
             throw;

@@ -228,6 +228,7 @@ struct FusedTuning {
     int net_points_per_block = 1;  // network-fused kernels
     int max_split = 4;             // lanes per composition, at most
     int max_split_adjoint = 1;     // lanes per adjoint composition, at most
+    int alias = 0;                 // network kernels: products write over their operand tile (one LDS tile)
     int forward_blocks = 2, backward_blocks = 2;  // blocks per CU the register budget must allow
     int col_tile = 0;              // column tile of the network products: 16, 32, or 0 (chosen per shape)
 };

@@ -381,6 +381,28 @@ std::vector<char> compile_module(const std::string& source, const std::string& a
     return code;
 }
 
+// Whether every hidden layer's forward and adjoint compositions have one lane
+// per (point, neuron) column (the row split of fused.hip.in's split_of is 1).
+static bool alias_tiles(const std::vector<int>& neurons, const FusedTuning& tuning) {
+    for (size_t l = 1; l + 1 < neurons.size(); ++l) {
+        const int lanes = tuning.net_points_per_block * neurons[l];
+        const int G = lanes * 4 <= 256 ? 4 : (lanes * 2 <= 256 ? 2 : 1);
+        if (std::min(G, tuning.max_split) != 1 || std::min(G, tuning.max_split_adjoint) != 1) return false;
+    }
+    return true;
+}
+
+// The network kernels' LDS tiles: the operand tile X and the product tile T,
+// which is X itself under CPDE_ALIAS_TILES.
+static std::string tile_declarations() {
+    return "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
+           "#ifdef CPDE_ALIAS_TILES\n"
+           "    float* const T = X;\n"
+           "#else\n"
+           "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n"
+           "#endif\n";
+}
+
 // Tuning macros, the generated compositions and the fused kernels' device code
 // for a schema and architecture.
 static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<int>& neurons,
@@ -407,6 +429,11 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
         o << "#define CPDE_COL_TILE " << col_tile << "\n";
     }
     o << "#define CPDE_MAX_SPLIT " << tuning.max_split << "\n";
+    // One LDS tile instead of two when every composition has whole columns per
+    // lane (no split): a lane then reads a column's z rows and writes its y
+    // rows in place, and the products wait for every wave's operand reads
+    // before they store.  Half the LDS per workgroup.
+    if (tuning.alias && alias_tiles(neurons, tuning)) o << "#define CPDE_ALIAS_TILES 1\n";
     o << "#define CPDE_MAX_SPLIT_ADJOINT " << tuning.max_split_adjoint << "\n";
     // row splits of the compositions used by the network-fused kernels
     std::vector<int> splits;
@@ -431,9 +458,18 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
 static std::string epoch_body(const std::vector<int>& neurons, const std::string& prefetch, const std::string& cost) {
     const int L = int(neurons.size()), NO = neurons[L - 1];
     std::ostringstream ep;
-    ep << "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
-       << "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n"
+    // S: the cost stage's scratch (matching terms, or a double and an int per
+    // point of an expression), T itself unless T is the operand tile X, which
+    // holds the last hidden layer's values until the output backward
+    const std::string scratch = "(kNNC * " + std::to_string(NO) + " > 4 * kNPB ? kNNC * " + std::to_string(NO) +
+                                " : 4 * kNPB)";
+    ep << tile_declarations()
        << "    __shared__ __attribute__((aligned(16))) float O[2 * kNNC * " << NO << "];\n"
+       << "#ifdef CPDE_ALIAS_TILES\n"
+       << "    __shared__ __attribute__((aligned(16))) float S[" << scratch << "];\n"
+       << "#else\n"
+       << "    float* const S = T;\n"
+       << "#endif\n"
        << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
        << prefetch << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
        << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
@@ -472,9 +508,7 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     for (int t = L - 3; t >= 1; --t)
         bwd << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
     bwd << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
-    const char* tiles =
-        "    __shared__ __attribute__((aligned(16))) float X[kNNC * kS];\n"
-        "    __shared__ __attribute__((aligned(16))) float T[kNNC * kS];\n";
+    const std::string tiles = tile_declarations();
     o << "\nextern \"C\" __global__ __launch_bounds__(256, " << tuning.forward_blocks
       << ") void network_forward_k(NetArgs a, int points) {\n"
       << tiles << fwd.str() << "}\n";
@@ -486,7 +520,7 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
         const std::string prefetch =
             "    const MatchTerm pre = match_prefetch<" + std::to_string(NO) + ">(m, p0, npts);\n";
         const std::string cost = "    net_match<" + std::to_string(NO) + ">(a, m, " + std::to_string(L - 1) +
-                                 ", T, p0, npts, O, O + kNNC * " + std::to_string(NO) + ", pre);\n";
+                                 ", S, p0, npts, O, O + kNNC * " + std::to_string(NO) + ", pre);\n";
         o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
           << ") void network_epoch_k(NetArgs a, MatchArgs m, int points) {\n" << epoch_body(neurons, prefetch, cost)
           << "}\n";
@@ -518,7 +552,7 @@ std::string expression_epoch_source(const Tables& t, const std::vector<int>& neu
     o << "// generated: one-pass epoch of an expression cost\n" << program << "\n#define CPDE_EXPRESSION_EPOCH 1\n";
     emit_prologue(o, t, neurons, tuning);
     const std::string cost = "    net_expression<" + std::to_string(NO) + ">(a, e, " + std::to_string(L - 1) +
-                             ", T, p0, npts, O, O + kNNC * " + std::to_string(NO) + ");\n";
+                             ", S, p0, npts, O, O + kNNC * " + std::to_string(NO) + ");\n";
     o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
       << ") void network_epoch_expression_k(NetArgs a, ExpressionArgs e, int points) {\n" << epoch_body(neurons, "", cost)
       << "}\n";

@@ -58,15 +58,22 @@ def test_epoch_against_reference_server(device, path, name):
     run.close()
 
 
-@pytest.mark.parametrize('col_tile', [16, 32])
+@pytest.mark.parametrize('col_tile', [16, 32, 'paired'])
 @pytest.mark.parametrize('name', ['fourier_order6', 'fourier3d_reduced', 'large_reduced'])
 def test_network_products_column_tiles(device, monkeypatch, name, col_tile):
     """The network-fused products on 16-column (v_mfma_f32_16x16x4f32) and
     32-column (v_mfma_f32_32x32x2f32) tiles, each forced on shapes where the
     other is the default (28 rows: 32 columns either way; 35 rows: 48 or 64),
-    against the reference server's epoch at the order-6 bars."""
+    and the long-grid form ('paired': two points per workgroup on 16-column
+    tiles, the product tile written over its operand tile) forced on these
+    short grids, against the reference server's epoch at the order-6 bars."""
     monkeypatch.setenv('CPDE_FUSED', '2')
-    monkeypatch.setenv('CPDE_NET_COLTILE', str(col_tile))
+    if col_tile == 'paired':
+        for k, v in (('CPDE_NET_COLTILE', '16'), ('CPDE_NET_POINTS', '2'), ('CPDE_NET_ALIAS', '1')):
+            monkeypatch.setenv(k, v)
+    else:
+        monkeypatch.setenv('CPDE_NET_COLTILE', str(col_tile))
+        monkeypatch.setenv('CPDE_NET_ALIAS', '0')
     g = load_golden(name)
     wl = golden_workload(g)
     print(f'[case] {name} col_tile={col_tile} R={wl.rows} P={wl.size}', flush=True)
