@@ -59,7 +59,7 @@ CPU_SAMPLE_MACS = 3.0e9
 # read, 268,435,456 B / 262,144 KiB written.
 COPY_SCALE = (268435456 / (131084.5625 * 1024), 268435456 / (262144 * 1024))
 TRAFFIC_KIB = {
-    'fourier_fit_order6': {'network_epoch': (24140.56, 140381.70), 'gemm_wgrad': (30695.50, 7740.00),
+    'fourier_fit_order6': {'network_epoch': (24141.80, 140462.07), 'gemm_wgrad': (30704.50, 7740.00),
                            'network_backward': (27619.29, 53473.79), 'network_forward': (1483.53, 83919.40)},
 }
 
