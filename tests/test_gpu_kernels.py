@@ -7,6 +7,8 @@ Tolerances (fp32 on both sides, different summation orders):
   * epoch:                  loss rel <= 1e-4, outputs and gradients rel-L2 <= 1e-3
                             (the order-6 bar), typically ~1e-6.
 """
+import functools
+
 import numpy as np
 import pytest
 
@@ -132,6 +134,7 @@ def small_workload(order, neurons, points, seed=5):
     (6, [2, 32, 32, 1], 50, 16),
     (2, [2, 48, 40, 24, 1], 101, 0),
     (4, [2, 16, 1], 64, 25),
+    (5, [2, 80, 96, 1], 4101, 0),   # a long grid: two points per workgroup, one LDS tile, a lone last point
 ])
 def test_epoch_matches_oracle(device, path, order, neurons, points, chunk):
     print(f'[case] epoch path={path} order={order} neurons={neurons} points={points} chunk={chunk}', flush=True)
@@ -141,9 +144,7 @@ def test_epoch_matches_oracle(device, path, order, neurons, points, chunk):
     device.synchronize()
     loss = run.loss()
     grads = run.gradients()
-    ref_loss, ref_grads, _ = oracle.matching_epoch(wl.neurons, wl.linear, wl.init, wl.schema,
-                                                   wl.inputs.transpose(0, 2, 1), wl.target[:, :, None],
-                                                   wl.row_weights[:, None, None], chunk=chunk)
+    ref_loss, ref_grads = oracle_epoch(order, tuple(neurons), points, chunk)
     print(f'[result] loss {loss!r} oracle {ref_loss!r}', flush=True)
     assert abs(loss / ref_loss - 1) < 1e-4
     for t, (g, r) in enumerate(zip(grads, ref_grads)):
@@ -151,6 +152,15 @@ def test_epoch_matches_oracle(device, path, order, neurons, points, chunk):
         print(f'[result] transition {t} gradient rel-L2 {e:.3e}', flush=True)
         assert e < 1e-3
     run.close()
+
+
+@functools.lru_cache(maxsize=None)
+def oracle_epoch(order, neurons, points, chunk):
+    """The oracle's epoch of small_workload, computed once for all kernel families."""
+    wl = small_workload(order, list(neurons), points)
+    loss, grads, _ = oracle.matching_epoch(wl.neurons, wl.linear, wl.init, wl.schema, wl.inputs.transpose(0, 2, 1),
+                                           wl.target[:, :, None], wl.row_weights[:, None, None], chunk=chunk)
+    return loss, grads
 
 
 @pytest.mark.parametrize('order,neurons,points,chunk,one_pass', [
