@@ -1133,7 +1133,11 @@ __device__ __forceinline__ bool entry_of(const OptimizerArgs& a, int& t, int& j)
 }
 
 // Resile_k (cuda/derivative_kernels_v4.cu:752-778), sign tests on float products.
+// The optimizers round every product and sum separately, as the reference's
+// CPU build does: no multiply-add contraction (hipcc contracts by default, and
+// __fmul_rn/__fadd_rn do not prevent it).
 __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs a) {
+#pragma clang fp contract(off)
     int t, j;
     if (entry_of(a, t, j)) {
         float* W = a.W[t] + j;
@@ -1141,7 +1145,7 @@ __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs 
         float* ga = a.Ga[t] + j;
         const float gi = a.Gi[t][j];
         const float g = *ga;
-        const float prod = __fmul_rn(g, gi);
+        const float prod = g * gi;
         float s = *step;
         if (prod > 0) s *= 1.2f;
         const float w = *W;
@@ -1167,12 +1171,13 @@ __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs 
 // ADAM_k (cuda/derivative_kernels_v4.cu:780-799); M in S, V in the inactive buffer.
 __global__ __launch_bounds__(kOptimizerThreads) void adam_kernel(OptimizerArgs a, float lr, float beta1, float beta2,
                                                                   float beta1t, float beta2t) {
+#pragma clang fp contract(off)
     int t, j;
     if (entry_of(a, t, j)) {
         const float g = a.Ga[t][j];
         float m = a.S[t][j], v = a.Gi[t][j];
-        m = __fadd_rn(__fmul_rn(beta1, m), __fmul_rn(1 - beta1, g));
-        v = __fadd_rn(__fmul_rn(beta2, v), __fmul_rn(__fmul_rn(1 - beta2, g), g));
+        m = beta1 * m + (1 - beta1) * g;
+        v = beta2 * v + (1 - beta2) * g * g;
         a.S[t][j] = m;
         a.Gi[t][j] = v;
         const float mh = m / (1 - beta1t), vh = v / (1 - beta2t);

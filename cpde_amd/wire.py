@@ -31,7 +31,12 @@ LEAF, ATTACH = 1, 15
 
 
 class ServerError(RuntimeError):
-    """A kind-1 reply: a validation or numerical error; the server stays usable."""
+    """A kind-1 reply: a validation or numerical error; the server stays usable.
+    ``events`` holds the training event frames that came before it."""
+
+    def __init__(self, message, events=()):
+        super().__init__(message)
+        self.events = list(events)
 
 
 class Writer:
@@ -341,8 +346,10 @@ class Session:
 
     def train(self, net, costs, epochs, method=0, fresh=0, steps=0.0, moments=0, lr=0.0, verbose=0,
               log=1, eval_every=0, outputs=0, save=0, stage='', diagnostics=0, graph=None,
-              restore_every=0, restore_step=0.0):
-        """op 8 (or op 15 with a graph).  Returns the event list and final result."""
+              restore_every=0, restore_step=0.0, on_event=None):
+        """op 8 (or op 15 with a graph).  Returns the event list and final result.
+        ``on_event(session, event)`` is called for every event frame as it
+        arrives (e.g. to send op 99 from there)."""
         w = Writer().put('Q', net).array(costs, 'u8').put('Q', epochs).put('i', method).put('i', fresh)
         w.put('f', steps).put('i', moments).put('f', lr)
         for v in (verbose, log, eval_every, outputs, save):
@@ -358,18 +365,17 @@ class Session:
             while True:
                 kind, r = self.receive()
                 if kind == 1:
-                    raise ServerError(r.string())
+                    raise ServerError(r.string(), events)
                 if kind in (2, 6):
                     ev = dict(kind=kind, completed=r.get('Q'), updates=r.get('Q'), after=r.get('i'),
                               values=r.array('f8'))
                     if kind == 6:
                         ev['total'] = r.get('d')
                     r.end()
-                    events.append(ev)
                 elif kind == 3:
-                    events.append(dict(kind=3, blob=r.data))
+                    ev = dict(kind=3, blob=r.data)
                 elif kind == 4:
-                    events.append(dict(kind=4, cost=r.get('Q'), outputs=r.array('f4')))
+                    ev = dict(kind=4, cost=r.get('Q'), outputs=r.array('f4'))
                     r.end()
                 elif kind == 5:
                     ev = dict(kind=5, epoch=r.get('Q'), updates=r.get('Q'))
@@ -377,7 +383,6 @@ class Session:
                     ev['layers'] = [dict(sq=r.get('d'), max=r.get('d'), nonfinite=r.get('Q'), first=r.get('i'))
                                     for _ in range(n)]
                     r.end()
-                    events.append(ev)
                 elif kind == 0:
                     completed, stopped = r.get('Q'), r.get('i')
                     meta = decode_metadata(Reader(r.take(r.get('Q'))))
@@ -385,6 +390,9 @@ class Session:
                     return dict(completed=completed, stopped=stopped, metadata=meta, events=events)
                 else:
                     raise RuntimeError(f'unexpected training event {kind}')
+                events.append(ev)
+                if on_event is not None:
+                    on_event(self, ev)
 
     def stop(self):
         self.send(99)

@@ -343,3 +343,48 @@ class PoissonWorkload:
         bnodes, bconsts = self.boundary_ir()
         cb = session.integral_cost(n, db, bnodes, bconsts, np.zeros((0, len(self.boundary))), self.boundary_w)
         return dict(interior=di, boundary=db, net=n, costs=[ci, cb])
+
+
+# ----------------------------------------------------------------------------- variations
+class VariationWorkload:
+    """2->6->5->1 sigmoid network on 12 quadrature points in [0,1]^2 with rows
+    (value, x); components u = 0, u_x = 1 (row * outputs + output)."""
+
+    def __init__(self, seed=61):
+        rng = np.random.default_rng(seed)
+        self.neurons = [2, 6, 5, 1]
+        self.schema = closed_schema(2, [(1, 0)])
+        self.points = rng.uniform(0, 1, (12, 2))
+        self.weights = rng.uniform(0.02, 0.1, 12)
+        self.init = xavier_weights(self.neurons, seed)
+
+    # expression IR of the leaves: (op, a, b) with b = frozen flag on components
+    A = ([(1, 0, 0)], [0.0])                                    # u
+    CORRECTION = ([(1, 0, 0), (1, 1, 1), (5, 0, 1)], [0.0, 0.0, 0.0])   # u * u_x, u_x frozen
+    FROZEN = ([(1, 0, 1), (7, 0, -1)], [0.0, 2.0])              # u ** 2, u frozen
+    FREE = ([(1, 0, 0), (7, 0, -1)], [0.0, 2.0])                # u ** 2
+
+    @staticmethod
+    def nested_graph():
+        """(a*a).with_variation(correction.with_variation(a)) + correction + a
+        (tests/test_integrals.py:176-186), nodes as the reference client's
+        prepare_graph numbers them: leaf a, Mul, leaf correction, Attach,
+        Attach, Add, Add."""
+        from .wire import graph_bytes
+        nodes = [(1, 0, -1), (5, 0, 0), (1, 1, -1), (15, 2, 0), (15, 1, 3), (3, 4, 2), (3, 5, 0)]
+        return graph_bytes(nodes, [0.0] * 7, 6)
+
+    @staticmethod
+    def cancelled_graph():
+        """a.with_variation(-a) (tests/test_audit_fixes.py:69-77)."""
+        from .wire import graph_bytes
+        return graph_bytes([(1, 0, -1), (8, 0, -1), (15, 0, 1)], [0.0] * 3, 2)
+
+    def upload(self, s):
+        d = s.data(input_stack(self.points, self.schema), self.schema)
+        n = s.network(self.neurons, linear_flags(self.neurons), self.init)
+        costs = {}
+        for name, (nodes, consts) in (('a', self.A), ('correction', self.CORRECTION), ('frozen', self.FROZEN),
+                                      ('free', self.FREE)):
+            costs[name] = s.integral_cost(n, d, nodes, consts, np.zeros((0, 12)), self.weights, chunk=5)
+        return n, d, costs

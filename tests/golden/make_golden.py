@@ -254,6 +254,203 @@ def case_training(s):
     return rec
 
 
+def state_arrays(blob):
+    """(metadata, [per transition: W, buffer 1, buffer 2, step/m, active])."""
+    meta, layers = wire.decode_state(blob)
+    return meta, [(*layer['buffers'], layer['active']) for layer in layers]
+
+
+def stepped_run(s, ids, epochs, first, later, prefix, rec):
+    """``epochs`` single-epoch op-8 calls (``first`` the first call's keyword
+    arguments, ``later`` the others'), each preceded by an op-14 gradient at
+    the current weights and followed by an op-9 snapshot: the exact gradient
+    every update consumed and the state it left."""
+    for k in range(epochs):
+        _, grads = s.graph_eval(ids['net'], [ids['cost']], SINGLE_LEAF, gradient=True)
+        for t, g in enumerate(grads):
+            rec[f'{prefix}_grad{k}_{t}'] = g
+        s.train(ids['net'], [ids['cost']], 1, log=1, **(first if k == 0 else later))
+        rec[f'{prefix}_state{k}'] = np.frombuffer(s.snapshot(ids['net']), np.uint8)
+    rec[f'{prefix}_epochs'] = np.int32(epochs)
+
+
+def case_optimizer(s):
+    """Optimizer trajectories with the gradient each update consumed:
+      * ``rprop``: six RPROP epochs from a fresh state (initial step 0.002);
+      * ``bigstep``: six RPROP epochs after reset_steps=0.05, so that sign
+        reversals (rollback, x0.5) occur early;
+      * ``restore``: four RPROP epochs with reset_steps=2e-4 and
+        restore_every=2, restore_step=1e-3 (cuda/cpde_server.cu:377,415-418);
+      * ``adam``: three Adam epochs with lr 0.01.
+    The initial weights and the state blob after every epoch are stored."""
+    wl = tiny_workload(seed=41, order=4, neurons=(2, 12, 12, 1), points=40)
+    rec = dict(neurons=np.asarray(wl.neurons, np.int32), schema=wl.schema, points=wl.points, target=wl.target,
+               row_weights=wl.row_weights, chunk=np.int32(16))
+    for t, w in enumerate(wl.init):
+        rec[f'init{t}'] = np.asarray(w, np.float32)
+    runs = [('rprop', dict(method=0, fresh=1), dict(method=0, fresh=0), 6),
+            ('bigstep', dict(method=0, fresh=1, steps=0.05), dict(method=0, fresh=0), 6),
+            ('restore', dict(method=0, fresh=1, steps=2e-4, restore_every=2, restore_step=1e-3),
+             dict(method=0, fresh=0, restore_every=2, restore_step=1e-3), 4),
+            ('adam', dict(method=1, fresh=1, lr=0.01), dict(method=1, fresh=0), 3)]
+    for prefix, first, later, epochs in runs:
+        ids = wl.upload(s, 16)
+        stepped_run(s, ids, epochs, first, later, prefix, rec)
+        for kind, key in ((2, 'cost'), (1, 'net'), (0, 'data'), (0, 'target')):
+            s.close_object(kind, ids[key])
+    return rec
+
+
+def events_record(res, ids_to_index):
+    """Event frames as arrays: kinds in order, report rows (completed, updates,
+    after, values...), state blobs and output frames (cost index, values)."""
+    kinds = np.asarray([e['kind'] for e in res['events']], np.int32)
+    reports = [(e['completed'], e['updates'], e['after'], *e['values']) for e in res['events'] if e['kind'] == 2]
+    blobs = [np.frombuffer(e['blob'], np.uint8) for e in res['events'] if e['kind'] == 3]
+    outputs = [(ids_to_index[e['cost']], e['outputs']) for e in res['events'] if e['kind'] == 4]
+    return kinds, np.asarray(reports, np.float64), blobs, outputs
+
+
+def linear_unit(s, weight, bias, x):
+    """The reference tests' one-input linear network u = weight*x + bias
+    (tests/test_interface.py:290-325) on a single value-row sample."""
+    n = s.network([1, 1], [1, 1], [np.array([weight, bias], np.float32)])
+    d = s.data(np.array([[[x]]], np.float32), np.array([[0, 0]], np.int32))
+    return n, d
+
+
+def case_protocol(s):
+    """Training-loop surface against the reference server:
+      * save_every=2, eval_every=2 and print_outputs over five epochs
+        (kind-2 reports, kind-3 snapshots, kind-4 outputs, cuda/cpde_server.cu:419-433);
+      * op 99 sent on the first kind-3 frame of a 100,000-epoch call, then a
+        resume of two remaining epochs from the stopped state
+        (tests/test_interface.py:204-222);
+      * non-finite weight gradient (u = 1e10 at x = 1e30: dE/dW overflows)
+        and non-finite dE/dY with a finite objective (1e30 * u at u = 1e-20),
+        both rejected before any update (tests/test_interface.py:290-325)."""
+    wl = tiny_workload(seed=51, order=2, neurons=(2, 10, 10, 1), points=30)
+    rec = dict(neurons=np.asarray(wl.neurons, np.int32), schema=wl.schema, points=wl.points, target=wl.target,
+               row_weights=wl.row_weights, chunk=np.int32(16))
+    for t, w in enumerate(wl.init):
+        rec[f'init{t}'] = np.asarray(w, np.float32)
+    ids = wl.upload(s, 16)
+    res = s.train(ids['net'], [ids['cost']], 5, method=0, fresh=1, log=2, eval_every=2, outputs=1, save=2)
+    kinds, reports, blobs, outputs = events_record(res, {ids['cost']: 0})
+    rec.update(periodic_kinds=kinds, periodic_reports=reports, periodic_completed=np.int64(res['completed']))
+    for i, b in enumerate(blobs):
+        rec[f'periodic_blob{i}'] = b
+    for i, (c, o) in enumerate(outputs):
+        rec[f'periodic_outputs{i}'] = o
+    rec['periodic_final'] = np.frombuffer(s.snapshot(ids['net']), np.uint8)
+
+    # stop at the first checkpoint of a long call, then resume two epochs
+    stop_ids = wl.upload(s, 16)
+
+    def stop_on_checkpoint(session, ev):
+        if ev['kind'] == 3 and not getattr(session, '_stop_sent', False):
+            session._stop_sent = True
+            session.stop()
+
+    s._stop_sent = False
+    res = s.train(stop_ids['net'], [stop_ids['cost']], 100000, method=1, fresh=1, lr=0.01, log=1, save=1,
+                  stage='stop-test', on_event=stop_on_checkpoint)
+    stopped_blob = s.snapshot(stop_ids['net'])
+    meta, layers = wire.decode_state(stopped_blob)
+    kinds = np.asarray([e['kind'] for e in res['events']], np.int32)
+    rec.update(stop_completed=np.int64(res['completed']), stop_stopped=np.int32(res['stopped']), stop_kinds=kinds,
+               stop_meta=np.asarray([meta['updates'], meta['adam_step'], meta['stage_done'], meta['remaining']],
+                                    np.int64))
+    meta['remaining'] = 2
+    s.restore(stop_ids['net'], wire.encode_state(meta, layers))
+    res = s.train(stop_ids['net'], [stop_ids['cost']], 2, method=1, fresh=0, log=1, stage='stop-test')
+    meta2, _ = wire.decode_state(s.snapshot(stop_ids['net']))
+    rec.update(resume_completed=np.int64(res['completed']), resume_stopped=np.int32(res['stopped']),
+               resume_meta=np.asarray([meta2['updates'], meta2['adam_step'], meta2['stage_done'],
+                                       meta2['remaining']], np.int64))
+
+    # non-finite weight gradient: objective and dE/dY finite, x * dE/dY overflows
+    n, d = linear_unit(s, 0.0, 1e10, 1e30)
+    c = s.polynomial_cost(n, d, [0], 1, [[0, 0, -1]], np.ones((1, 1), np.float32), np.zeros((1, 1), np.float32),
+                          np.ones((1, 1), np.float32))
+    before = s.snapshot(n)
+    try:
+        s.train(n, [c], 1, method=1, fresh=1, lr=0.01, log=1)
+        raise SystemExit('reference accepted a non-finite weight gradient')
+    except wire.ServerError as e:
+        rec['weight_gradient_error'] = np.array(str(e))
+        diag = [ev for ev in e.events if ev['kind'] == 5]
+        rec['weight_gradient_diag'] = np.asarray([(l['nonfinite'], l['first'], l['max']) for l in diag[0]['layers']],
+                                                 np.float64)
+    rec['weight_gradient_before'] = np.frombuffer(before, np.uint8)
+    rec['weight_gradient_after'] = np.frombuffer(s.snapshot(n), np.uint8)
+
+    # non-finite dE/dY with a finite objective
+    n, d = linear_unit(s, 0.0, 1e-20, 0.0)
+    c = s.polynomial_cost(n, d, [0], 1, [[0, 0, -1]], np.full((1, 1), 1e30, np.float32),
+                          np.zeros((1, 1), np.float32), np.ones((1, 1), np.float32))
+    before = s.snapshot(n)
+    try:
+        s.train(n, [c], 1, method=1, fresh=1, lr=0.01, log=1)
+        raise SystemExit('reference accepted a non-finite output gradient')
+    except wire.ServerError as e:
+        rec['output_gradient_error'] = np.array(str(e))
+    rec['output_gradient_before'] = np.frombuffer(before, np.uint8)
+    rec['output_gradient_after'] = np.frombuffer(s.snapshot(n), np.uint8)
+    return rec
+
+
+def case_variations(s):
+    """Attached variations and frozen components: each leaf alone, the nested
+    variation graph (value-dependent multipliers, shared leaves), the cancelled
+    variation, and two RPROP epochs of the nested graph."""
+    vw = W.VariationWorkload()
+    n, d, costs = vw.upload(s)
+    rec = dict(neurons=np.asarray(vw.neurons, np.int32), points=vw.points, quadrature=vw.weights)
+    for t, w in enumerate(vw.init):
+        rec[f'init{t}'] = np.asarray(w, np.float32)
+    for name in ('a', 'correction', 'frozen', 'free'):
+        value, grads = s.graph_eval(n, [costs[name]], SINGLE_LEAF, gradient=True)
+        rec[f'{name}_value'] = np.float64(value)
+        for t, g in enumerate(grads):
+            rec[f'{name}_grad{t}'] = g
+    value, grads = s.graph_eval(n, [costs['a'], costs['correction']], vw.nested_graph(), gradient=True)
+    rec['nested_value'] = np.float64(value)
+    for t, g in enumerate(grads):
+        rec[f'nested_grad{t}'] = g
+    value, grads = s.graph_eval(n, [costs['a']], vw.cancelled_graph(), gradient=True)
+    rec['cancelled_value'] = np.float64(value)
+    for t, g in enumerate(grads):
+        rec[f'cancelled_grad{t}'] = g
+    res = s.train(n, [costs['a'], costs['correction']], 2, method=0, fresh=1, log=1, graph=vw.nested_graph())
+    rec['nested_reports'] = np.asarray([(e['completed'], e['updates'], e['after'], e['total'])
+                                        for e in res['events'] if e['kind'] == 6], np.float64)
+    rec['nested_state'] = np.frombuffer(s.snapshot(n), np.uint8)
+    return rec
+
+
+def case_poisson_full(s):
+    """The Poisson workload at full size: 64 Gauss-Legendre radii x 64 angles
+    plus 256 boundary points.  Objective, leaves, gradient, and the state after
+    two RPROP epochs (reset_steps 2e-4)."""
+    pw = W.PoissonWorkload()
+    ids = pw.upload(s)
+    value, grads = s.graph_eval(ids['net'], ids['costs'], pw.graph(), gradient=True)
+    rec = dict(loss=np.float64(value))
+    for t, g in enumerate(grads):
+        rec[f'grad{t}'] = g
+    for leaf in range(2):
+        v, _ = s.graph_eval(ids['net'], [ids['costs'][leaf]], SINGLE_LEAF, gradient=False)
+        rec[f'leaf{leaf}'] = np.float64(v)
+    res = s.train(ids['net'], ids['costs'], 2, method=0, fresh=1, steps=2e-4, log=1, graph=pw.graph())
+    rec['reports'] = np.asarray([(e['completed'], e['updates'], e['after'], e['total'])
+                                 for e in res['events'] if e['kind'] == 6], np.float64)
+    rec['state'] = np.frombuffer(s.snapshot(ids['net']), np.uint8)
+    rec['checksums'] = np.stack([checksum(pw.interior), checksum(pw.interior_w), checksum(pw.boundary),
+                                 checksum(pw.f), checksum(np.concatenate(pw.init))])
+    return rec
+
+
 CASES = {
     'tiny_order6': case_tiny_order6,
     'tiny_3var_order4': case_tiny_3var_order4,
@@ -265,6 +462,10 @@ CASES = {
     'poisson': case_poisson,
     'polynomial': case_polynomial,
     'training': case_training,
+    'optimizer': case_optimizer,
+    'protocol': case_protocol,
+    'variations': case_variations,
+    'poisson_full': case_poisson_full,
 }
 
 

@@ -154,6 +154,38 @@ def test_epoch_matches_oracle(device, path, order, neurons, points, chunk):
     run.close()
 
 
+PAIRED_ALIASED = dict(CPDE_FUSED='2', CPDE_NET_POINTS='2', CPDE_NET_ALIAS='1', CPDE_NET_COLTILE='16',
+                      CPDE_NET_SPLIT='1', CPDE_NET_SPLIT_ADJOINT='1')
+
+
+@pytest.mark.parametrize('order,neurons,points', [
+    (5, [2, 80, 96, 1], 4101),   # more workgroups than co-reside: separate forward and backward launches
+    (5, [2, 80, 96, 1], 301),    # co-resident: the one-pass epoch, its cost scratch apart from the tiles
+    (3, [2, 48, 32, 1], 257),    # few rows: two points share one 16-column tile pair
+])
+def test_paired_aliased_network_forms(device, monkeypatch, order, neurons, points):
+    """The network kernels' two-points-per-workgroup, one-LDS-tile form forced
+    by its tuning variables (by default it is chosen only on long grids of
+    many-row points, depending on the CU count), with an odd point count so the
+    last workgroup holds a lone point."""
+    for k, v in PAIRED_ALIASED.items():
+        monkeypatch.setenv(k, v)
+    print(f'[case] paired aliased order={order} neurons={neurons} points={points}', flush=True)
+    wl = small_workload(order, neurons, points)
+    run = hip.MatchingRun(device, wl)
+    run.step()
+    device.synchronize()
+    loss, grads = run.loss(), run.gradients()
+    ref_loss, ref_grads = oracle_epoch(order, tuple(neurons), points, 0)
+    print(f'[result] loss {loss!r} oracle {ref_loss!r}', flush=True)
+    assert abs(loss / ref_loss - 1) < 1e-4
+    for t, (g, r) in enumerate(zip(grads, ref_grads)):
+        e = rel_l2(g, r)
+        print(f'[result] transition {t} gradient rel-L2 {e:.3e}', flush=True)
+        assert e < 1e-3
+    run.close()
+
+
 @functools.lru_cache(maxsize=None)
 def oracle_epoch(order, neurons, points, chunk):
     """The oracle's epoch of small_workload, computed once for all kernel families."""

@@ -111,6 +111,29 @@ def test_one_pass_expression_epoch_matches_separate_launches(server):
         np.testing.assert_array_equal(a['buffers'][0], b['buffers'][0])
 
 
+def test_paired_aliased_expression_epoch(server):
+    """The Poisson objective on a server whose network kernels are forced to
+    two points per workgroup with one LDS tile (the one-pass expression epoch
+    then keeps its per-point double and flag records in a scratch apart from
+    the tiles): the reference's objective and gradients, and the same
+    gradients as the default form to the fp32 bar."""
+    import os
+    from cpde_amd import workloads as W
+    g = load_golden('poisson')
+    pw = W.PoissonWorkload(radial=int(g['radial']), angular=int(g['angular']), boundary=int(g['boundary']))
+    forced = wire.Session(SERVER, env=dict(os.environ, CPDE_FUSED='2', CPDE_NET_POINTS='2', CPDE_NET_ALIAS='1',
+                                           CPDE_NET_COLTILE='16', CPDE_NET_SPLIT='1', CPDE_NET_SPLIT_ADJOINT='1'))
+    try:
+        ids = pw.upload(forced)
+        value, grads = forced.graph_eval(ids['net'], ids['costs'], pw.graph(), gradient=True)
+    finally:
+        forced.close()
+    print(f'[result] paired aliased poisson objective {value!r} reference {float(g["loss"])!r}', flush=True)
+    assert abs(value / g['loss'] - 1) < 1e-4
+    for t, grad in enumerate(grads):
+        assert rel_l2(grad, g[f'grad{t}']) < 1e-3
+
+
 def test_graph_without_leaf_dependence_zeroes_the_gradient(server):
     """A root that depends on no leaf: every multiplier is known to be 0, no
     leaf runs a backward pass, and the gradient must come back zero although
