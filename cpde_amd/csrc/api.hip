@@ -366,9 +366,17 @@ static void fused_forward(Plan& p) {
 struct GradientPlan {
     WgradArgs wa{};
     ReduceArgs ra{};
-    std::vector<size_t> offset;
+    size_t offset[kMaxTransitions] = {};  // first partial of each transition (local index)
     double flops = 0;
     size_t total = 0;
+};
+
+// Where a gradient plan's split partials live: the network's own lazily grown
+// buffer (base == nullptr), or a fixed region of `floats` floats that is never
+// grown (the no-allocation epoch's static scratch).
+struct PartialSpace {
+    float* base = nullptr;
+    size_t floats = 0;
 };
 
 // Weight-gradient tiles per compute unit the split-K decomposition aims for
@@ -376,27 +384,34 @@ struct GradientPlan {
 // SIMD to cover the other's loads and barriers).
 static int wgrad_blocks_per_cu() { return std::max(1, env_int("CPDE_WGRAD_OCC", 2)); }
 
-static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<int>& external_splits) {
+// The gradient plan of transitions [first, first + count), count at most
+// kMaxTransitions (one grouped launch and one reduction); external_splits is
+// indexed by the absolute transition.
+static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external_splits, int first, int count,
+                                   PartialSpace space = {}) {
     Net& n = *p.net;
     Device& d = *n.dev;
-    const int L = n.layers, T = L - 1, K = int(p.columns());
+    const int K = int(p.columns());
+    const int T = count;
     GradientPlan g;
-    g.offset.assign(T, 0);
-    auto thin = [&](int t) { return n.neurons[t + 1] <= 16 || n.neurons[t] <= 16; };
+    // local transition k is the network's transition first + k
+    auto thin = [&](int k) { return n.neurons[first + k + 1] <= 16 || n.neurons[first + k] <= 16; };
     // 128x128 tiles, or 64x64 when both widths are at most 64 -- or when the
     // 128x128 splits would be short (fewer than kWgradMinColumns columns each):
     // then four times the tiles give each split four times the columns, and
     // the split partials the reduction reads shrink fourfold
     bool small_tiles = false;
-    auto tile_of = [&](int t) { return small_tiles || (n.neurons[t + 1] <= 64 && n.neurons[t] <= 64) ? 64 : 128; };
-    auto tiles_of = [&](int t) {
-        const int T0 = tile_of(t);
-        return ((n.neurons[t + 1] + T0 - 1) / T0) * ((n.neurons[t] + T0 - 1) / T0);
+    auto tile_of = [&](int k) {
+        return small_tiles || (n.neurons[first + k + 1] <= 64 && n.neurons[first + k] <= 64) ? 64 : 128;
+    };
+    auto tiles_of = [&](int k) {
+        const int T0 = tile_of(k);
+        return ((n.neurons[first + k + 1] + T0 - 1) / T0) * ((n.neurons[first + k] + T0 - 1) / T0);
     };
     auto count_tiles = [&] {
         int total = 0;
-        for (int t = 0; t < T; ++t)
-            if (!thin(t) && !external_splits[t]) total += tiles_of(t);
+        for (int k = 0; k < T; ++k)
+            if (!thin(k) && !external_splits[first + k]) total += tiles_of(k);
         return total;
     };
     // whole waves of tiles: a partial last wave would run alone for a whole split
@@ -415,12 +430,13 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
     g.ra.begin[0] = 0;
     g.ra.block_begin[0] = 0;
     int w = 0;
-    for (int t = 0; t < T; ++t) {
+    for (int k = 0; k < T; ++k) {
+        const int t = first + k;
         const int M = n.neurons[t + 1], N = n.neurons[t];
         int s = external_splits[t];
         if (!s) {
-            const int tiles = thin(t) ? 1 : tiles_of(t);
-            s = thin(t) ? 2 * d.compute_units : tile_splits;
+            const int tiles = thin(k) ? 1 : tiles_of(k);
+            s = thin(k) ? 2 * d.compute_units : tile_splits;
             s = std::max(1, std::min(s, std::max(1, K / kWgradChunk)));
             int chunk = (K + s - 1) / s;
             chunk = (chunk + kWgradChunk - 1) / kWgradChunk * kWgradChunk;
@@ -428,35 +444,44 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const std::vector<i
             g.wa.M[w] = M;
             g.wa.N[w] = N;
             g.wa.kchunk[w] = chunk;
-            g.wa.tile[w] = tile_of(t);
+            g.wa.tile[w] = tile_of(k);
             g.wa.block_begin[w + 1] = g.wa.block_begin[w] + tiles * s;
             g.wa.G[w] = n.g[t + 1];
             g.wa.Y[w] = activations(p, t);
             g.flops += 2.0 * M * N * double(K);
             ++w;
         }
-        g.offset[t] = g.total;
+        g.offset[k] = g.total;
         g.total += size_t(s) * M * (N + 1);
-        g.ra.M[t] = M;
-        g.ra.N[t] = N;
-        g.ra.splits[t] = s;
-        g.ra.grad[t] = n.state[n.active[t]][t];
-        g.ra.begin[t + 1] = g.ra.begin[t] + M * (N + 1);
-        g.ra.split_minor[t] = external_splits[t] ? 1 : 0;
-        g.ra.block_begin[t + 1] = g.ra.block_begin[t] + reduce_blocks(M * (N + 1), external_splits[t] != 0);
+        g.ra.M[k] = M;
+        g.ra.N[k] = N;
+        g.ra.splits[k] = s;
+        g.ra.grad[k] = n.state[n.active[t]][t];
+        g.ra.begin[k + 1] = g.ra.begin[k] + M * (N + 1);
+        g.ra.split_minor[k] = external_splits[t] ? 1 : 0;
+        g.ra.block_begin[k + 1] = g.ra.block_begin[k] + reduce_blocks(M * (N + 1), external_splits[t] != 0);
     }
     g.wa.transitions = w;
-    if (g.total > n.partial_capacity) {
-        HIP_CHECK(hipStreamSynchronize(d.stream));
-        if (n.partials) HIP_CHECK(hipFree(n.partials));
-        n.partials = nullptr;
-        HIP_CHECK(hipMalloc(&n.partials, g.total * sizeof(float)));
-        n.partial_capacity = g.total;
+    float* base = space.base;
+    if (base) {
+        if (g.total > space.floats)
+            throw invalid("the weight-gradient split partials need " + std::to_string(g.total * sizeof(float)) +
+                          " bytes, beyond the " + std::to_string(space.floats * sizeof(float)) +
+                          " bytes of static scratch left after the cost records");
+    } else {
+        if (g.total > n.partial_capacity) {
+            HIP_CHECK(hipStreamSynchronize(d.stream));
+            if (n.partials) HIP_CHECK(hipFree(n.partials));
+            n.partials = nullptr;
+            HIP_CHECK(hipMalloc(&n.partials, g.total * sizeof(float)));
+            n.partial_capacity = g.total;
+        }
+        base = n.partials;
     }
     w = 0;
-    for (int t = 0; t < T; ++t) {
-        g.ra.partial[t] = n.partials + g.offset[t];
-        if (!external_splits[t]) g.wa.partial[w++] = n.partials + g.offset[t];
+    for (int k = 0; k < T; ++k) {
+        g.ra.partial[k] = base + g.offset[k];
+        if (!external_splits[first + k]) g.wa.partial[w++] = base + g.offset[k];
     }
     return g;
 }
@@ -512,34 +537,39 @@ static CostStats* epoch_records(Plan& p) {
 
 // Forward, cost and backward of one chunk in one network-fused launch of
 // `kernel` (arguments: the network, `cost_args`, the chunk width), then the
-// cost's fixed-order finish and the weight-gradient contraction.
-static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, int cost_index, bool accumulate) {
+// cost's fixed-order finish and the weight-gradient contraction.  `records`
+// holds the launch's per-workgroup cost records; `space` says where the
+// weight-gradient split partials go.  Everything that can be refused is
+// checked before the first launch.
+static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostStats* records, int cost_index,
+                           bool accumulate, PartialSpace space = {}) {
     Net& n = *p.net;
     Device& d = *n.dev;
     const int L = n.layers;
     int width = p.width;
     const double cols = double(p.columns());
     const int blocks = epoch_blocks(p);
-    std::vector<int> external(L - 1, 0);
+    int external[kMaxTransitions] = {};
     external[0] = external[L - 2] = blocks;
-    GradientPlan g = plan_gradients(p, accumulate, external);
+    GradientPlan g = plan_gradients(p, accumulate, external, 0, L - 1, space);
     NetArgsHost a = net_args(p);
-    a.partial_in = n.partials + g.offset[0];
-    a.partial_out = n.partials + g.offset[L - 2];
+    a.partial_in = const_cast<float*>(g.ra.partial[0]);
+    a.partial_out = const_cast<float*>(g.ra.partial[L - 2]);
     if (!n.wt_current) {
         // the backward half reads the row-major weight copies of every hidden
         // transition, which no workgroup of the same launch may still be
         // writing; RPROP and Adam keep them current between epochs
-        std::vector<const float*> W;
-        std::vector<float*> WT;
-        std::vector<int> ni, no;
-        for (int t = 1; t + 2 < L; ++t) {
-            W.push_back(n.state[0][t]);
-            WT.push_back(n.wt[t]);
-            ni.push_back(n.neurons[t]);
-            no.push_back(n.neurons[t + 1]);
+        const float* W[kMaxTransitions];
+        float* WT[kMaxTransitions];
+        int ni[kMaxTransitions], no[kMaxTransitions];
+        int count = 0;
+        for (int t = 1; t + 2 < L; ++t, ++count) {
+            W[count] = n.state[0][t];
+            WT[count] = n.wt[t];
+            ni[count] = n.neurons[t];
+            no[count] = n.neurons[t + 1];
         }
-        launch_transpose(d, W.data(), WT.data(), ni.data(), no.data(), int(W.size()));
+        launch_transpose(d, W, WT, ni, no, count);
         n.wt_current = true;
     }
     void* args[] = {&a, cost_args, &width};
@@ -551,12 +581,12 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, int c
         launch_module(d, kernel, unsigned(blocks), 1, args);
     }
     if (blocks <= kMaxCostBlocks) {  // the cost's finish rides in the gradient reduction launch
-        g.ra.cost_partials = p.epoch_partials;
+        g.ra.cost_partials = records;
         g.ra.cost_total = d.cost_totals + cost_index;
         g.ra.cost_count = blocks;
         g.ra.cost_overwrite = d.take_fresh(cost_index) ? 1 : 0;
     } else {
-        launch_finish_cost(d, p.epoch_partials, blocks, cost_index);
+        launch_finish_cost(d, records, blocks, cost_index);
     }
     run_gradients(d, g);
 }
@@ -585,8 +615,14 @@ static hipFunction_t expression_epoch(Plan& p, const Program& program) {
     return e->function;
 }
 
+// Every transition's weight gradient, kMaxTransitions transitions per grouped
+// launch and reduction (the groups reuse the partials in stream order).
 static void weight_gradients(Plan& p, bool accumulate) {
-    run_gradients(*p.net->dev, plan_gradients(p, accumulate, std::vector<int>(p.net->layers - 1, 0)));
+    const int T = p.net->layers - 1;
+    const std::vector<int> none(T, 0);
+    for (int first = 0; first < T; first += kMaxTransitions)
+        run_gradients(*p.net->dev,
+                      plan_gradients(p, accumulate, none.data(), first, std::min(kMaxTransitions, T - first)));
 }
 
 static void fused_backward(Plan& p, bool accumulate) {
@@ -598,12 +634,12 @@ static void fused_backward(Plan& p, bool accumulate) {
     const double cols = double(p.columns());
     if (p.network) {
         const int blocks = (width + fm.net_points_per_block - 1) / fm.net_points_per_block;
-        std::vector<int> external(L - 1, 0);
+        int external[kMaxTransitions] = {};
         external[0] = external[L - 2] = blocks;
-        const GradientPlan g = plan_gradients(p, accumulate, external);
+        const GradientPlan g = plan_gradients(p, accumulate, external, 0, L - 1);
         NetArgsHost a = net_args(p);
-        a.partial_in = n.partials + g.offset[0];
-        a.partial_out = n.partials + g.offset[L - 2];
+        a.partial_in = const_cast<float*>(g.ra.partial[0]);
+        a.partial_out = const_cast<float*>(g.ra.partial[L - 2]);
         void* args[] = {&a, &width};
         double flops = 0;
         for (int t = 1; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
@@ -956,9 +992,10 @@ int cpde_epoch_matching(cpde_plan* plan, const float* target, int target_width, 
             if (int code = cpde_backward(plan, accumulate)) throw_code(code);
             return;
         }
-        MatchArgsHost m{target, target_rows, weights, epoch_records(*plan), target_width, weight_samples, offset, valid,
+        CostStats* records = epoch_records(*plan);
+        MatchArgsHost m{target, target_rows, weights, records, target_width, weight_samples, offset, valid,
                         collect != 0};
-        one_pass_epoch(*plan, plan->fused->network_epoch, &m, cost_index, accumulate != 0);
+        one_pass_epoch(*plan, plan->fused->network_epoch, &m, records, cost_index, accumulate != 0);
     });
 }
 
@@ -1182,9 +1219,9 @@ int cpde_epoch_expression(cpde_plan* plan, cpde_program* program, const double* 
             return;
         }
         const hipFunction_t kernel = expression_epoch(*plan, *program);
-        ExpressionArgsHost e{fields, quadrature_weights, multiplier, epoch_records(*plan), samples, offset, valid,
-                             collect != 0};
-        one_pass_epoch(*plan, kernel, &e, cost_index, accumulate != 0);
+        CostStats* records = epoch_records(*plan);
+        ExpressionArgsHost e{fields, quadrature_weights, multiplier, records, samples, offset, valid, collect != 0};
+        one_pass_epoch(*plan, kernel, &e, records, cost_index, accumulate != 0);
     });
 }
 

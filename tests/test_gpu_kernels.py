@@ -254,6 +254,42 @@ def test_multi_output_epoch_matches_oracle(device, path, order, neurons, points,
     net.destroy()
 
 
+def test_deep_network_beyond_one_gradient_group(device):
+    """41 transitions (the protocol takes up to 255): more than one grouped
+    weight-gradient launch and reduction (32 transitions each), then RPROP and
+    the gradient statistics over two launch groups as well.  Loss and every
+    gradient against the oracle; the first RPROP step bit-exact against the
+    oracle's on our gradients."""
+    neurons = [2] + [6] * 40 + [1]
+    print(f'[case] deep network {len(neurons) - 1} transitions', flush=True)
+    wl = small_workload(1, neurons, 20, seed=9)
+    # wide enough initial weights that the signal survives forty layers
+    wl.init = [w * 3 for w in wl.init]
+    run = hip.MatchingRun(device, wl)
+    run.step()
+    device.synchronize()
+    loss, grads = run.loss(), run.gradients()
+    ref_loss, ref_grads, _ = oracle.matching_epoch(wl.neurons, wl.linear, wl.init, wl.schema,
+                                                   wl.inputs.transpose(0, 2, 1), wl.target[:, :, None],
+                                                   wl.row_weights[:, None, None], outputs=False)
+    print(f'[result] loss {loss!r} oracle {ref_loss!r}', flush=True)
+    assert abs(loss / ref_loss - 1) < 1e-4
+    errs = [rel_l2(g, r) for g, r in zip(grads, ref_grads)]
+    print(f'[result] worst gradient rel-L2 {max(errs):.3e}', flush=True)
+    assert max(errs) < 1e-3
+    run.net.inspect_gradients()
+    stats = device.scalars(0, len(neurons) - 1)[1]
+    for s, g in zip(stats, grads):
+        assert s.nonfinite_count == 0
+        assert s.max_abs == np.abs(g).max()
+    before = [run.net.state(t, 0) for t in range(len(neurons) - 1)]
+    run.net.rprop()
+    for t, (w, g) in enumerate(zip(before, grads)):
+        rW, _, _, _ = oracle.rprop(w, np.full_like(w, 0.002), g, np.zeros_like(w))
+        np.testing.assert_array_equal(run.net.state(t, 0), rW)
+    run.close()
+
+
 def test_oversized_chunk_is_rejected(device):
     """A chunk whose (point, row) pairs would overflow the kernels' 32-bit
     indexing is refused at plan creation, before any allocation, and the
