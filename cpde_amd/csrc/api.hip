@@ -17,6 +17,15 @@ struct cpde_program_s : cpde::Program {};
 
 namespace cpde {
 
+// The no-allocation epoch's scratch (cpde_epoch_matching_static): one static
+// device array that every GPU the library runs on holds until the process
+// ends -- the launch's per-workgroup cost records (256-byte aligned), then its
+// weight-gradient split partials.  Each kernel writes what it later reads
+// within the same call, so nothing needs clearing between calls.  Host code
+// never uses the array's name as an address: cpde_device_open takes this GPU's
+// address with hipGetSymbolAddress (Device::static_scratch).
+static __device__ __align__(256) unsigned char scratch[CPDE_STATIC_SCRATCH_BYTES];
+
 static thread_local std::string last_error;
 
 void set_error(const std::string& message) { last_error = message; }
@@ -694,6 +703,13 @@ int cpde_device_open(int ordinal, cpde_device** out) {
         HIP_CHECK(hipGetDeviceProperties(&prop, ordinal));
         d->compute_units = prop.multiProcessorCount;
         HIP_CHECK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+        {
+            // this GPU's address of the static scratch (the device is current)
+            void* ptr = nullptr;
+            const hipError_t status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+            if (status == hipSuccess && ptr) d->static_scratch = static_cast<unsigned char*>(ptr);
+            else d->static_scratch_error = std::string("hipGetSymbolAddress failed: ") + hipGetErrorString(status);
+        }
         HIP_CHECK(hipMalloc(&d->cost_blocks, sizeof(CostStats) * kMaxCostBlocks));
         for (auto& e : d->marks) HIP_CHECK(hipEventCreate(&e));
         d->reserve_scalars(8, 8);
@@ -996,6 +1012,32 @@ int cpde_epoch_matching(cpde_plan* plan, const float* target, int target_width, 
         MatchArgsHost m{target, target_rows, weights, records, target_width, weight_samples, offset, valid,
                         collect != 0};
         one_pass_epoch(*plan, plan->fused->network_epoch, &m, records, cost_index, accumulate != 0);
+    });
+}
+
+int cpde_epoch_matching_static(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
+                               const float* weights, int weight_samples, int offset, int valid, int cost_index,
+                               int collect, int accumulate) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        if (!d.static_scratch) throw invalid("no static scratch on this device: " + d.static_scratch_error);
+        require(!d.tracing, "kernel tracing records events: the no-allocation epoch runs with tracing off");
+        require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
+        require(plan->backward, "plan has no adjoint storage");
+        require(valid >= 0 && valid <= plan->width && offset >= 0, "invalid chunk range");
+        require(one_pass_fits(*plan),
+                "the no-allocation epoch needs a plan whose one-pass epoch applies (network-fused kernels, the "
+                "chunk's workgroups resident on the device together)");
+        const int blocks = epoch_blocks(*plan);
+        const size_t record_bytes = (sizeof(CostStats) * size_t(blocks) + 255) / 256 * 256;
+        require(record_bytes < size_t(CPDE_STATIC_SCRATCH_BYTES), "cost records beyond the static scratch");
+        CostStats* records = reinterpret_cast<CostStats*>(d.static_scratch);
+        const PartialSpace space{reinterpret_cast<float*>(d.static_scratch + record_bytes),
+                                 (size_t(CPDE_STATIC_SCRATCH_BYTES) - record_bytes) / sizeof(float)};
+        MatchArgsHost m{target, target_rows, weights, records, target_width, weight_samples, offset, valid,
+                        collect != 0};
+        one_pass_epoch(*plan, plan->fused->network_epoch, &m, records, cost_index, accumulate != 0, space);
     });
 }
 

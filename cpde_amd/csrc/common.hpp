@@ -143,6 +143,10 @@ struct Device {
     int ordinal = 0;
     int compute_units = 0;
     hipStream_t stream = nullptr;
+    // this GPU's copy of the library's static scratch array (api.hip), or null
+    // with the reason when its address could not be taken
+    unsigned char* static_scratch = nullptr;
+    std::string static_scratch_error;
     // reduction workspace (cuda/reduction_kernels.cuh:101-178)
     CostStats* cost_blocks = nullptr;   // kMaxCostBlocks
     // cost and gradient totals in one device block, [cost_capacity] then

@@ -67,6 +67,7 @@ SIGNATURES = {
     'cpde_backward': (i32, [vp, i32]),
     'cpde_inspect_gradients': (i32, [vp]),
     'cpde_epoch_matching': (i32, [vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32]),
+    'cpde_epoch_matching_static': (i32, [vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32]),
     'cpde_scalars_download': (i32, [vp, i32, vp, i32, vp]),
     'cpde_scalars_download_graph': (i32, [vp, i32, vp, i32, vp, vp, vp]),
     'cpde_rprop': (i32, [vp]),
@@ -317,6 +318,13 @@ class Plan:
         check(load().cpde_epoch_matching(self.handle, target.ptr, target_width, target_rows.ptr, weights.ptr,
                                          weight_samples, offset, valid, cost_index, int(collect), int(accumulate)))
 
+    def epoch_matching_static(self, target, target_width, target_rows, weights, weight_samples, offset, valid,
+                              cost_index, collect=True, accumulate=False):
+        """epoch_matching with the library's static scratch: no allocation."""
+        check(load().cpde_epoch_matching_static(self.handle, target.ptr, target_width, target_rows.ptr, weights.ptr,
+                                                weight_samples, offset, valid, cost_index, int(collect),
+                                                int(accumulate)))
+
     def matching(self, target, target_width, target_rows, weights, weight_samples, offset, valid, cost_index,
                  collect=True, gradient=True):
         check(load().cpde_cost_matching(self.handle, target.ptr, target_width, target_rows.ptr, weights.ptr,
@@ -356,10 +364,11 @@ class MatchingRun:
     """One matching cost on one plan: the unit of work of the benchmark step
     (forward + cost + weight gradient), driven through the C ABI."""
 
-    def __init__(self, device, workload, chunk=None, one_pass=True):
+    def __init__(self, device, workload, chunk=None, one_pass=True, static_scratch=False):
         wl = workload
         self.device, self.wl = device, wl
         self.one_pass = one_pass
+        self.static_scratch = static_scratch
         self.net = Net(device, wl.neurons, wl.linear, wl.init)
         self.samples = wl.size
         self.width = min(chunk or wl.chunk or wl.size, wl.size)
@@ -384,7 +393,10 @@ class MatchingRun:
             if self._loaded != (offset, valid):
                 self.plan.activate(self.data, self.samples, self.rows, offset, valid)
                 self._loaded = (offset, valid)
-            if self.one_pass:
+            if self.static_scratch:
+                self.plan.epoch_matching_static(self.target, self.samples, self.target_rows, self.weights, 1, offset,
+                                                valid, 0, collect, not first)
+            elif self.one_pass:
                 self.plan.epoch_matching(self.target, self.samples, self.target_rows, self.weights, 1, offset, valid, 0,
                                          collect, not first)
             else:

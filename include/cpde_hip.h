@@ -160,6 +160,24 @@ int cpde_cost_matching(cpde_plan* plan, const float* target, int target_width, c
 int cpde_epoch_matching(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
                         const float* weights, int weight_samples, int offset, int valid, int cost_index, int collect,
                         int accumulate);
+/* cpde_epoch_matching that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The same kernels as cpde_epoch_matching's one-pass epoch, with the same
+ * results; the per-workgroup cost records and the weight-gradient split
+ * partials live in the library's static device scratch of
+ * CPDE_STATIC_SCRATCH_BYTES, which every GPU the library runs on holds until
+ * the process ends, instead of buffers grown on demand.  Refused with
+ * CPDE_EINVAL, before any launch: a plan whose one-pass epoch does not apply
+ * (network-fused kernels, the chunk's workgroups resident together), a plan
+ * needing more scratch than that, a cost slot not reserved by
+ * cpde_costs_begin, or kernel tracing on.  Every call on one GPU shares its
+ * scratch: calls that overlap on one GPU (from different device handles or
+ * threads) race. */
+#define CPDE_STATIC_SCRATCH_BYTES (16u << 20)
+int cpde_epoch_matching_static(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
+                               const float* weights, int weight_samples, int offset, int valid, int cost_index,
+                               int collect, int accumulate);
 /* Sparse linear/quadratic residual cost (cuda/cost_kernels.cuh:37-90); all device. */
 int cpde_cost_polynomial(cpde_plan* plan, const cpde_poly_term* terms, int term_count, const float* coefficients,
                          const float* rhs, const float* weights, int equations, int samples, int offset, int valid,
