@@ -261,6 +261,7 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
     }
     t.points_per_block = std::max(1, env_int("CPDE_FUSED_POINTS", t.points_per_block));
     t.net_points_per_block = std::max(1, env_int("CPDE_NET_POINTS", npb));
+    t.net_threads = env_int("CPDE_NET_THREADS", t.net_threads) == 512 ? 512 : 256;
     // a composition split over lanes pays off while a point's rows fit one
     // matrix-core tile; with two tiles (R > 32) whole compositions per lane are faster
     t.max_split = std::max(1, env_int("CPDE_NET_SPLIT", rows > 32 ? 1 : t.max_split));
@@ -283,6 +284,7 @@ static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const
     auto m = std::make_shared<FusedModule>();
     m->points_per_block = tune.points_per_block;
     m->net_points_per_block = tune.net_points_per_block;
+    m->net_threads = tune.net_threads;
     HIP_CHECK(hipModuleLoadData(&m->module, code.data()));
     HIP_CHECK(hipModuleGetFunction(&m->network_forward, m->module, "network_forward_k"));
     HIP_CHECK(hipModuleGetFunction(&m->network_backward, m->module, "network_backward_k"));
@@ -301,8 +303,8 @@ static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const
     return m;
 }
 
-static void launch_module(Device& d, hipFunction_t f, unsigned gx, unsigned gy, void** args) {
-    HIP_CHECK(hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, d.stream, args, nullptr));
+static void launch_module(Device& d, hipFunction_t f, unsigned gx, unsigned gy, void** args, unsigned threads = 256) {
+    HIP_CHECK(hipModuleLaunchKernel(f, gx, gy, 1, threads, 1, 1, 0, d.stream, args, nullptr));
 }
 
 static NetArgsHost net_args(const Plan& p) {
@@ -339,7 +341,7 @@ static void fused_forward(Plan& p) {
         for (int t = 0; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
         TraceScope trace(d, kTraceNetworkForward, flops);
         launch_module(d, fm.network_forward, unsigned((width + fm.net_points_per_block - 1) / fm.net_points_per_block),
-                      1, args);
+                      1, args, unsigned(fm.net_threads));
         n.wt_current = true;  // written by the forward's side job
         return;
     }
@@ -392,6 +394,15 @@ struct PartialSpace {
 // (CPDE_WGRAD_OCC; two, the kernel's occupancy, keep a second wave on every
 // SIMD to cover the other's loads and barriers).
 static int wgrad_blocks_per_cu() { return std::max(1, env_int("CPDE_WGRAD_OCC", 2)); }
+// Direct tiles per CU the split-K aims for (CPDE_WGRAD_DIRECT_OCC; two
+// measured best on 2->128^4->1 over 729 points: 29.4 us against 31.0 at three
+// and 43.7 at four).
+static int wgrad_direct_blocks_per_cu() { return std::max(1, env_int("CPDE_WGRAD_DIRECT_OCC", 2)); }
+// Direct tiles are chosen for short splits only when a split still has this
+// many columns: on 2->128^4->1 over 729 points at order 6 (512 columns per
+// split) they took the weight gradient and its reduction from 39.0 to 37.2 us;
+// at order 2 (128 columns per split) from 21.1 to 22.4 us.
+constexpr int kWgradDirectMinColumns = 256;
 
 // The gradient plan of transitions [first, first + count), count at most
 // kMaxTransitions (one grouped launch and one reduction); external_splits is
@@ -409,9 +420,9 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
     // 128x128 splits would be short (fewer than kWgradMinColumns columns each):
     // then four times the tiles give each split four times the columns, and
     // the split partials the reduction reads shrink fourfold
-    bool small_tiles = false;
+    bool small_tiles = false, direct = false;
     auto tile_of = [&](int k) {
-        return small_tiles || (n.neurons[first + k + 1] <= 64 && n.neurons[first + k] <= 64) ? 64 : 128;
+        return direct || small_tiles || (n.neurons[first + k + 1] <= 64 && n.neurons[first + k] <= 64) ? 64 : 128;
     };
     auto tiles_of = [&](int k) {
         const int T0 = tile_of(k);
@@ -424,12 +435,25 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
         return total;
     };
     // whole waves of tiles: a partial last wave would run alone for a whole split
-    auto splits_for = [&](int tiles) { return std::max(1, wgrad_blocks_per_cu() * d.compute_units / std::max(1, tiles)); };
+    auto splits_for = [&](int tiles) {
+        const int per_cu = direct ? wgrad_direct_blocks_per_cu() : wgrad_blocks_per_cu();
+        return std::max(1, per_cu * d.compute_units / std::max(1, tiles));
+    };
     int total_tiles = count_tiles();
+    const int force = env_int("CPDE_WGRAD_DIRECT", -1);  // 0: LDS-staged tiles, 2: direct tiles, else chosen
     if (total_tiles > 0 && K / splits_for(total_tiles) < kWgradMinColumns) {
+        // short splits: 64x64 tiles, fed straight from global memory while a
+        // split keeps enough columns, LDS-staged otherwise
         small_tiles = true;
+        direct = true;  // the split count the direct tiles would have
+        const bool long_enough = K / splits_for(count_tiles()) >= kWgradDirectMinColumns;
+        direct = force == 2 || (force != 0 && long_enough);
+        total_tiles = count_tiles();
+    } else if (total_tiles > 0 && force == 2) {
+        direct = true;  // forced on long reductions too
         total_tiles = count_tiles();
     }
+    g.wa.direct = direct ? 1 : 0;
     const int tile_splits = splits_for(total_tiles);
     g.wa.K = K;
     g.wa.R = p.rows;
@@ -587,7 +611,7 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostS
     for (int t = 1; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
     {
         TraceScope trace(d, kTraceNetworkEpoch, flops);
-        launch_module(d, kernel, unsigned(blocks), 1, args);
+        launch_module(d, kernel, unsigned(blocks), 1, args, unsigned(p.fused->net_threads));
     }
     if (blocks <= kMaxCostBlocks) {  // the cost's finish rides in the gradient reduction launch
         g.ra.cost_partials = records;
@@ -654,7 +678,7 @@ static void fused_backward(Plan& p, bool accumulate) {
         for (int t = 1; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
         {
             TraceScope trace(d, kTraceNetworkBackward, flops);
-            launch_module(d, fm.network_backward, unsigned(blocks), 1, args);
+            launch_module(d, fm.network_backward, unsigned(blocks), 1, args, unsigned(fm.net_threads));
         }
         run_gradients(d, g);
         return;

@@ -198,6 +198,7 @@ struct WgradArgs {
     int tile[kMaxTransitions];  // 128, or 64 when both sides are at most 64
     int block_begin[kMaxTransitions + 1];
     int transitions, K, R;
+    int direct;  // 1: 64x64 tiles fed straight from global memory (wgrad_direct_kernel)
 };
 struct ReduceArgs {
     const float* partial[kMaxTransitions];
@@ -222,7 +223,7 @@ struct FusedModule {
     hipFunction_t input_layer = nullptr, output_backward = nullptr;
     std::vector<hipFunction_t> hidden_forward, hidden_backward;  // per transition (index t)
     hipFunction_t network_forward = nullptr, network_backward = nullptr, network_epoch = nullptr;
-    int points_per_block = 2, net_points_per_block = 1;
+    int points_per_block = 2, net_points_per_block = 1, net_threads = 256;
     ~FusedModule();
 };
 std::string compose_source(const Tables& t, const std::vector<int>& splits);
@@ -230,6 +231,7 @@ std::string compose_source(const Tables& t, const std::vector<int>& splits);
 struct FusedTuning {
     int points_per_block = 2;      // layer-fused kernels
     int net_points_per_block = 1;  // network-fused kernels
+    int net_threads = 256;         // network-fused kernels: lanes per workgroup (4 or 8 waves)
     int max_split = 4;             // lanes per composition, at most
     int max_split_adjoint = 1;     // lanes per adjoint composition, at most
     int alias = 0;                 // network kernels: products write over their operand tile (one LDS tile)

@@ -385,8 +385,8 @@ std::vector<char> compile_module(const std::string& source, const std::string& a
 // per (point, neuron) column (the row split of fused.hip.in's split_of is 1).
 static bool alias_tiles(const std::vector<int>& neurons, const FusedTuning& tuning) {
     for (size_t l = 1; l + 1 < neurons.size(); ++l) {
-        const int lanes = tuning.net_points_per_block * neurons[l];
-        const int G = lanes * 4 <= 256 ? 4 : (lanes * 2 <= 256 ? 2 : 1);
+        const int lanes = tuning.net_points_per_block * neurons[l], T = tuning.net_threads;
+        const int G = lanes * 4 <= T ? 4 : (lanes * 2 <= T ? 2 : 1);
         if (std::min(G, tuning.max_split) != 1 || std::min(G, tuning.max_split_adjoint) != 1) return false;
     }
     return true;
@@ -413,6 +413,7 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
     for (int l = 1; l + 1 < L; ++l) widest = std::max(widest, neurons[l]);
     o << "// generated: cPDE layer-fused kernels\n#define CPDE_POINTS " << points_per_block << "\n";
     o << "#define CPDE_NET_POINTS " << net_points_per_block << "\n";
+    o << "#define CPDE_NET_THREADS " << tuning.net_threads << "\n";
     o << "#define CPDE_STRIDE " << ((widest + 7) / 8 * 8 + 4) << "\n";
     // Column tile of the network products: 16 (v_mfma_f32_16x16x4f32) when a
     // block holds one point and every hidden width is a multiple of 16; else 32
@@ -438,8 +439,8 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
     // row splits of the compositions used by the network-fused kernels
     std::vector<int> splits;
     for (int l = 1; l + 1 < L; ++l) {
-        const int lanes = net_points_per_block * neurons[l];
-        const int G = lanes * 4 <= 256 ? 4 : (lanes * 2 <= 256 ? 2 : 1);
+        const int lanes = net_points_per_block * neurons[l], T = tuning.net_threads;
+        const int G = lanes * 4 <= T ? 4 : (lanes * 2 <= T ? 2 : 1);
         for (int cap : {tuning.max_split, tuning.max_split_adjoint}) {
             const int g = std::min(G, cap);
             if (std::find(splits.begin(), splits.end(), g) == splits.end()) splits.push_back(g);
@@ -509,10 +510,11 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
         bwd << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
     bwd << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
     const std::string tiles = tile_declarations();
-    o << "\nextern \"C\" __global__ __launch_bounds__(256, " << tuning.forward_blocks
+    const std::string nt = std::to_string(tuning.net_threads);
+    o << "\nextern \"C\" __global__ __launch_bounds__(" << nt << ", " << tuning.forward_blocks
       << ") void network_forward_k(NetArgs a, int points) {\n"
       << tiles << fwd.str() << "}\n";
-    o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
+    o << "extern \"C\" __global__ __launch_bounds__(" << nt << ", " << tuning.backward_blocks
       << ") void network_backward_k(NetArgs a, int points) {\n"
       << tiles << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n" << bwd.str() << "}\n";
     {
@@ -521,7 +523,7 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
             "    const MatchTerm pre = match_prefetch<" + std::to_string(NO) + ">(m, p0, npts);\n";
         const std::string cost = "    net_match<" + std::to_string(NO) + ">(a, m, " + std::to_string(L - 1) +
                                  ", S, p0, npts, O, O + kNNC * " + std::to_string(NO) + ", pre);\n";
-        o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
+        o << "extern \"C\" __global__ __launch_bounds__(" << nt << ", " << tuning.backward_blocks
           << ") void network_epoch_k(NetArgs a, MatchArgs m, int points) {\n" << epoch_body(neurons, prefetch, cost)
           << "}\n";
     }
@@ -553,7 +555,7 @@ std::string expression_epoch_source(const Tables& t, const std::vector<int>& neu
     emit_prologue(o, t, neurons, tuning);
     const std::string cost = "    net_expression<" + std::to_string(NO) + ">(a, e, " + std::to_string(L - 1) +
                              ", S, p0, npts, O, O + kNNC * " + std::to_string(NO) + ");\n";
-    o << "extern \"C\" __global__ __launch_bounds__(256, " << tuning.backward_blocks
+    o << "extern \"C\" __global__ __launch_bounds__(" << tuning.net_threads << ", " << tuning.backward_blocks
       << ") void network_epoch_expression_k(NetArgs a, ExpressionArgs e, int points) {\n" << epoch_body(neurons, "", cost)
       << "}\n";
     return o.str();

@@ -12,6 +12,7 @@
 namespace cpde {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------------------------------
 // sigma^{(k)}(z), k = 1..7, from q = 1/(1+e^z): the reference's recurrences
@@ -552,21 +553,35 @@ __global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
     const int local = int(blockIdx.x) - a.block_begin[t];
     const int M = a.M[t], N1 = a.N[t] + 1, S = a.splits[t];
     const int count = M * N1;
+    // Sixteen running sums per lane, each fed by an unconditional load (an
+    // index past the last split reads the last split and adds nothing), so a
+    // round's sixteen loads are in flight together; the sums then meet in a
+    // fixed tree.
+    constexpr int U = 16;
+    auto tree = [](float (&acc)[U]) {
+#pragma unroll
+        for (int w = 1; w < U; w *= 2)
+#pragma unroll
+            for (int u = 0; u < U; u += 2 * w) acc[u] += acc[u + w];
+        return acc[0];
+    };
     if (!a.split_minor[t]) {
         const size_t stride = size_t(count);
         const int j = local * 64 + lane;
         float s = 0.0f;
         if (j < count) {
             const float* P = a.partial[t] + j;
-            float acc[8];
+            float acc[U];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
-            int q = wave;
-            for (; q + 28 < S; q += 32)
+            for (int u = 0; u < U; ++u) acc[u] = 0.0f;
+            for (int q = wave; q < S; q += 4 * U) {  // wave w: splits w, w + 4, ...
+                float v[U];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) acc[u] += P[(q + 4 * u) * stride];
-            for (int u = 0; q < S; q += 4, ++u) acc[u] += P[q * stride];
-            s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+                for (int u = 0; u < U; ++u) v[u] = P[size_t(min(q + 4 * u, S - 1)) * stride];
+#pragma unroll
+                for (int u = 0; u < U; ++u) acc[u] += q + 4 * u < S ? v[u] : 0.0f;
+            }
+            s = tree(acc);
         }
         part[wave][lane] = s;
         __syncthreads();
@@ -580,13 +595,17 @@ __global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
         const int j = local * 4 + wave;
         if (j >= count) return;
         const float* P = a.partial[t] + size_t(j) * S;
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four loads in flight per lane
-        int q = lane;
-        for (; q + 192 < S; q += 256)
+        float acc[U];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) acc[u] += P[q + 64 * u];
-        for (int u = 0; q < S; q += 64, ++u) acc[u] += P[q];
-        float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        for (int u = 0; u < U; ++u) acc[u] = 0.0f;
+        for (int q = lane; q < S + 63; q += 64 * U) {  // lane l: splits l, l + 64, ...
+            float v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = P[min(q + 64 * u, S - 1)];
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc[u] += q + 64 * u < S ? v[u] : 0.0f;
+        }
+        float s = tree(acc);
         for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
         if (lane == 0) {
             const int mrow = j / N1, n = j - mrow * N1;
@@ -595,10 +614,232 @@ __global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
         }
     }
 }
+// Direct weight-gradient tiles, for short reductions: a workgroup owns one
+// 64x64 tile of dW over its split's columns, and its four waves take the
+// split's 4-column groups in turn (wave w: groups w, w + 4, ...).  Operands
+// come straight from global memory into registers, no LDS staging: lane l
+// loads the float4 G[c][m0 + 4(l%16) .. +3] and Y[c][n0 + 4(l%16) .. +3] of
+// column c = c0 + l/16, and that pair feeds sixteen v_mfma_f32_16x16x4f32 --
+// tile (tr, tc) takes component tr of the G float4 as A[l%16][l/16] and
+// component tc of the Y float4 as B[l/16][l%16], so its accumulator register
+// v of lane l is dW(m0 + 4(4(l/16) + v) + tr, n0 + 4(l%16) + tc).  The
+// workgroup then sums its four waves' tiles in LDS in the fixed order
+// (w0 + w2) + (w1 + w3) and writes its split's partial, as the LDS-staged
+// tiles do.  The bias (n-tile 0 only) is the sum of G over value-row columns.
+constexpr int kWdStride = 65;                  // LDS row stride of a 64x64 tile
+constexpr int kWdLds = 2 * 64 * kWdStride;     // two tiles; also the thin roles' 256 x 17 scratch
+constexpr int kWdDepth = 2;                    // column groups loaded ahead
+
+// 4 consecutive entries [w0, w0 + 4) of row c of a [column][width] stack
+// (offset = c * width + w0).  MASK: zeros beyond the width -- VEC (width % 4
+// == 0) then loads the float4 only where it is inside; unmasked, the load is
+// unconditional (full tiles).
+template <bool VEC, bool MASK>
+__device__ __forceinline__ float4 wd_load(const float* __restrict__ base, unsigned offset, int w0, int width) {
+    const float* p = base + offset;
+    if constexpr (!MASK) {
+        return *reinterpret_cast<const float4*>(p);
+    } else if constexpr (VEC) {
+        return w0 < width ? *reinterpret_cast<const float4*>(p) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    } else {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (w0 + 0 < width) v.x = p[0];
+        if (w0 + 1 < width) v.y = p[1];
+        if (w0 + 2 < width) v.z = p[2];
+        if (w0 + 3 < width) v.w = p[3];
+        return v;
+    }
+}
+
+// The main loop of a direct tile: acc += this wave's columns of G^T Y.
+template <bool VEC, bool MASK>
+__device__ __forceinline__ void wd_accumulate(floatx4 (&acc)[4][4], const float* __restrict__ G,
+                                              const float* __restrict__ Y, int M, int N, int kbegin, int kend,
+                                              int gm, int yn, int wave, int q) {
+    auto mma = [&](const float4 g, const float4 y) {
+        const float gv[4] = {g.x, g.y, g.z, g.w}, yv[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int z = 0; z < 4; ++z)
+                acc[x][z] = __builtin_amdgcn_mfma_f32_16x16x4f32(gv[x], yv[z], acc[x][z], 0, 0, 0);
+    };
+    // full steps of 16 columns (this wave's column c = kbegin + 16 s + 4 wave + q),
+    // loaded kWdDepth steps ahead; then at most one partial step with the
+    // columns beyond the split zeroed.  The steady-state loop is branch-free,
+    // so the loads stay in flight across its iterations.
+    const int full = (kend - kbegin) / 16;
+    const unsigned c0 = unsigned(kbegin + 4 * wave + q);
+    unsigned go = c0 * unsigned(M) + unsigned(gm), yo = c0 * unsigned(N) + unsigned(yn);
+    const unsigned gstep = 16u * unsigned(M), ystep = 16u * unsigned(N);
+    if (full >= kWdDepth) {
+        float4 gb[kWdDepth], yb[kWdDepth];
+#pragma unroll
+        for (int d = 0; d < kWdDepth; ++d) {
+            gb[d] = wd_load<VEC, MASK>(G, go, gm, M);
+            yb[d] = wd_load<VEC, MASK>(Y, yo, yn, N);
+            go += gstep;
+            yo += ystep;
+        }
+        int s0 = 0;
+#pragma unroll 1
+        for (; s0 + 2 * kWdDepth <= full; s0 += kWdDepth) {
+            // the next kWdDepth steps' loads go out first (kept at the top of
+            // the body: scheduled later, their latency would fall on the next
+            // iteration's first products)
+            float4 gn[kWdDepth], yn4[kWdDepth];
+#pragma unroll
+            for (int d = 0; d < kWdDepth; ++d) {
+                gn[d] = wd_load<VEC, MASK>(G, go, gm, M);
+                yn4[d] = wd_load<VEC, MASK>(Y, yo, yn, N);
+                go += gstep;
+                yo += ystep;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int d = 0; d < kWdDepth; ++d) mma(gb[d], yb[d]);
+#pragma unroll
+            for (int d = 0; d < kWdDepth; ++d) {
+                gb[d] = gn[d];
+                yb[d] = yn4[d];
+            }
+        }
+        // steps s0 .. s0 + kWdDepth - 1 are loaded; fewer than kWdDepth full steps follow
+#pragma unroll
+        for (int d = 0; d < kWdDepth; ++d) mma(gb[d], yb[d]);
+        for (int s = s0 + kWdDepth; s < full; ++s) {
+            mma(wd_load<VEC, MASK>(G, go, gm, M), wd_load<VEC, MASK>(Y, yo, yn, N));
+            go += gstep;
+            yo += ystep;
+        }
+    } else {
+        for (int s = 0; s < full; ++s) {
+            mma(wd_load<VEC, MASK>(G, go, gm, M), wd_load<VEC, MASK>(Y, yo, yn, N));
+            go += gstep;
+            yo += ystep;
+        }
+    }
+    if (full * 16 < kend - kbegin) {
+        const int c = kbegin + 16 * full + 4 * wave + q;
+        float4 g = make_float4(0.0f, 0.0f, 0.0f, 0.0f), y = g;
+        if (c < kend) {
+            g = wd_load<VEC, MASK>(G, unsigned(c) * unsigned(M) + unsigned(gm), gm, M);
+            y = wd_load<VEC, MASK>(Y, unsigned(c) * unsigned(N) + unsigned(yn), yn, N);
+        }
+        mma(g, y);
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void wgrad_direct_tile(const WgradArgs& a, int t, int local, float* lds) {
+    const int M = a.M[t], N = a.N[t], K = a.K, R = a.R;
+    const int tiles_m = (M + 63) / 64, tiles_n = (N + 63) / 64;
+    const int tile = local % (tiles_m * tiles_n), split = local / (tiles_m * tiles_n);
+    const int m0 = (tile % tiles_m) * 64, n0 = (tile / tiles_m) * 64;
+    const int kbegin = split * a.kchunk[t], kend = min(K, kbegin + a.kchunk[t]);
+    const float* __restrict__ G = a.G[t];
+    const float* __restrict__ Y = a.Y[t];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15, q = lane >> 4;
+    const int gm = m0 + 4 * j, yn = n0 + 4 * j;
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) acc[x][y] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (VEC && m0 + 64 <= M && n0 + 64 <= N) wd_accumulate<VEC, false>(acc, G, Y, M, N, kbegin, kend, gm, yn, wave, q);
+    else wd_accumulate<VEC, true>(acc, G, Y, M, N, kbegin, kend, gm, yn, wave, q);
+    // (w0 + w2) + (w1 + w3): waves 2 and 3 store, waves 0 and 1 add
+    auto store = [&](float* T) {
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int z = 0; z < 4; ++z)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) T[(4 * (4 * q + v) + x) * kWdStride + 4 * j + z] = acc[x][z][v];
+    };
+    auto add = [&](const float* T) {
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int z = 0; z < 4; ++z)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[x][z][v] += T[(4 * (4 * q + v) + x) * kWdStride + 4 * j + z];
+    };
+    if (wave >= 2) store(lds + (wave - 2) * 64 * kWdStride);
+    __syncthreads();
+    if (wave < 2) add(lds + wave * 64 * kWdStride);
+    __syncthreads();
+    if (wave == 1) store(lds);
+    __syncthreads();
+    if (wave == 0) add(lds);
+    float* P = a.partial[t] + size_t(split) * M * (N + 1);
+    if (wave == 0) {
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int m = m0 + 4 * (4 * q + v) + x;
+                if (m >= M) continue;
+#pragma unroll
+                for (int z = 0; z < 4; ++z) {
+                    const int n = yn + z;
+                    if (n < N) P[size_t(m) * (N + 1) + n] = acc[x][z][v];
+                }
+            }
+    }
+    // bias (n-tile 0): the sum of G over the split's value-row columns; lane
+    // group (wave, q) takes value columns first + R (4 wave + q + 16 i) for its
+    // 4 rows, the sixteen groups then meet in a fixed order
+    if (n0 == 0) {
+        float4 bias = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const int first = (kbegin + R - 1) / R * R;
+        for (int c = first + R * (4 * wave + q); c < kend; c += 16 * R) {
+            const float4 g = wd_load<VEC, true>(G, unsigned(c) * unsigned(M) + unsigned(gm), gm, M);
+            bias.x += g.x;
+            bias.y += g.y;
+            bias.z += g.z;
+            bias.w += g.w;
+        }
+        bias.x += __shfl_xor(bias.x, 16);
+        bias.y += __shfl_xor(bias.y, 16);
+        bias.z += __shfl_xor(bias.z, 16);
+        bias.w += __shfl_xor(bias.w, 16);
+        bias.x += __shfl_xor(bias.x, 32);
+        bias.y += __shfl_xor(bias.y, 32);
+        bias.z += __shfl_xor(bias.z, 32);
+        bias.w += __shfl_xor(bias.w, 32);
+        float* bias_lds = lds + 64 * kWdStride;  // wave 1's tile slot, free since the second barrier
+        if (q == 0) {
+            bias_lds[wave * 64 + 4 * j + 0] = bias.x;
+            bias_lds[wave * 64 + 4 * j + 1] = bias.y;
+            bias_lds[wave * 64 + 4 * j + 2] = bias.z;
+            bias_lds[wave * 64 + 4 * j + 3] = bias.w;
+        }
+        __syncthreads();
+        if (wave == 0 && m0 + lane < M)
+            P[size_t(m0 + lane) * (N + 1) + N] =
+                (bias_lds[lane] + bias_lds[128 + lane]) + (bias_lds[64 + lane] + bias_lds[192 + lane]);
+    }
+}
+
+// Direct tiles and the thin transitions' roles in one launch; three
+// workgroups per CU (33 KB of LDS each).
+__global__ __launch_bounds__(256, 3) void wgrad_direct_kernel(WgradArgs a) {
+    __shared__ __attribute__((aligned(16))) float lds[kWdLds];
+    static_assert(256 * 17 <= kWdLds, "thin-transition scratch exceeds the shared LDS");
+    const int b = xcd_grouped(int(blockIdx.x), int(gridDim.x));
+    int t = 0;
+    while (t + 1 < a.transitions && b >= a.block_begin[t + 1]) ++t;
+    const int local = b - a.block_begin[t];
+    if (a.M[t] <= 16 || a.N[t] <= 16) wgrad_thin(a, t, local, lds);
+    else if (a.M[t] % 4 == 0 && a.N[t] % 4 == 0) wgrad_direct_tile<true>(a, t, local, lds);
+    else wgrad_direct_tile<false>(a, t, local, lds);
+}
 
 void launch_wgrad_grouped(Device& d, const WgradArgs& a, double flops) {
     TraceScope trace(d, kTraceWgrad, flops);
-    hipLaunchKernelGGL(wgrad_grouped_kernel, a.block_begin[a.transitions], 256, 0, d.stream, a);
+    if (a.direct) hipLaunchKernelGGL(wgrad_direct_kernel, a.block_begin[a.transitions], 256, 0, d.stream, a);
+    else hipLaunchKernelGGL(wgrad_grouped_kernel, a.block_begin[a.transitions], 256, 0, d.stream, a);
     HIP_CHECK(hipGetLastError());
 }
 

@@ -154,6 +154,37 @@ def test_epoch_matches_oracle(device, path, order, neurons, points, chunk):
     run.close()
 
 
+@pytest.mark.parametrize('order,neurons,points', [
+    (4, [2, 128, 128, 1], 729),   # 64x64 tiles over short splits: direct tiles by default
+    (6, [2, 64, 48, 1], 300),
+    (3, [2, 30, 18, 1], 101),     # widths that are not multiples of 4: scalar operand loads
+    (2, [2, 80, 96, 40, 1], 2000),
+])
+def test_weight_gradient_tile_forms(device, monkeypatch, order, neurons, points):
+    """The weight gradient's direct tiles (operands from global memory straight
+    into the matrix cores) and LDS-staged tiles, forced in turn
+    (CPDE_WGRAD_DIRECT 2 and 0): each against the oracle, and the two within
+    fp32 summation-order noise of each other."""
+    print(f'[case] wgrad forms order={order} neurons={neurons} points={points}', flush=True)
+    wl = small_workload(order, neurons, points)
+    ref_loss, ref_grads = oracle_epoch(order, tuple(neurons), points, 0)
+    got = {}
+    for form in ('2', '0'):
+        monkeypatch.setenv('CPDE_WGRAD_DIRECT', form)
+        run = hip.MatchingRun(device, wl)
+        run.step()
+        device.synchronize()
+        got[form] = run.gradients()
+        assert abs(run.loss() / ref_loss - 1) < 1e-4
+        run.close()
+        for t, (g, r) in enumerate(zip(got[form], ref_grads)):
+            e = rel_l2(g, r)
+            print(f'[result] form {form} transition {t} gradient rel-L2 {e:.3e}', flush=True)
+            assert e < 1e-3
+    for a, b in zip(got['2'], got['0']):
+        assert rel_l2(a, b) < 1e-5
+
+
 PAIRED_ALIASED = dict(CPDE_FUSED='2', CPDE_NET_POINTS='2', CPDE_NET_ALIAS='1', CPDE_NET_COLTILE='16',
                       CPDE_NET_SPLIT='1', CPDE_NET_SPLIT_ADJOINT='1')
 
@@ -183,6 +214,31 @@ def test_paired_aliased_network_forms(device, monkeypatch, order, neurons, point
         e = rel_l2(g, r)
         print(f'[result] transition {t} gradient rel-L2 {e:.3e}', flush=True)
         assert e < 1e-3
+    run.close()
+
+
+@pytest.mark.parametrize('order,neurons,points,per_block', [
+    (6, [2, 128, 128, 128, 1], 100, 3),   # one-pass epoch, three points per 512-lane workgroup
+    (4, [2, 64, 48, 1], 61, 2),
+    (5, [2, 80, 96, 1], 4101, 2),         # separate forward and backward launches
+])
+def test_network_kernels_with_eight_waves(device, monkeypatch, order, neurons, points, per_block):
+    """The network kernels on 512-lane workgroups (CPDE_NET_THREADS=512: eight
+    waves share the products' row blocks) against the oracle."""
+    monkeypatch.setenv('CPDE_FUSED', '2')
+    monkeypatch.setenv('CPDE_NET_THREADS', '512')
+    monkeypatch.setenv('CPDE_NET_POINTS', str(per_block))
+    print(f'[case] eight waves order={order} neurons={neurons} points={points} per_block={per_block}', flush=True)
+    wl = small_workload(order, neurons, points)
+    run = hip.MatchingRun(device, wl)
+    run.step()
+    device.synchronize()
+    loss, grads = run.loss(), run.gradients()
+    ref_loss, ref_grads = oracle_epoch(order, tuple(neurons), points, 0)
+    print(f'[result] loss {loss!r} oracle {ref_loss!r}', flush=True)
+    assert abs(loss / ref_loss - 1) < 1e-4
+    for t, (g, r) in enumerate(zip(grads, ref_grads)):
+        assert rel_l2(g, r) < 1e-3, t
     run.close()
 
 
