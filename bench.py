@@ -53,14 +53,15 @@ MFMA_KINDS = {'gemm_forward', 'gemm_transposed', 'gemm_wgrad', 'fused_forward', 
 CPU_SAMPLE_MACS = 3.0e9
 
 # HBM bytes per launch from rocprofv3 counter passes over this benchmark
-# (profiles/network_kernels_fourier_fit_order6_traffic.md): mean FETCH_SIZE and
+# (profiles/network_kernels_<workload>_traffic.md): mean FETCH_SIZE and
 # WRITE_SIZE in KiB per dispatch, scaled by what the same counters read for a
-# plain 256 MiB copy (``--copy-calibration``): 268,435,456 B / 131,084.56 KiB
+# plain 256 MiB copy (``--copy-calibration``): 268,435,456 B / 131,084.475 KiB
 # read, 268,435,456 B / 262,144 KiB written.
-COPY_SCALE = (268435456 / (131084.5625 * 1024), 268435456 / (262144 * 1024))
+COPY_SCALE = (268435456 / (131084.475 * 1024), 268435456 / (262144 * 1024))
 TRAFFIC_KIB = {
-    'fourier_fit_order6': {'network_epoch': (24141.80, 140462.07), 'gemm_wgrad': (30704.50, 7740.00),
-                           'network_backward': (27619.29, 53473.79), 'network_forward': (1483.53, 83919.40)},
+    'fourier_fit_order6': {'network_epoch': (24131.83, 140509.01), 'gemm_wgrad': (30982.37, 7740.57)},
+    'fourier_large_order6': {'network_backward': (5014165.6, 8780106.3), 'network_forward': (427992.19, 14688010.08),
+                             'gemm_wgrad': (7914105.67, 35085.07)},
 }
 
 
