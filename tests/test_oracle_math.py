@@ -113,7 +113,7 @@ def test_pair_tables_small_case():
     assert d[j, i] == -1
 
 
-@pytest.mark.parametrize('ta,tb', [(0, 0), (1, 0), (0, 1)])
+@pytest.mark.parametrize('ta,tb', [(0, 0), (1, 0), (0, 1), (1, 1)])
 def test_gemm_against_float64(ta, tb):
     rng = np.random.default_rng(4)
     m, n, k = 7, 9, 13
