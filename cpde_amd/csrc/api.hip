@@ -270,6 +270,7 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
     t.backward_blocks = std::max(1, env_int("CPDE_NET_BWD_OCC", t.backward_blocks));
     t.col_tile = env_int("CPDE_NET_COLTILE", t.col_tile);
     t.alias = env_int("CPDE_NET_ALIAS", t.alias);
+    t.scaled = env_int("CPDE_SCALED", t.scaled) ? 1 : 0;
     return t;
 }
 
@@ -285,6 +286,7 @@ static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const
     m->points_per_block = tune.points_per_block;
     m->net_points_per_block = tune.net_points_per_block;
     m->net_threads = tune.net_threads;
+    m->scaled = tune.scaled != 0;
     HIP_CHECK(hipModuleLoadData(&m->module, code.data()));
     HIP_CHECK(hipModuleGetFunction(&m->network_forward, m->module, "network_forward_k"));
     HIP_CHECK(hipModuleGetFunction(&m->network_backward, m->module, "network_backward_k"));
@@ -952,6 +954,21 @@ int cpde_plan_stack(cpde_plan* plan, int layer, int kind, float** device_ptr) {
         float* p = kind == 0 || kind == 3 ? (layer == 0 ? plan->input : n.z[layer]) : kind == 1 ? n.y[layer] : n.g[layer];
         require(p != nullptr, "stack not present for this layer");
         *device_ptr = p;
+    });
+}
+
+int cpde_plan_stack_scale(cpde_plan* plan, int layer, int kind, float* row_factor) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        require(layer >= 0 && layer < n.layers && kind >= 0 && kind <= 3 && row_factor, "invalid stack");
+        // scaled network kernels: sigmoid layers hold y, u as row / alpha! and dE/dz as alpha! dE/dz
+        const bool scaled = plan->fused && plan->network && plan->fused->scaled && !n.linear[layer] && kind != 0;
+        for (int r = 0; r < plan->rows; ++r) {
+            double f = 1.0;
+            for (int v = 0; v < plan->tables.variables; ++v)
+                for (int k = 2; k <= plan->tables.table[r * (plan->tables.variables + 1) + 1 + v]; ++k) f *= k;
+            row_factor[r] = !scaled ? 1.0f : kind == 2 ? float(1.0 / f) : float(f);
+        }
     });
 }
 

@@ -224,9 +224,10 @@ struct FusedModule {
     std::vector<hipFunction_t> hidden_forward, hidden_backward;  // per transition (index t)
     hipFunction_t network_forward = nullptr, network_backward = nullptr, network_epoch = nullptr;
     int points_per_block = 2, net_points_per_block = 1, net_threads = 256;
+    bool scaled = false;  // sigmoid stacks of the network kernels hold row alpha / alpha! (dE/dz: times alpha!)
     ~FusedModule();
 };
-std::string compose_source(const Tables& t, const std::vector<int>& splits);
+std::string compose_source(const Tables& t, const std::vector<int>& splits, bool scaled = false);
 // Launch-shape choices of the fused kernels (environment overrides in api.hip).
 struct FusedTuning {
     int points_per_block = 2;      // layer-fused kernels
@@ -237,7 +238,11 @@ struct FusedTuning {
     int alias = 0;                 // network kernels: products write over their operand tile (one LDS tile)
     int forward_blocks = 2, backward_blocks = 2;  // blocks per CU the register budget must allow
     int col_tile = 0;              // column tile of the network products: 16, 32, or 0 (chosen per shape)
+    int scaled = 1;                // network kernels keep Taylor-scaled sigmoid stacks (row alpha / alpha!)
 };
+// Whether the schema is closed under swapping variables 0 and 1 (the scaled
+// forward composition then splits over two lanes, one per mirror image).
+bool mirror_symmetric(const Tables& t);
 std::string fused_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning);
 std::string expression_epoch_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning,
                                     const std::string& program);

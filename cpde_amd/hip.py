@@ -57,6 +57,7 @@ SIGNATURES = {
     'cpde_plan_create': (i32, [vp, i32, i32, vp, i32, i32, ctypes.POINTER(vp)]),
     'cpde_plan_destroy': (i32, [vp]),
     'cpde_plan_stack': (i32, [vp, i32, i32, ctypes.POINTER(vp)]),
+    'cpde_plan_stack_scale': (i32, [vp, i32, i32, vp]),
     'cpde_activate': (i32, [vp, vp, i32, vp, i32, i32]),
     'cpde_forward': (i32, [vp]),
     'cpde_output': (i32, [vp, vp, i32, vp, i32, i32]),
@@ -294,6 +295,16 @@ class Plan:
         n = self.net.neurons[layer]
         a = self.net.device.download_ptr(self.stack_ptr(layer, kind), np.float32, self.width * self.rows * n)
         return a.reshape(self.width, self.rows, n)
+
+    def stack_scale(self, layer, kind):
+        """(rows,) factors turning stored rows of a stack into unscaled rows."""
+        f = np.zeros(self.rows, np.float32)
+        check(load().cpde_plan_stack_scale(self.handle, layer, kind, _ptr(f)))
+        return f
+
+    def unscaled_stack(self, layer, kind):
+        """stack() with every row in the reference's (unscaled) form."""
+        return self.stack(layer, kind) * self.stack_scale(layer, kind)[None, :, None]
 
     def set_stack(self, layer, kind, values):
         self.net.device.upload_ptr(self.stack_ptr(layer, kind), np.ascontiguousarray(values, np.float32))

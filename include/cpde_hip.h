@@ -129,6 +129,13 @@ int cpde_plan_destroy(cpde_plan* plan);
  * sigma'(z0)).  Network-fused plans keep u instead of z for sigmoid layers
  * (their adjoint needs only u); other plans keep z.  Layout [point][row][neuron]. */
 int cpde_plan_stack(cpde_plan* plan, int layer, int kind, float** device_ptr);
+/* Network-fused plans keep sigmoid layers' stacks Taylor-scaled: row alpha of y
+ * and u holds d^alpha / alpha!, and of dE/dz holds alpha! dE/dz_alpha (the
+ * adjoint of the scaled rows).  This fills row_factor[rows] with the factor
+ * that turns a stored row into the reference's row (all ones for unscaled
+ * stacks).  No counterpart in the reference, whose stacks are unscaled; for
+ * callers that inspect stacks. */
+int cpde_plan_stack_scale(cpde_plan* plan, int layer, int kind, float* row_factor);
 
 /* ---- hot path ---------------------------------------------------------------------- */
 /* Server::activate (cuda/cpde_server.cu:158-170): copy the chunk's rows of wire

@@ -25,10 +25,12 @@ def device():
     d.close()
 
 
-@pytest.fixture(params=['network', 'layer', 'table'])
+@pytest.fixture(params=['network', 'partition', 'layer', 'table'])
 def path(request, monkeypatch):
     """Which kernel family a plan uses (chosen at plan creation): the
-    schema-specialised network-fused or layer-fused kernels, or the
-    table-driven ones."""
-    monkeypatch.setenv('CPDE_FUSED', {'network': '2', 'layer': '1', 'table': '0'}[request.param])
+    schema-specialised network-fused kernels on Taylor-scaled stacks (the
+    default) or on unscaled stacks with partition-sum compositions, the
+    layer-fused kernels, or the table-driven ones."""
+    monkeypatch.setenv('CPDE_FUSED', {'network': '2', 'partition': '2', 'layer': '1', 'table': '0'}[request.param])
+    monkeypatch.setenv('CPDE_SCALED', '0' if request.param == 'partition' else '1')
     return request.param

@@ -67,10 +67,10 @@ def test_linear_step_and_composition(device, path, name):
     plan.forward()
     device.synchronize()
     want = linear_step(schema, data, w0, n)
-    if path == 'network':
+    if path in ('network', 'partition'):
         zref = hip.stack_to_reference(want).reshape(R, -1).astype(np.float32)
         uref = oracle.compose_prime(schema, zref).reshape(R, points, n)
-        u1 = hip.stack_to_reference(plan.stack(1, 3))
+        u1 = hip.stack_to_reference(plan.unscaled_stack(1, 3))
         err = scaled_error(u1, uref, axis=(1, 2))
         print(f'[result] {name} sigma-prime jet scaled error {err:.3e}', flush=True)
         assert err < 1e-4
@@ -78,7 +78,7 @@ def test_linear_step_and_composition(device, path, name):
         z1 = plan.stack(1, 0)                   # (points, R, n)
         assert scaled_error(z1, want) < 2e-5
         zref = hip.stack_to_reference(z1).reshape(R, -1)
-    y1 = plan.stack(1, 1)
+    y1 = plan.unscaled_stack(1, 1)
     yref = oracle.compose(schema, zref).reshape(R, points, n)
     err = scaled_error(hip.stack_to_reference(y1), yref, axis=(1, 2))
     print(f'[result] {name} composition scaled error {err:.3e}', flush=True)
@@ -103,14 +103,14 @@ def test_adjoint_composition(device, path, name):
     plan.matching(tbuf, points, trows, wts, 1, 0, points, 0)
     plan.backward(False)
     device.synchronize()
-    if path == 'network':  # z is not kept: the float64 linear step stands in
+    if path in ('network', 'partition'):  # z is not kept: the float64 linear step stands in
         z1 = hip.stack_to_reference(linear_step(schema, data, w0, n)).reshape(R, -1).astype(np.float32)
     else:
         z1 = hip.stack_to_reference(plan.stack(1, 0)).reshape(R, -1)
-    g2 = plan.stack(2, 2)[:, :, 0].astype(np.float64)         # (points, R)
+    g2 = plan.unscaled_stack(2, 2)[:, :, 0].astype(np.float64)         # (points, R)
     gy = np.einsum('i,pr->rpi', w1[:n].astype(np.float64), g2).reshape(R, -1).astype(np.float32)
     gz_ref = oracle.compose_adjoint(schema, z1, gy).reshape(R, points, n)
-    gz = hip.stack_to_reference(plan.stack(1, 2))
+    gz = hip.stack_to_reference(plan.unscaled_stack(1, 2))
     err = scaled_error(gz, gz_ref, axis=(1, 2))
     print(f'[result] {name} adjoint scaled error {err:.3e}', flush=True)
     assert err < 1e-4
