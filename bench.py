@@ -253,8 +253,7 @@ def run_direct(wl, steps, warmup, trace_steps, settle_ms):
     run = hip.MatchingRun(device, wl)
 
     def step():
-        run.step(collect=True)
-        run.net.rprop()
+        run.step(collect=True, update=True)
 
     settled = settle(step, device.synchronize, settle_ms)
     for _ in range(warmup):

@@ -521,9 +521,20 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
     return g;
 }
 
-static void run_gradients(Device& d, const GradientPlan& g) {
+// `update`: the reduction also applies RPROP to the group's transitions
+// (transitions [first, first + count) of `update`), whose gradients it
+// completes; the caller flips the active buffers once every group is done.
+static void run_gradients(Device& d, const GradientPlan& g, Net* update = nullptr, int first = 0) {
     if (g.wa.transitions > 0) launch_wgrad_grouped(d, g.wa, g.flops);
-    launch_reduce_grouped(d, g.ra);
+    if (update) launch_reduce_rprop(d, g.ra, *update, first);
+    else launch_reduce_grouped(d, g.ra);
+}
+
+// Host bookkeeping of an RPROP update launched as part of a reduction
+// (launch_rprop does the same after its own launch).
+static void rprop_done(Net& n) {
+    for (auto& act : n.active) act = act == 1 ? 2 : 1;
+    n.wt_current = true;
 }
 
 // Host mirror of the one-pass epoch's matching arguments (fused.hip.in MatchArgs).
@@ -577,7 +588,7 @@ static CostStats* epoch_records(Plan& p) {
 // weight-gradient split partials go.  Everything that can be refused is
 // checked before the first launch.
 static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostStats* records, int cost_index,
-                           bool accumulate, PartialSpace space = {}) {
+                           bool accumulate, PartialSpace space = {}, bool update = false) {
     Net& n = *p.net;
     Device& d = *n.dev;
     const int L = n.layers;
@@ -623,7 +634,8 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostS
     } else {
         launch_finish_cost(d, records, blocks, cost_index);
     }
-    run_gradients(d, g);
+    run_gradients(d, g, update ? &n : nullptr, 0);
+    if (update) rprop_done(n);
 }
 
 // The plan's one-pass epoch kernel for an expression program: the program's
@@ -1053,6 +1065,29 @@ int cpde_epoch_matching(cpde_plan* plan, const float* target, int target_width, 
         MatchArgsHost m{target, target_rows, weights, records, target_width, weight_samples, offset, valid,
                         collect != 0};
         one_pass_epoch(*plan, plan->fused->network_epoch, &m, records, cost_index, accumulate != 0);
+    });
+}
+
+int cpde_epoch_matching_rprop(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
+                              const float* weights, int weight_samples, int offset, int valid, int cost_index,
+                              int collect, int accumulate) {
+    return guarded([&] {
+        Net& n = *plan->net;
+        Device& d = *n.dev;
+        require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
+        require(plan->backward, "plan has no adjoint storage");
+        require(valid >= 0 && valid <= plan->width && offset >= 0, "invalid chunk range");
+        if (!one_pass_fits(*plan) || n.layers - 1 > kMaxTransitions) {
+            if (int code = cpde_epoch_matching(plan, target, target_width, target_rows, weights, weight_samples, offset,
+                                               valid, cost_index, collect, accumulate))
+                throw_code(code);
+            launch_rprop(d, n);
+            return;
+        }
+        CostStats* records = epoch_records(*plan);
+        MatchArgsHost m{target, target_rows, weights, records, target_width, weight_samples, offset, valid,
+                        collect != 0};
+        one_pass_epoch(*plan, plan->fused->network_epoch, &m, records, cost_index, accumulate != 0, {}, true);
     });
 }
 

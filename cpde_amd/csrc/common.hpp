@@ -297,6 +297,7 @@ void launch_fill(Device& d, float* p, size_t count, float value);
 void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, int NI, int NO, int R, int columns);
 void launch_wgrad_grouped(Device& d, const WgradArgs& a, double flops);
 void launch_reduce_grouped(Device& d, const ReduceArgs& a);
+void launch_reduce_rprop(Device& d, const ReduceArgs& a, Net& net, int first);
 void launch_rprop(Device& d, Net& net);
 void launch_adam(Device& d, Net& net, int step, float lr);
 void launch_set_steps(Device& d, Net& net, float value);

@@ -530,6 +530,63 @@ __global__ __launch_bounds__(256, 2) void wgrad_grouped_kernel(WgradArgs a) {
     else wgrad_tile<128>(a, t, local, lds);
 }
 
+// Optimizers: one launch covers every transition.  Each transition's buffers
+// are separate allocations; the launch carries their pointers by value.
+struct OptimizerArgs {
+    float* W[kMaxTransitions];
+    float* S[kMaxTransitions];   // RPROP step / Adam first moment
+    float* Ga[kMaxTransitions];  // active gradient
+    float* Gi[kMaxTransitions];  // inactive gradient / Adam second moment
+    float* WT[kMaxTransitions];  // row-major copy of the weights, kept current by RPROP and Adam
+    int NO[kMaxTransitions], NI[kMaxTransitions];
+    int begin[kMaxTransitions + 1];
+    int block_begin[kMaxTransitions + 1];  // blocks of kOptimizerThreads entries, per transition
+    int transitions;
+};
+
+constexpr int kOptimizerThreads = 256;
+
+// Entry j = o + NO*i of a weight block into its row-major copy (bias column i = NI excluded).
+__device__ __forceinline__ void copy_transposed(const OptimizerArgs& a, int t, int j, float w) {
+    const int i = j / a.NO[t], o = j - i * a.NO[t];
+    if (i < a.NI[t]) a.WT[t][i + a.NI[t] * o] = w;
+}
+
+
+// Resile_k (cuda/derivative_kernels_v4.cu:752-778) on entry j of transition t
+// with gradient g: sign tests on float products, the gradient kept (or zeroed
+// on a rollback or a rejected step) in the active buffer.  The optimizers
+// round every product and sum separately, as the reference's CPU build does:
+// no multiply-add contraction (hipcc contracts by default, and
+// __fmul_rn/__fadd_rn do not prevent it).
+__device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int j, float g) {
+#pragma clang fp contract(off)
+    float* W = a.W[t] + j;
+    float* step = a.S[t] + j;
+    const float gi = a.Gi[t][j];
+    const float prod = g * gi;
+    float s = *step;
+    if (prod > 0) s *= 1.2f;
+    const float w = *W;
+    const float nW = w - copysignf(s, g);
+    float kept = w, kept_g = g;
+    if (prod < 0) {
+        kept = w + copysignf(s, gi);
+        s *= 0.5f;
+        kept_g = 0.0f;
+    } else if (g != 0.0f) {
+        if (fabsf(nW) <= 20.0f) kept = nW;
+        else {
+            s = 0.1f;
+            kept_g = 0.0f;
+        }
+    }
+    a.Ga[t][j] = kept_g;
+    *W = kept;
+    *step = s;
+    copy_transposed(a, t, j, kept);
+}
+
 // grad_t[m + M*n] (+)= sum over splits of the partials of entry (m, n), n = N
 // being the bias.  Split-major partials ([split][entry]): block = 64 consecutive
 // entries x 4 waves, wave w sums splits w, w+4, ... (eight running sums,
@@ -541,7 +598,11 @@ __global__ __launch_bounds__(256, 2) void wgrad_grouped_kernel(WgradArgs a) {
 __device__ void finish_cost_records(const CostStats* __restrict__ records, int count, CostStats* __restrict__ total,
                                     int overwrite);
 
-__global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
+// UPDATE: the lane that finishes an entry's gradient applies RPROP to it
+// (reduce_rprop_kernel), which is the reduction followed by rprop_kernel in one
+// launch, bit for bit.
+template <bool UPDATE>
+__device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const OptimizerArgs& o) {
     __shared__ float part[4][64];
     if (a.cost_count && int(blockIdx.x) == a.block_begin[a.transitions]) {
         finish_cost_records(a.cost_partials, a.cost_count, a.cost_total, a.cost_overwrite);
@@ -588,8 +649,10 @@ __global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
         if (wave == 0 && j < count) {
             const float sum = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
             const int mrow = j / N1, n = j - mrow * N1;
-            float* g = a.grad[t] + mrow + size_t(M) * n;
-            *g = a.accumulate ? *g + sum : sum;
+            const int idx = mrow + M * n;
+            const float v = a.accumulate ? a.grad[t][idx] + sum : sum;
+            if constexpr (UPDATE) rprop_update(o, t, idx, v);
+            else a.grad[t][idx] = v;
         }
     } else {
         const int j = local * 4 + wave;
@@ -609,10 +672,18 @@ __global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) {
         for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
         if (lane == 0) {
             const int mrow = j / N1, n = j - mrow * N1;
-            float* g = a.grad[t] + mrow + size_t(M) * n;
-            *g = a.accumulate ? *g + s : s;
+            const int idx = mrow + M * n;
+            const float v = a.accumulate ? a.grad[t][idx] + s : s;
+            if constexpr (UPDATE) rprop_update(o, t, idx, v);
+            else a.grad[t][idx] = v;
         }
     }
+}
+
+__global__ __launch_bounds__(256) void reduce_grouped_kernel(ReduceArgs a) { reduce_grouped<false>(a, OptimizerArgs{}); }
+
+__global__ __launch_bounds__(256) void reduce_rprop_kernel(ReduceArgs a, OptimizerArgs o) {
+    reduce_grouped<true>(a, o);
 }
 // Direct weight-gradient tiles, for short reductions: a workgroup owns one
 // 64x64 tile of dW over its split's columns, and its four waves take the
@@ -840,6 +911,34 @@ void launch_wgrad_grouped(Device& d, const WgradArgs& a, double flops) {
     TraceScope trace(d, kTraceWgrad, flops);
     if (a.direct) hipLaunchKernelGGL(wgrad_direct_kernel, a.block_begin[a.transitions], 256, 0, d.stream, a);
     else hipLaunchKernelGGL(wgrad_grouped_kernel, a.block_begin[a.transitions], 256, 0, d.stream, a);
+    HIP_CHECK(hipGetLastError());
+}
+
+// The reduction of a gradient group followed by RPROP on the same
+// transitions: transitions [first, first + a.transitions) of `net`, whose
+// active gradient buffers are a.grad.
+void launch_reduce_rprop(Device& d, const ReduceArgs& a, Net& net, int first) {
+    OptimizerArgs o{};
+    o.transitions = a.transitions;
+    for (int k = 0; k < a.transitions; ++k) {
+        const int t = first + k;
+        const int act = net.active[t], inact = act == 1 ? 2 : 1;
+        require(a.grad[k] == net.state[act][t], "fused update: gradient group is not the active buffer");
+        o.W[k] = net.state[0][t];
+        o.S[k] = net.state[3][t];
+        o.Ga[k] = net.state[act][t];
+        o.Gi[k] = net.state[inact][t];
+        o.WT[k] = net.wt[t];
+        o.NO[k] = net.neurons[t + 1];
+        o.NI[k] = net.neurons[t];
+    }
+    double bytes = 0;
+    for (int t = 0; t < a.transitions; ++t)
+        bytes += 4.0 * (a.begin[t + 1] - a.begin[t]) * (a.splits[t] + (a.accumulate ? 2 : 1) + 6);
+    if (a.cost_count) bytes += double(sizeof(CostStats)) * (a.cost_count + 2);
+    TraceScope trace(d, kTraceSplitReduce, bytes);
+    hipLaunchKernelGGL(reduce_rprop_kernel, a.block_begin[a.transitions] + (a.cost_count ? 1 : 0), 256, 0, d.stream, a,
+                       o);
     HIP_CHECK(hipGetLastError());
 }
 
@@ -1342,28 +1441,7 @@ void launch_fill(Device& d, float* p, size_t count, float value) {
 }
 
 // ------------------------------------------------------------------------------------------
-// Optimizers: one launch covers every transition.  Each transition's buffers
-// are separate allocations; the launch carries their pointers by value.
-struct OptimizerArgs {
-    float* W[kMaxTransitions];
-    float* S[kMaxTransitions];   // RPROP step / Adam first moment
-    float* Ga[kMaxTransitions];  // active gradient
-    float* Gi[kMaxTransitions];  // inactive gradient / Adam second moment
-    float* WT[kMaxTransitions];  // row-major copy of the weights, kept current by RPROP and Adam
-    int NO[kMaxTransitions], NI[kMaxTransitions];
-    int begin[kMaxTransitions + 1];
-    int block_begin[kMaxTransitions + 1];  // blocks of kOptimizerThreads entries, per transition
-    int transitions;
-};
-
-constexpr int kOptimizerThreads = 256;
-
-// Entry j = o + NO*i of a weight block into its row-major copy (bias column i = NI excluded).
-__device__ __forceinline__ void copy_transposed(const OptimizerArgs& a, int t, int j, float w) {
-    const int i = j / a.NO[t], o = j - i * a.NO[t];
-    if (i < a.NI[t]) a.WT[t][i + a.NI[t] * o] = w;
-}
-
+// Optimizer launches (OptimizerArgs and the RPROP update are defined with the reductions).
 // Entry j of transition t for this lane: each block lies within one
 // transition, so t and its pointers are uniform (scalar loads).
 __device__ __forceinline__ bool entry_of(const OptimizerArgs& a, int& t, int& j) {
@@ -1373,40 +1451,10 @@ __device__ __forceinline__ bool entry_of(const OptimizerArgs& a, int& t, int& j)
     return j < a.begin[t + 1] - a.begin[t];
 }
 
-// Resile_k (cuda/derivative_kernels_v4.cu:752-778), sign tests on float products.
-// The optimizers round every product and sum separately, as the reference's
-// CPU build does: no multiply-add contraction (hipcc contracts by default, and
-// __fmul_rn/__fadd_rn do not prevent it).
+// One lane per entry: the gradient already reduced into the active buffer.
 __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs a) {
-#pragma clang fp contract(off)
     int t, j;
-    if (entry_of(a, t, j)) {
-        float* W = a.W[t] + j;
-        float* step = a.S[t] + j;
-        float* ga = a.Ga[t] + j;
-        const float gi = a.Gi[t][j];
-        const float g = *ga;
-        const float prod = g * gi;
-        float s = *step;
-        if (prod > 0) s *= 1.2f;
-        const float w = *W;
-        const float nW = w - copysignf(s, g);
-        float kept = w;
-        if (prod < 0) {
-            kept = w + copysignf(s, gi);
-            s *= 0.5f;
-            *ga = 0.0f;
-        } else if (g != 0.0f) {
-            if (fabsf(nW) <= 20.0f) kept = nW;
-            else {
-                s = 0.1f;
-                *ga = 0.0f;
-            }
-        }
-        *W = kept;
-        *step = s;
-        copy_transposed(a, t, j, kept);
-    }
+    if (entry_of(a, t, j)) rprop_update(a, t, j, a.Ga[t][j]);
 }
 
 // ADAM_k (cuda/derivative_kernels_v4.cu:780-799); M in S, V in the inactive buffer.

@@ -69,6 +69,7 @@ SIGNATURES = {
     'cpde_inspect_gradients': (i32, [vp]),
     'cpde_epoch_matching': (i32, [vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32]),
     'cpde_epoch_matching_static': (i32, [vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32]),
+    'cpde_epoch_matching_rprop': (i32, [vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32]),
     'cpde_scalars_download': (i32, [vp, i32, vp, i32, vp]),
     'cpde_scalars_download_graph': (i32, [vp, i32, vp, i32, vp, vp, vp]),
     'cpde_rprop': (i32, [vp]),
@@ -329,6 +330,14 @@ class Plan:
         check(load().cpde_epoch_matching(self.handle, target.ptr, target_width, target_rows.ptr, weights.ptr,
                                          weight_samples, offset, valid, cost_index, int(collect), int(accumulate)))
 
+    def epoch_matching_rprop(self, target, target_width, target_rows, weights, weight_samples, offset, valid,
+                             cost_index, collect=True, accumulate=False):
+        """epoch_matching, then RPROP on the network, the update riding in the
+        gradient reduction's launch."""
+        check(load().cpde_epoch_matching_rprop(self.handle, target.ptr, target_width, target_rows.ptr, weights.ptr,
+                                               weight_samples, offset, valid, cost_index, int(collect),
+                                               int(accumulate)))
+
     def epoch_matching_static(self, target, target_width, target_rows, weights, weight_samples, offset, valid,
                               cost_index, collect=True, accumulate=False):
         """epoch_matching with the library's static scratch: no allocation."""
@@ -393,10 +402,11 @@ class MatchingRun:
         self._loaded = None
         device.costs_begin(1)
 
-    def step(self, collect=True):
+    def step(self, collect=True, update=False):
         """forward + cost + backward over every chunk (Server::pass).  As in
         Server::activate (cuda/cpde_server.cu:163) the input copy is skipped when
-        the loaded chunk is unchanged."""
+        the loaded chunk is unchanged.  `update`: then RPROP, riding in the last
+        chunk's gradient reduction (one-pass epochs) or launched after it."""
         self.device.costs_begin(1)
         first = True
         for offset in range(0, self.samples, self.width):
@@ -404,6 +414,11 @@ class MatchingRun:
             if self._loaded != (offset, valid):
                 self.plan.activate(self.data, self.samples, self.rows, offset, valid)
                 self._loaded = (offset, valid)
+            last = offset + self.width >= self.samples
+            if update and last and self.one_pass and not self.static_scratch:
+                self.plan.epoch_matching_rprop(self.target, self.samples, self.target_rows, self.weights, 1, offset,
+                                               valid, 0, collect, not first)
+                return
             if self.static_scratch:
                 self.plan.epoch_matching_static(self.target, self.samples, self.target_rows, self.weights, 1, offset,
                                                 valid, 0, collect, not first)
@@ -416,6 +431,8 @@ class MatchingRun:
                                    collect, True)
                 self.plan.backward(not first)
             first = False
+        if update:
+            self.net.rprop()
 
     def loss(self):
         c, _ = self.device.scalars(1, 0)

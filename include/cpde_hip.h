@@ -167,6 +167,15 @@ int cpde_cost_matching(cpde_plan* plan, const float* target, int target_width, c
 int cpde_epoch_matching(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
                         const float* weights, int weight_samples, int offset, int valid, int cost_index, int collect,
                         int accumulate);
+/* cpde_epoch_matching followed by cpde_rprop, with the split reduction of the
+ * weight gradients and the RPROP update in one launch (one launch fewer per
+ * epoch); the gradients, weights and optimizer state end bit-identical to the
+ * two calls.  No counterpart in the reference, whose training step launches
+ * them separately (cuda/cpde_server.cu:384-409); for callers that update after
+ * every epoch of a single matching cost (the last chunk of the epoch). */
+int cpde_epoch_matching_rprop(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
+                              const float* weights, int weight_samples, int offset, int valid, int cost_index,
+                              int collect, int accumulate);
 /* cpde_epoch_matching that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -242,3 +242,45 @@ def test_adam_from_reference_states(server):
             assert rel_l2(a['buffers'][3], b['buffers'][3]) < 1e-3      # m
             assert rel_l2(a['buffers'][2], b['buffers'][2]) < 2e-3      # v
             assert rel_l2(a['buffers'][1], b['buffers'][1]) < 1e-3      # the gradient
+
+
+def fourier_case(order, neurons, points, seed=9):
+    schema = W.full_schema(neurons[0], order)
+    rng = np.random.default_rng(seed)
+    pts = rng.uniform(0, 1, (points, neurons[0]))
+    freq, coef, phase = W.fourier_modes(neurons[0], 4, 3, seed)
+    target = W.fourier_target(pts, schema, freq, coef, phase)
+    return W.MatchingWorkload('fused', neurons, pts, schema, target, 1.0 / target.var(axis=1),
+                              W.xavier_weights(neurons, seed))
+
+
+@pytest.mark.parametrize('order, neurons, points, chunk, one_pass', [
+    (6, [2, 64, 48, 1], 61, 0, '1'),        # one chunk, one-pass epoch
+    (3, [2, 40, 40, 40, 1], 300, 128, '1'),  # three chunks: the update rides in the last one's reduction
+    (2, [3, 32, 24, 1], 90, 0, '0'),        # no one-pass epoch: separate launches, then RPROP
+])
+def test_epoch_with_fused_rprop_matches_separate_update(device, monkeypatch, order, neurons, points, chunk, one_pass):
+    """cpde_epoch_matching_rprop (the split reduction and RPROP in one launch)
+    leaves weights, steps, both gradient buffers and the row-major weight copy
+    bit-identical to cpde_epoch_matching followed by cpde_rprop, over five
+    epochs (growth, rollback and plain steps all occur)."""
+    monkeypatch.setenv('CPDE_ONE_PASS', one_pass)
+    print(f'[case] fused rprop order={order} neurons={neurons} points={points} chunk={chunk} one_pass={one_pass}',
+          flush=True)
+    wl = fourier_case(order, neurons, points)
+    runs = [hip.MatchingRun(device, wl, chunk=chunk or None) for _ in range(2)]
+    losses = [[], []]
+    for _ in range(5):
+        runs[0].step(update=False)
+        runs[0].net.rprop()
+        runs[1].step(update=True)
+        for k in range(2):
+            losses[k].append(runs[k].loss())
+    device.synchronize()
+    assert losses[0] == losses[1]
+    for t in range(len(neurons) - 1):
+        for b in range(4):
+            np.testing.assert_array_equal(runs[1].net.state(t, b), runs[0].net.state(t, b))
+        assert runs[0].net.active(t) == runs[1].net.active(t)
+    for r in runs:
+        r.close()
