@@ -699,7 +699,10 @@ __global__ __launch_bounds__(256) void reduce_rprop_kernel(ReduceArgs a, Optimiz
 // tiles do.  The bias (n-tile 0 only) is the sum of G over value-row columns.
 constexpr int kWdStride = 65;                  // LDS row stride of a 64x64 tile
 constexpr int kWdLds = 2 * 64 * kWdStride;     // two tiles; also the thin roles' 256 x 17 scratch
-constexpr int kWdDepth = 2;                    // column groups loaded ahead
+#ifndef CPDE_WD_DEPTH
+#define CPDE_WD_DEPTH 2
+#endif
+constexpr int kWdDepth = CPDE_WD_DEPTH;        // column groups loaded ahead
 
 // 4 consecutive entries [w0, w0 + 4) of row c of a [column][width] stack
 // (offset = c * width + w0).  MASK: zeros beyond the width -- VEC (width % 4
@@ -836,27 +839,25 @@ __device__ __forceinline__ void wgrad_direct_tile(const WgradArgs& a, int t, int
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[x][z][v] += T[(4 * (4 * q + v) + x) * kWdStride + 4 * j + z];
     };
+    // waves 2 and 3 put their tiles in the two LDS slots, waves 0 and 1 add
+    // them and put w0 + w2 and w1 + w3 back; every lane then adds the two
+    // sums of 16 entries, a wave writing one 64-entry row per instruction
     if (wave >= 2) store(lds + (wave - 2) * 64 * kWdStride);
     __syncthreads();
-    if (wave < 2) add(lds + wave * 64 * kWdStride);
+    if (wave < 2) {
+        add(lds + wave * 64 * kWdStride);
+        store(lds + wave * 64 * kWdStride);
+    }
     __syncthreads();
-    if (wave == 1) store(lds);
-    __syncthreads();
-    if (wave == 0) add(lds);
     float* P = a.partial[t] + size_t(split) * M * (N + 1);
-    if (wave == 0) {
-#pragma unroll
-        for (int x = 0; x < 4; ++x)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int m = m0 + 4 * (4 * q + v) + x;
-                if (m >= M) continue;
-#pragma unroll
-                for (int z = 0; z < 4; ++z) {
-                    const int n = yn + z;
-                    if (n < N) P[size_t(m) * (N + 1) + n] = acc[x][z][v];
-                }
-            }
+    if (n0 + lane < N) {
+#pragma unroll 4
+        for (int i = 0; i < 16; ++i) {
+            const int ml = wave + 4 * i;
+            if (m0 + ml < M)
+                P[size_t(m0 + ml) * (N + 1) + n0 + lane] =
+                    lds[ml * kWdStride + lane] + lds[(64 + ml) * kWdStride + lane];
+        }
     }
     // bias (n-tile 0): the sum of G over the split's value-row columns; lane
     // group (wave, q) takes value columns first + R (4 wave + q + 16 i) for its
@@ -879,7 +880,8 @@ __device__ __forceinline__ void wgrad_direct_tile(const WgradArgs& a, int t, int
         bias.y += __shfl_xor(bias.y, 32);
         bias.z += __shfl_xor(bias.z, 32);
         bias.w += __shfl_xor(bias.w, 32);
-        float* bias_lds = lds + 64 * kWdStride;  // wave 1's tile slot, free since the second barrier
+        float* bias_lds = lds + 64 * kWdStride;  // the second tile slot
+        __syncthreads();                          // every lane has read the slots
         if (q == 0) {
             bias_lds[wave * 64 + 4 * j + 0] = bias.x;
             bias_lds[wave * 64 + 4 * j + 1] = bias.y;
