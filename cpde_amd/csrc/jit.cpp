@@ -700,10 +700,13 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
        << "    __syncthreads();\n";
     for (int t = 1; t + 2 < L; ++t)
         ep << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
-    ep << "    net_output<" << neurons[L - 2] << ", " << NO << ">(a, " << L - 2 << ", X, p0, npts, O);\n"
+    const std::string last = std::to_string(neurons[L - 2]);
+    ep << "    float ua[R];  // the last hidden layer's u rows, in flight during the output layer and the cost\n"
+       << "    u_ahead<" << last << ", output_adjoint_split<" << last << ">()>(a, " << L - 2 << ", p0, npts, ua);\n"
+       << "    net_output<" << neurons[L - 2] << ", " << NO << ">(a, " << L - 2 << ", X, p0, npts, O);\n"
        << "    __syncthreads();  // the output values of the block's columns are in O\n"
        << cost << "    net_output_backward<" << neurons[L - 2] << ", " << NO << ", true>(a, " << L - 2
-       << ", X, p0, npts, O + kNNC * " << NO << ");\n";
+       << ", X, p0, npts, ua, O + kNNC * " << NO << ");\n";
     for (int t = L - 3; t >= 1; --t)
         ep << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
     ep << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
@@ -727,8 +730,13 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     for (int t = 1; t + 2 < L; ++t)
         fwd << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
     fwd << "    net_output<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2 << ", X, p0, npts);\n";
-    bwd << "    net_output_backward<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2
-        << ", X, p0, npts);\n";
+    {
+        const std::string last = std::to_string(neurons[L - 2]);
+        bwd << "    float ua[R];\n    u_ahead<" << last << ", output_adjoint_split<" << last << ">()>(a, " << L - 2
+            << ", p0, npts, ua);\n"
+            << "    net_output_backward<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2
+            << ", X, p0, npts, ua);\n";
+    }
     for (int t = L - 3; t >= 1; --t)
         bwd << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
     bwd << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
