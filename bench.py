@@ -59,9 +59,9 @@ CPU_SAMPLE_MACS = 3.0e9
 # read, 268,435,456 B / 262,144 KiB written.
 COPY_SCALE = (268435456 / (131084.475 * 1024), 268435456 / (262144 * 1024))
 TRAFFIC_KIB = {
-    'fourier_fit_order6': {'network_epoch': (24131.83, 140509.01), 'gemm_wgrad': (30982.37, 7740.57)},
-    'fourier_large_order6': {'network_backward': (5014165.6, 8780106.3), 'network_forward': (427992.19, 14688010.08),
-                             'gemm_wgrad': (7914105.67, 35085.07)},
+    'fourier_fit_order6': {'network_epoch': (21271.59, 134691.65), 'gemm_wgrad': (30998.85, 7740.46)},
+    'fourier_large_order6': {'network_backward': (4986304.06, 8850894.45), 'network_forward': (429759.76, 14688003.15),
+                             'gemm_wgrad': (7840131.41, 35119.54)},
 }
 
 
