@@ -229,6 +229,7 @@ struct NetArgsHost {
     float* partial_in;
     float* partial_out;
     float* WT[32];
+    float* partial_hidden[32];
 };
 
 // Tuning of the fused kernels for a schema of `rows` derivative rows over chunks
@@ -271,6 +272,19 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
     t.col_tile = env_int("CPDE_NET_COLTILE", t.col_tile);
     t.alias = env_int("CPDE_NET_ALIAS", t.alias);
     t.scaled = env_int("CPDE_SCALED", t.scaled) ? 1 : 0;
+    // Hidden weight-gradient partials from the network backward itself, on
+    // request (CPDE_INKERNEL_WGRAD=1; hidden widths that are multiples of 16).
+    // Measured on the Poisson graph epoch, whose 256-point one-row boundary
+    // leaf runs 256 one-point workgroups: 0.0951 ms per epoch against 0.0932
+    // with the separate weight-gradient launch (each workgroup writes a whole
+    // 64 x 65 partial for its rank-one contribution), 0.107 with both leaves
+    // in the kernel; so it is off by default.
+    {
+        bool widths16 = neurons.size() >= 4;
+        for (size_t l = 1; l + 2 < neurons.size(); ++l)
+            widths16 = widths16 && neurons[l] % 16 == 0 && neurons[l + 1] % 16 == 0;
+        t.inkernel_wgrad = widths16 && env_int("CPDE_INKERNEL_WGRAD", 0) == 1 ? 1 : 0;
+    }
     return t;
 }
 
@@ -287,6 +301,7 @@ static std::shared_ptr<FusedModule> load_fused(Device& d, const Tables& t, const
     m->net_points_per_block = tune.net_points_per_block;
     m->net_threads = tune.net_threads;
     m->scaled = tune.scaled != 0;
+    m->inkernel_wgrad = tune.inkernel_wgrad != 0;
     HIP_CHECK(hipModuleLoadData(&m->module, code.data()));
     HIP_CHECK(hipModuleGetFunction(&m->network_forward, m->module, "network_forward_k"));
     HIP_CHECK(hipModuleGetFunction(&m->network_backward, m->module, "network_backward_k"));
@@ -325,6 +340,11 @@ static NetArgsHost net_args(const Plan& p) {
     a.Z[0] = p.input;
     return a;
 }
+
+struct GradientPlan;
+struct PartialSpace;
+static GradientPlan network_gradients(Plan& p, int blocks, bool accumulate, const PartialSpace& space,
+                                      NetArgsHost& a);
 
 // Mode of the fused path: CPDE_FUSED=2 (default) network-fused, 1 layer-fused.
 static bool network_mode() { return env_int("CPDE_FUSED", 2) >= 2; }
@@ -409,8 +429,11 @@ constexpr int kWgradDirectMinColumns = 256;
 // The gradient plan of transitions [first, first + count), count at most
 // kMaxTransitions (one grouped launch and one reduction); external_splits is
 // indexed by the absolute transition.
+// external_splits[t] > 0: transition t's partials come from the network
+// kernels' workgroups (that many), split-minor, or split-major where
+// external_major[t].
 static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external_splits, int first, int count,
-                                   PartialSpace space = {}) {
+                                   PartialSpace space = {}, const unsigned char* external_major = nullptr) {
     Net& n = *p.net;
     Device& d = *n.dev;
     const int K = int(p.columns());
@@ -493,8 +516,9 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
         g.ra.splits[k] = s;
         g.ra.grad[k] = n.state[n.active[t]][t];
         g.ra.begin[k + 1] = g.ra.begin[k] + M * (N + 1);
-        g.ra.split_minor[k] = external_splits[t] ? 1 : 0;
-        g.ra.block_begin[k + 1] = g.ra.block_begin[k] + reduce_blocks(M * (N + 1), external_splits[t] != 0);
+        const bool minor = external_splits[t] && !(external_major && external_major[t]);
+        g.ra.split_minor[k] = minor ? 1 : 0;
+        g.ra.block_begin[k + 1] = g.ra.block_begin[k] + reduce_blocks(M * (N + 1), minor);
     }
     g.wa.transitions = w;
     float* base = space.base;
@@ -518,6 +542,28 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
         g.ra.partial[k] = base + g.offset[k];
         if (!external_splits[first + k]) g.wa.partial[w++] = base + g.offset[k];
     }
+    return g;
+}
+
+// The gradient plan of a network backward over `blocks` workgroups: the input
+// and output transitions' partials come from the workgroups (split-minor), and
+// so do the hidden transitions' (split-major) when the module computes them in
+// the kernel; the partial pointers go into `a`.
+static GradientPlan network_gradients(Plan& p, int blocks, bool accumulate, const PartialSpace& space,
+                                      NetArgsHost& a) {
+    const int L = p.net->layers;
+    int external[kMaxTransitions] = {};
+    unsigned char major[kMaxTransitions] = {};
+    external[0] = external[L - 2] = blocks;
+    if (p.fused->inkernel_wgrad)
+        for (int t = 1; t + 2 < L; ++t) {
+            external[t] = blocks;
+            major[t] = 1;
+        }
+    GradientPlan g = plan_gradients(p, accumulate, external, 0, L - 1, space, major);
+    a.partial_in = const_cast<float*>(g.ra.partial[0]);
+    a.partial_out = const_cast<float*>(g.ra.partial[L - 2]);
+    for (int t = 1; t + 2 < L; ++t) a.partial_hidden[t] = const_cast<float*>(g.ra.partial[t]);
     return g;
 }
 
@@ -595,12 +641,8 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostS
     int width = p.width;
     const double cols = double(p.columns());
     const int blocks = epoch_blocks(p);
-    int external[kMaxTransitions] = {};
-    external[0] = external[L - 2] = blocks;
-    GradientPlan g = plan_gradients(p, accumulate, external, 0, L - 1, space);
     NetArgsHost a = net_args(p);
-    a.partial_in = const_cast<float*>(g.ra.partial[0]);
-    a.partial_out = const_cast<float*>(g.ra.partial[L - 2]);
+    GradientPlan g = network_gradients(p, blocks, accumulate, space, a);
     if (!n.wt_current) {
         // the backward half reads the row-major weight copies of every hidden
         // transition, which no workgroup of the same launch may still be
@@ -681,12 +723,8 @@ static void fused_backward(Plan& p, bool accumulate) {
     const double cols = double(p.columns());
     if (p.network) {
         const int blocks = (width + fm.net_points_per_block - 1) / fm.net_points_per_block;
-        int external[kMaxTransitions] = {};
-        external[0] = external[L - 2] = blocks;
-        const GradientPlan g = plan_gradients(p, accumulate, external, 0, L - 1);
         NetArgsHost a = net_args(p);
-        a.partial_in = const_cast<float*>(g.ra.partial[0]);
-        a.partial_out = const_cast<float*>(g.ra.partial[L - 2]);
+        const GradientPlan g = network_gradients(p, blocks, accumulate, PartialSpace{}, a);
         void* args[] = {&a, &width};
         double flops = 0;
         for (int t = 1; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;

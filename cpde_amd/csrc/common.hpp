@@ -225,6 +225,7 @@ struct FusedModule {
     hipFunction_t network_forward = nullptr, network_backward = nullptr, network_epoch = nullptr;
     int points_per_block = 2, net_points_per_block = 1, net_threads = 256;
     bool scaled = false;  // sigmoid stacks of the network kernels hold row alpha / alpha! (dE/dz: times alpha!)
+    bool inkernel_wgrad = false;  // the network backward writes every hidden transition's per-block partial
     ~FusedModule();
 };
 std::string compose_source(const Tables& t, const std::vector<int>& splits, bool scaled = false);
@@ -239,6 +240,7 @@ struct FusedTuning {
     int forward_blocks = 2, backward_blocks = 2;  // blocks per CU the register budget must allow
     int col_tile = 0;              // column tile of the network products: 16, 32, or 0 (chosen per shape)
     int scaled = 1;                // network kernels keep Taylor-scaled sigmoid stacks (row alpha / alpha!)
+    int inkernel_wgrad = 0;        // network backward kernels write hidden weight-gradient partials themselves
 };
 // Whether the schema is closed under swapping variables 0 and 1 (the scaled
 // forward composition then splits over two lanes, one per mirror image).

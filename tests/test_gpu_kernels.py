@@ -185,6 +185,39 @@ def test_weight_gradient_tile_forms(device, monkeypatch, order, neurons, points)
         assert rel_l2(a, b) < 1e-5
 
 
+@pytest.mark.parametrize('order,neurons,points,one_pass', [
+    (6, [2, 64, 48, 32, 1], 61, '1'),     # one-pass epoch, scaled rows on three hidden layers
+    (2, [2, 64, 64, 64, 1], 300, '1'),    # several points per workgroup
+    (3, [2, 80, 96, 1], 97, '0'),         # separate forward and backward launches
+    (0, [2, 64, 64, 64, 1], 256, '1'),    # the Poisson boundary leaf's shape: one row, one point per workgroup
+])
+def test_weight_gradient_inside_the_backward(device, monkeypatch, order, neurons, points, one_pass):
+    """Hidden transitions' weight-gradient partials written by the network
+    backward itself (CPDE_INKERNEL_WGRAD=1) against the separate
+    weight-gradient launch (=0): the same loss bit for bit, gradients within
+    fp32 summation-order noise, and both against the oracle."""
+    print(f'[case] in-kernel wgrad order={order} neurons={neurons} points={points} one_pass={one_pass}', flush=True)
+    monkeypatch.setenv('CPDE_ONE_PASS', one_pass)
+    wl = small_workload(order, neurons, points)
+    ref_loss, ref_grads = oracle_epoch(order, tuple(neurons), points, 0)
+    got, losses = {}, {}
+    for form in ('1', '0'):
+        monkeypatch.setenv('CPDE_INKERNEL_WGRAD', form)
+        run = hip.MatchingRun(device, wl)
+        run.step()
+        device.synchronize()
+        got[form], losses[form] = run.gradients(), run.loss()
+        run.close()
+        assert abs(losses[form] / ref_loss - 1) < 1e-4
+        for t, (g, r) in enumerate(zip(got[form], ref_grads)):
+            e = rel_l2(g, r)
+            print(f'[result] in-kernel {form} transition {t} gradient rel-L2 {e:.3e}', flush=True)
+            assert e < 1e-3
+    assert losses['1'] == losses['0']
+    for a, b in zip(got['1'], got['0']):
+        assert rel_l2(a, b) < 1e-5
+
+
 PAIRED_ALIASED = dict(CPDE_FUSED='2', CPDE_NET_POINTS='2', CPDE_NET_ALIAS='1', CPDE_NET_COLTILE='16',
                       CPDE_NET_SPLIT='1', CPDE_NET_SPLIT_ADJOINT='1')
 
