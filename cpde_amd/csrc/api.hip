@@ -283,7 +283,12 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
         bool widths16 = neurons.size() >= 4;
         for (size_t l = 1; l + 2 < neurons.size(); ++l)
             widths16 = widths16 && neurons[l] % 16 == 0 && neurons[l + 1] % 16 == 0;
-        t.inkernel_wgrad = widths16 && env_int("CPDE_INKERNEL_WGRAD", 0) == 1 ? 1 : 0;
+        // 2: only where the partials stay small (blocks x hidden weights <= 2^20 floats)
+        int hidden = 0;
+        for (size_t l = 1; l + 2 < neurons.size(); ++l) hidden += neurons[l + 1] * (neurons[l] + 1);
+        const long blocks = width > 0 ? (width + t.net_points_per_block - 1) / t.net_points_per_block : 1L << 30;
+        const int mode = env_int("CPDE_INKERNEL_WGRAD", 0);
+        t.inkernel_wgrad = widths16 && (mode == 1 || (mode == 2 && blocks * hidden <= (1L << 20))) ? 1 : 0;
     }
     return t;
 }
