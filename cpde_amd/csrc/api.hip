@@ -13,6 +13,7 @@
 struct cpde_device_s : cpde::Device {};
 struct cpde_net_s : cpde::Net {};
 struct cpde_plan_s : cpde::Plan {};
+struct cpde_stacks_s : cpde::Stacks {};
 struct cpde_program_s : cpde::Program {};
 
 namespace cpde {
@@ -120,6 +121,7 @@ static void reserve_arena(Net& net, const Plan& p) {
     for (int l = 0; l < net.layers; ++l)
         if (p.columns() * net.neurons[l] > net.capacity[l]) grow = true;
     if (!grow) return;
+    require(!net.bound, "a stack set is bound to this network: unbind it before using another plan");
     HIP_CHECK(hipStreamSynchronize(net.dev->stream));
     for (int l = 0; l < net.layers; ++l) {
         const size_t need = std::max(net.capacity[l], p.columns() * net.neurons[l]);
@@ -134,6 +136,16 @@ static void reserve_arena(Net& net, const Plan& p) {
         net.capacity[l] = need;
     }
     ++net.generation;
+}
+
+// Swap the network's arena and the plan's input with the stack set's.
+static void swap_binding(Net& n, Plan& p, Stacks& s) {
+    std::swap(n.z, s.z);
+    std::swap(n.y, s.y);
+    std::swap(n.g, s.g);
+    std::swap(n.capacity, s.capacity);
+    std::swap(p.input, s.input);
+    ++n.generation;
 }
 
 template <class F>
@@ -912,6 +924,10 @@ int cpde_net_create(cpde_device* dev, int layers, const int* neurons, const int*
 int cpde_net_destroy(cpde_net* net) {
     return guarded([&] {
         if (!net) return;
+        if (net->bound) {  // the arena's buffers go back to the network before it frees them
+            swap_binding(*net, *net->bound->plan, *net->bound);
+            net->bound = nullptr;
+        }
         (void)hipStreamSynchronize(net->dev->stream);
         for (auto& s : net->state)
             for (float* p : s) (void)hipFree(p);
@@ -989,12 +1005,79 @@ int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, i
 int cpde_plan_destroy(cpde_plan* plan) {
     return guarded([&] {
         if (!plan) return;
+        Net& n = *plan->net;
+        if (n.bound && n.bound->plan == plan) {
+            swap_binding(n, *plan, *n.bound);
+            n.bound = nullptr;
+        }
         (void)hipStreamSynchronize(plan->net->dev->stream);
         (void)hipFree(plan->dev_tables);
         (void)hipFree(plan->dev_rows);
         (void)hipFree(plan->epoch_partials);
         (void)hipFree(plan->input);
         delete plan;
+    });
+}
+
+int cpde_stacks_create(cpde_plan* plan, cpde_stacks** out) {
+    return guarded([&] {
+        require(plan && out, "null argument");
+        Net& n = *plan->net;
+        auto s = std::make_unique<cpde_stacks>();
+        s->plan = plan;
+        s->z.assign(n.layers, nullptr);
+        s->y.assign(n.layers, nullptr);
+        s->g.assign(n.layers, nullptr);
+        s->capacity.assign(n.layers, 0);
+        try {
+            for (int l = 0; l < n.layers; ++l) {
+                const size_t need = plan->columns() * n.neurons[l];
+                HIP_CHECK(hipMalloc(&s->z[l], need * sizeof(float)));
+                if (!n.linear[l]) HIP_CHECK(hipMalloc(&s->y[l], need * sizeof(float)));
+                if (l > 0) HIP_CHECK(hipMalloc(&s->g[l], need * sizeof(float)));
+                s->capacity[l] = need;
+            }
+            HIP_CHECK(hipMalloc(&s->input, plan->columns() * n.neurons[0] * sizeof(float)));
+        } catch (...) {
+            for (auto* v : {&s->z, &s->y, &s->g})
+                for (float* q : *v) (void)hipFree(q);
+            (void)hipFree(s->input);
+            throw;
+        }
+        *out = s.release();
+    });
+}
+
+int cpde_plan_bind(cpde_plan* plan, cpde_stacks* stacks) {
+    return guarded([&] {
+        require(plan, "null argument");
+        Net& n = *plan->net;
+        if (n.bound) {  // unbind whatever is bound: the set goes back to its own pointers
+            Stacks& b = *n.bound;
+            swap_binding(n, *b.plan, b);
+            n.bound = nullptr;
+        }
+        if (stacks) {
+            require(stacks->plan == plan, "the stack set belongs to another plan");
+            swap_binding(n, *plan, *stacks);
+            n.bound = stacks;
+        }
+    });
+}
+
+int cpde_stacks_destroy(cpde_stacks* stacks) {
+    return guarded([&] {
+        if (!stacks) return;
+        Net& n = *stacks->plan->net;
+        if (n.bound == stacks) {
+            swap_binding(n, *stacks->plan, *stacks);
+            n.bound = nullptr;
+        }
+        (void)hipStreamSynchronize(n.dev->stream);
+        for (auto* v : {&stacks->z, &stacks->y, &stacks->g})
+            for (float* q : *v) (void)hipFree(q);
+        (void)hipFree(stacks->input);
+        delete stacks;
     });
 }
 
@@ -1383,6 +1466,14 @@ int cpde_epoch_expression(cpde_plan* plan, cpde_program* program, const double* 
         CostStats* records = epoch_records(*plan);
         ExpressionArgsHost e{fields, quadrature_weights, multiplier, records, samples, offset, valid, collect != 0};
         one_pass_epoch(*plan, kernel, &e, records, cost_index, accumulate != 0);
+    });
+}
+
+int cpde_epoch_expression_fused(cpde_plan* plan, cpde_program* program, int* fused) {
+    return guarded([&] {
+        require(plan && program && fused, "null argument");
+        *fused = plan->backward && one_pass_fits(*plan) &&
+                 program->source.find("cpde_expression_point") != std::string::npos;
     });
 }
 

@@ -93,7 +93,21 @@ struct Net {
     // split-K partial buffer for the weight-gradient contraction
     float* partials = nullptr;
     size_t partial_capacity = 0;
+    // a plan's own stack set bound in place of the arena (cpde_plan_bind); while
+    // bound, the set holds the arena's pointers and the plan's own input
+    struct Stacks* bound = nullptr;
     int param_count(int t) const { return neurons[t + 1] * (neurons[t] + 1); }
+};
+
+// A plan's own set of layer stacks and input chunk, for forward results kept
+// until a later backward (retention): bound, it stands in for the network's
+// arena and the plan's input.
+struct Plan;
+struct Stacks {
+    Plan* plan = nullptr;
+    std::vector<float*> z, y, g;
+    std::vector<size_t> capacity;
+    float* input = nullptr;
 };
 
 struct Plan {

@@ -221,8 +221,22 @@ struct NetRecord {
         }
     };
     std::map<cpde_plan*, Input> inputs;
+    // retained forward results: per cost, one stack set per chunk of its plan
+    struct Retained {
+        cpde_plan* plan = nullptr;
+        std::vector<cpde_stacks*> sets;
+    };
+    std::map<uint64_t, Retained> retained;
+    void drop_retained(uint64_t cost) {
+        auto it = retained.find(cost);
+        if (it == retained.end()) return;
+        for (cpde_stacks* s : it->second.sets) cpde_stacks_destroy(s);
+        retained.erase(it);
+    }
     int transitions() const { return int(neurons.size()) - 1; }
     ~NetRecord() {
+        for (auto& kv : retained)
+            for (cpde_stacks* s : kv.second.sets) cpde_stacks_destroy(s);
         for (auto& kv : plans) cpde_plan_destroy(kv.second);
         if (net) cpde_net_destroy(net);
     }
@@ -568,6 +582,10 @@ private:
     // With CPDE_TRACE_FILE set, every launch of the session is timed per kernel
     // class and the totals are written there as JSON when the server ends.
     std::string trace_file_;
+    static double retain_budget_mb() {
+        const char* v = std::getenv("CPDE_RETAIN_MB");
+        return v && *v ? std::max(0.0, std::atof(v)) : 16384.0;
+    }
     void open_device() {
         if (dev_) return;
         call(cpde_device_open(ordinal_, &dev_));
@@ -660,7 +678,14 @@ private:
         const double* multiplier;
         int begin, end;
         bool reuse_forward;
+        // 1: each chunk's forward goes into the cost's retained stack set for
+        // that chunk; 2: the cost and backward run on the retained forward
+        // (`id` names the cost)
+        int retain = 0;
+        uint64_t id = 0;
     };
+    bool retention_fits(NetRecord& n, CostRecord& c, double& budget);
+    void bind_retained(NetRecord& n, uint64_t id, cpde_plan* plan, int chunk);
     void pass(NetRecord& n, CostRecord& c, int slot, bool& first, const Pass& how);
     void prepare_costs(NetRecord& n, const std::vector<uint64_t>& ids, uint64_t ni);
     void graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord& graph, bool backward);
@@ -709,7 +734,13 @@ void Server::pass(NetRecord& n, CostRecord& c, int slot, bool& first, const Pass
     cpde_plan* plan = plan_for(n, c.schema, c.width, true);
     for (int offset = how.begin; offset < end; offset += c.width) {
         const int valid = std::min(c.width, input.samples - offset);
-        if (how.reuse_forward) {
+        if (how.retain) {
+            bind_retained(n, how.id, plan, offset / c.width);
+            if (how.retain == 1) {  // this chunk's forward, kept in its own stack set
+                call(cpde_activate(plan, input.values.as<float>(), input.samples, c.rows.data(), offset, valid));
+                if (c.has_components) call(cpde_forward(plan));
+            }
+        } else if (how.reuse_forward) {
             DataRecord& d = data(c.input);
             const NetRecord::Loaded want{plan, c.input, d.version, cpde_net_generation(n.net), offset, valid, c.rows};
             require(n.loaded == want, "forward context is no longer current");
@@ -752,7 +783,59 @@ void Server::pass(NetRecord& n, CostRecord& c, int slot, bool& first, const Pass
             call(cpde_backward(plan, first ? 0 : 1));
             first = false;
         }
+        if (how.retain) call(cpde_plan_bind(plan, nullptr));
     }
+}
+
+// Retention of forward results (the reference's plan, IMPLEMENTATION_PLAN.md:750-831;
+// its engine recomputes instead, cuda/cpde_server.cu:273-318): a cost whose
+// multiplier depends on the graph's values keeps every chunk's forward in a
+// stack set of its own between the value pass and the backward, while the sets
+// of all such costs fit CPDE_RETAIN_MB (default 16384; 0: recompute, as the
+// reference does).  `budget` is what is left of it.  An expression cost whose
+// backward runs as one launch with the forward inside it keeps its forwards
+// only when a chunk's forward is large (2^28 multiply-adds and up): below that
+// the separate cost and backward launches cost more than the recomputation.
+// Measured per epoch of a two-leaf graph whose value-dependent leaf has one
+// row: 2->128^3->1 on 2048-point chunks (6.8e7 multiply-adds) 0.478 ms kept,
+// 0.455 recomputed; 2->256^3->1 on 4096-point chunks (5.4e8) 0.574 kept,
+// 0.597 recomputed; 2->512^3->1 (no one-launch backward) 5.64 kept, 6.68
+// recomputed.
+bool Server::retention_fits(NetRecord& n, CostRecord& c, double& budget) {
+    if (!c.input || !c.has_gradient || !c.has_components) return false;
+    const int samples = data(c.input).samples;
+    const double chunks = std::ceil(double(samples) / c.width);
+    double floats = 0;
+    const double columns = double(c.width) * c.schema.rows;
+    if (c.kind == 2) {
+        int fused = 0;
+        call(cpde_epoch_expression_fused(plan_for(n, c.schema, c.width, true), c.program, &fused));
+        double macs = 0;
+        for (size_t l = 0; l + 1 < n.neurons.size(); ++l) macs += double(n.neurons[l]) * n.neurons[l + 1];
+        if (fused && macs * columns < std::ldexp(1.0, 28)) return false;
+    }
+    for (size_t l = 0; l < n.neurons.size(); ++l)
+        floats += columns * n.neurons[l] * (1 + (n.linear[l] ? 0 : 1) + (l > 0 ? 1 : 0));
+    floats += columns * n.neurons[0];  // the chunk's input
+    const double bytes = chunks * floats * sizeof(float);
+    if (bytes > budget) return false;
+    budget -= bytes;
+    return true;
+}
+
+void Server::bind_retained(NetRecord& n, uint64_t id, cpde_plan* plan, int chunk) {
+    auto& r = n.retained[id];
+    if (r.plan != plan) {  // a new plan for this cost (chunk width or schema changed)
+        for (cpde_stacks* set : r.sets) cpde_stacks_destroy(set);
+        r.sets.clear();
+        r.plan = plan;
+    }
+    while (int(r.sets.size()) <= chunk) {
+        cpde_stacks* set = nullptr;
+        call(cpde_stacks_create(plan, &set));
+        r.sets.push_back(set);
+    }
+    call(cpde_plan_bind(plan, r.sets[chunk]));
 }
 
 // Server::prepare_costs (cuda/cpde_server.cu:258-272): costs belong to this net,
@@ -816,6 +899,7 @@ void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
     bool first = true;
     int reuse = -1, last_offset = 0;
     double best_work = -1;
+    std::vector<char> keep(ids.size(), 0);  // leaves whose forwards are retained until their backward
     if (backward) {
         // The reference zeroes the gradient here (cuda/cpde_server.cu:278).  The
         // first backward pass overwrites all of it (accumulate 0), so the zero
@@ -827,10 +911,14 @@ void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
             written = runs && c.input && c.has_gradient && data(c.input).samples > 0;
         }
         if (!written) call(cpde_zero_gradient(n.net));
-        // run the most expensive leaf with an unknown multiplier last so its
-        // final forward can be reused by its backward (a work estimate)
+        double budget = retain_budget_mb() * 1048576.0;
+        for (size_t i = 0; i < ids.size(); ++i)
+            if (!graph.schedule[i].known && retention_fits(n, cost(ids[i]), budget)) keep[i] = 1;
+        // run the most expensive leaf with an unknown multiplier and no
+        // retained forwards last, so its final forward can be reused by its
+        // backward (a work estimate)
         for (size_t i = 0; i < ids.size(); ++i) {
-            if (graph.schedule[i].known) continue;
+            if (graph.schedule[i].known || keep[i]) continue;
             CostRecord& c = cost(ids[i]);
             if (!c.input || !c.has_gradient || !c.has_components) continue;
             double derivative_work = 0, work = 0;
@@ -851,7 +939,8 @@ void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
     for (size_t i = 0; i < ids.size(); ++i) {
         if (int(i) == reuse) continue;
         const bool immediate = backward && graph.schedule[i].known && graph.schedule[i].value != 0;
-        pass(n, cost(ids[i]), int(i), first, Pass{immediate, true, immediate ? fixed + i : nullptr, 0, INT_MAX, false});
+        pass(n, cost(ids[i]), int(i), first,
+             Pass{immediate, true, immediate ? fixed + i : nullptr, 0, INT_MAX, false, keep[i] ? 1 : 0, ids[i]});
     }
     if (reuse >= 0) {
         CostRecord& c = cost(ids[reuse]);
@@ -869,7 +958,8 @@ void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
         for (size_t i = 0; i < ids.size(); ++i)
             if (!graph.schedule[i].known)
                 pass(n, cost(ids[i]), int(i), first,
-                     Pass{true, false, multipliers + i, 0, int(i) == reuse ? last_offset : INT_MAX, false});
+                     Pass{true, false, multipliers + i, 0, int(i) == reuse ? last_offset : INT_MAX, false,
+                          keep[i] ? 2 : 0, ids[i]});
     }
 }
 
@@ -1432,8 +1522,14 @@ void Server::command(uint32_t op, Frame& b, std::atomic<bool>& stop) {
         } else if (kind == 1) {
             for (auto& kv : costs_) require(kv.second->net != id, "network is retained by a cost; close that cost first");
             nets_.erase(id);
-        } else if (kind == 2)
+        } else if (kind == 2) {
+            auto it = costs_.find(id);
+            if (it != costs_.end()) {
+                auto nt = nets_.find(it->second->net);
+                if (nt != nets_.end()) nt->second->drop_retained(id);
+            }
             costs_.erase(id);
+        }
         else
             require(false, "invalid object kind");
     } else if (op == 12) {

@@ -58,6 +58,9 @@ SIGNATURES = {
     'cpde_plan_destroy': (i32, [vp]),
     'cpde_plan_stack': (i32, [vp, i32, i32, ctypes.POINTER(vp)]),
     'cpde_plan_stack_scale': (i32, [vp, i32, i32, vp]),
+    'cpde_stacks_create': (i32, [vp, ctypes.POINTER(vp)]),
+    'cpde_plan_bind': (i32, [vp, vp]),
+    'cpde_stacks_destroy': (i32, [vp]),
     'cpde_activate': (i32, [vp, vp, i32, vp, i32, i32]),
     'cpde_forward': (i32, [vp]),
     'cpde_output': (i32, [vp, vp, i32, vp, i32, i32]),
@@ -82,6 +85,7 @@ SIGNATURES = {
     'cpde_program_destroy': (i32, [vp]),
     'cpde_cost_expression': (i32, [vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, i32]),
     'cpde_epoch_expression': (i32, [vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, i32]),
+    'cpde_epoch_expression_fused': (i32, [vp, vp, vp]),
     'cpde_graph_execute': (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, i32]),
     'cpde_jit_prepare': (i32, [i32, i32, vp, i32, vp, i32, i32, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     'cpde_trace_enable': (i32, [vp, i32]),

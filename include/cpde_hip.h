@@ -41,6 +41,7 @@ typedef struct cpde_device_s cpde_device;
 typedef struct cpde_net_s cpde_net;
 typedef struct cpde_plan_s cpde_plan;
 typedef struct cpde_program_s cpde_program;
+typedef struct cpde_stacks_s cpde_stacks;
 
 /* Per-cost reduction result: signed double sum and the first bad (sample,
  * component); component -1 means the objective itself
@@ -136,6 +137,20 @@ int cpde_plan_stack(cpde_plan* plan, int layer, int kind, float** device_ptr);
  * stacks).  No counterpart in the reference, whose stacks are unscaled; for
  * callers that inspect stacks. */
 int cpde_plan_stack_scale(cpde_plan* plan, int layer, int kind, float* row_factor);
+/* Retained forward results.  A stack set is a plan's own copy of every layer's
+ * stacks and of its activated input chunk; cpde_plan_bind(plan, set) makes the
+ * plan's launches (activate, forward, costs, backward) use the set in place of
+ * the network's shared arena until cpde_plan_bind(plan, NULL) or another bind.
+ * A forward into a bound set stays there while other chunks and plans run, so a
+ * later backward needs no second forward: the retention the reference plans
+ * for costs with value-dependent multipliers (IMPLEMENTATION_PLAN.md:750-831,
+ * not implemented in its engine, which recomputes those forwards and keeps
+ * only the last chunk's, cuda/cpde_server.cu:273-318).  While a set is bound,
+ * other plans of the network must not run.  Destroying a bound set, its plan or
+ * its network unbinds it first. */
+int cpde_stacks_create(cpde_plan* plan, cpde_stacks** out);
+int cpde_plan_bind(cpde_plan* plan, cpde_stacks* stacks);
+int cpde_stacks_destroy(cpde_stacks* stacks);
 
 /* ---- hot path ---------------------------------------------------------------------- */
 /* Server::activate (cuda/cpde_server.cu:158-170): copy the chunk's rows of wire
@@ -260,6 +275,11 @@ int cpde_cost_expression(cpde_plan* plan, cpde_program* program, const double* f
 int cpde_epoch_expression(cpde_plan* plan, cpde_program* program, const double* fields,
                           const double* quadrature_weights, int samples, int offset, int valid,
                           const double* multiplier, void* scratch, int cost_index, int collect, int accumulate);
+/* Whether cpde_epoch_expression runs (plan, program) as one launch (1) or as
+ * its three separate steps (0).  No counterpart in the reference: the server
+ * asks it when it chooses between keeping a chunk's forward for a later
+ * backward and recomputing it inside that launch. */
+int cpde_epoch_expression_fused(cpde_plan* plan, cpde_program* program, int* fused);
 /* cost_graph::execute (cuda/cost_graph.cuh:6-27) on one lane: reads cost slots,
  * writes values/adjoints/multipliers/active (device) and the summary (device;
  * NULL: the device's own summary slot, see cpde_scalars_download_graph). */

@@ -127,3 +127,52 @@ def test_poisson_at_full_size(server):
     assert ours[0] == ref[0]
     for a, b in zip(ours[1], ref[1]):
         assert rel_l2(a['buffers'][0], b['buffers'][0]) < 1e-5
+
+
+def run_nested(env, trace=None):
+    """Value, gradients and a two-epoch RPROP state of the nested-variation
+    graph (three chunks per leaf) in a fresh server with `env`; the server's
+    per-kernel launch counts when `trace` names a file."""
+    import json
+    import os
+    extra = dict(env)
+    if trace:
+        extra['CPDE_TRACE_FILE'] = str(trace)
+    s = wire.Session(SERVER, env=dict(os.environ, **extra))
+    try:
+        vw = W.VariationWorkload()
+        n, d, costs = vw.upload(s)
+        value, grads = s.graph_eval(n, [costs['a'], costs['correction']], vw.nested_graph(), gradient=True)
+        s.train(n, [costs['a'], costs['correction']], 2, method=0, fresh=1, log=1, graph=vw.nested_graph())
+        state = s.snapshot(n)
+    finally:
+        s.close()
+    launches = json.loads(trace.read_text()) if trace else None
+    return value, grads, state, launches
+
+
+def test_retained_forwards_match_recomputed(tmp_path):
+    """Leaves with value-dependent multipliers keep every chunk's forward in a
+    stack set of its own until their backward, instead of recomputing it as
+    the reference does (CPDE_RETAIN_MB=0), unless their backward runs as one
+    launch with a small forward inside it.  With the one-launch epochs off
+    (CPDE_ONE_PASS=0) this graph's leaves keep their forwards: fewer forward
+    launches, the same value, and the gradient to rounding (the recomputing
+    run sums the chunks' backwards in another order: it starts with the last
+    chunk of its costliest leaf, whose forward is still in place).  With them
+    on, both runs recompute."""
+    for serial in ({'CPDE_ONE_PASS': '0'}, {}):
+        kept = run_nested(serial, tmp_path / 'kept.json')
+        again = run_nested(dict(serial, CPDE_RETAIN_MB='0'), tmp_path / 'again.json')
+        assert kept[0] == again[0]
+        for a, b in zip(kept[1], again[1]):
+            assert rel_l2(a, b) < 1e-6
+        ours, theirs = wire.decode_state(kept[2]), wire.decode_state(again[2])
+        assert ours[0] == theirs[0]
+        for a, b in zip(ours[1], theirs[1]):
+            assert rel_l2(a['buffers'][0], b['buffers'][0]) < 1e-6
+        forwards = [sum(v[0] for k, v in r[3].items() if k in ('network_forward', 'fused_forward', 'gemm_forward'))
+                    for r in (kept, again)]
+        print(f'[result] {serial} forward launches retained {forwards[0]} recomputed {forwards[1]}', flush=True)
+        if serial:
+            assert forwards[0] < forwards[1]
