@@ -15,6 +15,17 @@ struct cpde_net_s : cpde::Net {};
 struct cpde_plan_s : cpde::Plan {};
 struct cpde_stacks_s : cpde::Stacks {};
 struct cpde_program_s : cpde::Program {};
+struct cpde_replay_s {
+    cpde::Device* dev = nullptr;
+    hipGraphExec_t exec = nullptr;
+    uint64_t layout = 0;
+    struct NetState {
+        cpde::Net* net;
+        std::vector<int> before, after;  // active gradient buffers when recorded, and after the recording
+        uint64_t generation;
+    };
+    std::vector<NetState> nets;
+};
 
 namespace cpde {
 
@@ -39,6 +50,13 @@ void check_hip(hipError_t status, const char* what, const char* file, int line) 
     throw device_error(buf);
 }
 
+void sync_stream(Device& d) {
+    if (d.capturing)
+        throw invalid("this call synchronises the device (it allocates, frees or reads back), which a capture "
+                      "cannot record: run it once before cpde_capture_begin");
+    HIP_CHECK(hipStreamSynchronize(d.stream));
+}
+
 TraceScope::TraceScope(Device& dev, int kind, double work) : d(dev) {
     if (!d.tracing) return;
     if (d.event_pool.size() < 2 * d.pending.size() + 2) {
@@ -60,7 +78,7 @@ TraceScope::~TraceScope() {
 
 void Device::fold_trace() {
     if (pending.empty()) return;
-    HIP_CHECK(hipStreamSynchronize(stream));
+    sync_stream(*this);
     for (const auto& r : pending) {
         float ms = 0;
         HIP_CHECK(hipEventElapsedTime(&ms, r.start, r.stop));
@@ -83,7 +101,7 @@ void Device::reserve_scalars(int costs, int layers) {
     costs = std::max(costs, cost_capacity);
     layers = std::max(layers, grad_capacity);
     if (costs == cost_capacity && layers == grad_capacity && scalar_block) return;
-    HIP_CHECK(hipStreamSynchronize(stream));
+    sync_stream(*this);
     const size_t cost_bytes = (sizeof(CostStats) * size_t(costs) + 255) / 256 * 256;
     const size_t grad_bytes = (sizeof(GradStats) * size_t(layers) + 255) / 256 * 256;
     const size_t bytes = cost_bytes + grad_bytes + sizeof(cpde_graph_summary);
@@ -99,7 +117,10 @@ void Device::reserve_scalars(int costs, int layers) {
     if (graph_summary)
         HIP_CHECK(hipMemcpy(summary, graph_summary, sizeof(cpde_graph_summary), hipMemcpyDeviceToDevice));
     else HIP_CHECK(hipMemcpy(summary, &none, sizeof(cpde_graph_summary), hipMemcpyHostToDevice));
-    if (scalar_block) HIP_CHECK(hipFree(scalar_block));
+    if (scalar_block) {
+        ++layout;
+        HIP_CHECK(hipFree(scalar_block));
+    }
     if (host_block) HIP_CHECK(hipHostFree(host_block));
     scalar_block = block;
     host_block = host;
@@ -122,7 +143,8 @@ static void reserve_arena(Net& net, const Plan& p) {
         if (p.columns() * net.neurons[l] > net.capacity[l]) grow = true;
     if (!grow) return;
     require(!net.bound, "a stack set is bound to this network: unbind it before using another plan");
-    HIP_CHECK(hipStreamSynchronize(net.dev->stream));
+    sync_stream(*net.dev);
+    ++net.dev->layout;
     for (int l = 0; l < net.layers; ++l) {
         const size_t need = std::max(net.capacity[l], p.columns() * net.neurons[l]);
         if (need == net.capacity[l]) continue;
@@ -191,7 +213,7 @@ static const float* activations(const Plan& p, int l) {
 static const int* plan_rows(Plan& p, const int* rows) {
     std::vector<int> map(rows, rows + p.rows);
     if (map != p.host_rows) {
-        HIP_CHECK(hipStreamSynchronize(p.net->dev->stream));
+        sync_stream(*p.net->dev);
         HIP_CHECK(hipMemcpy(p.dev_rows, map.data(), map.size() * sizeof(int), hipMemcpyHostToDevice));
         p.host_rows = map;
     }
@@ -546,7 +568,8 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
                           " bytes of static scratch left after the cost records");
     } else {
         if (g.total > n.partial_capacity) {
-            HIP_CHECK(hipStreamSynchronize(d.stream));
+            sync_stream(d);
+            ++d.layout;
             if (n.partials) HIP_CHECK(hipFree(n.partials));
             n.partials = nullptr;
             HIP_CHECK(hipMalloc(&n.partials, g.total * sizeof(float)));
@@ -630,12 +653,29 @@ static bool one_pass_fits(const Plan& p) {
     return env_int("CPDE_ONE_PASS", 1) && p.fused && p.network && epoch_blocks(p) <= 4 * p.net->dev->compute_units;
 }
 
+// Rewrite the row-major weight copies of every hidden transition from the
+// weights (one launch).
+static void refresh_wt(Net& n) {
+    std::vector<const float*> W;
+    std::vector<float*> WT;
+    std::vector<int> ni, no;
+    for (int t = 1; t + 2 < n.layers; ++t) {
+        W.push_back(n.state[0][t]);
+        WT.push_back(n.wt[t]);
+        ni.push_back(n.neurons[t]);
+        no.push_back(n.neurons[t + 1]);
+    }
+    if (!W.empty()) launch_transpose(*n.dev, W.data(), WT.data(), ni.data(), no.data(), int(W.size()));
+    n.wt_current = true;
+}
+
 // The per-workgroup cost records of a one-pass epoch.
 static CostStats* epoch_records(Plan& p) {
     Device& d = *p.net->dev;
     const int blocks = epoch_blocks(p);
     if (blocks > p.epoch_capacity) {
-        HIP_CHECK(hipStreamSynchronize(d.stream));
+        sync_stream(d);
+        ++d.layout;
         if (p.epoch_partials) HIP_CHECK(hipFree(p.epoch_partials));
         p.epoch_partials = nullptr;
         HIP_CHECK(hipMalloc(&p.epoch_partials, sizeof(CostStats) * size_t(blocks)));
@@ -660,23 +700,10 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostS
     const int blocks = epoch_blocks(p);
     NetArgsHost a = net_args(p);
     GradientPlan g = network_gradients(p, blocks, accumulate, space, a);
-    if (!n.wt_current) {
-        // the backward half reads the row-major weight copies of every hidden
-        // transition, which no workgroup of the same launch may still be
-        // writing; RPROP and Adam keep them current between epochs
-        const float* W[kMaxTransitions];
-        float* WT[kMaxTransitions];
-        int ni[kMaxTransitions], no[kMaxTransitions];
-        int count = 0;
-        for (int t = 1; t + 2 < L; ++t, ++count) {
-            W[count] = n.state[0][t];
-            WT[count] = n.wt[t];
-            ni[count] = n.neurons[t];
-            no[count] = n.neurons[t + 1];
-        }
-        launch_transpose(d, W, WT, ni, no, count);
-        n.wt_current = true;
-    }
+    // the backward half reads the row-major weight copies of every hidden
+    // transition, which no workgroup of the same launch may still be writing;
+    // RPROP and Adam keep them current between epochs
+    if (!n.wt_current) refresh_wt(n);
     void* args[] = {&a, cost_args, &width};
     double flops = 0;
     for (int t = 0; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
@@ -814,6 +841,12 @@ int cpde_device_open(int ordinal, cpde_device** out) {
 int cpde_device_close(cpde_device* dev) {
     return guarded([&] {
         if (!dev) return;
+        if (dev->capturing) {  // an open capture is abandoned
+            hipGraph_t graph = nullptr;
+            (void)hipStreamEndCapture(dev->stream, &graph);
+            if (graph) (void)hipGraphDestroy(graph);
+            dev->capturing = false;
+        }
         (void)hipStreamSynchronize(dev->stream);
         for (auto& e : dev->marks) (void)hipEventDestroy(e);
         for (auto& e : dev->event_pool) (void)hipEventDestroy(e);
@@ -827,7 +860,7 @@ int cpde_device_close(cpde_device* dev) {
 }
 
 int cpde_device_synchronize(cpde_device* dev) {
-    return guarded([&] { HIP_CHECK(hipStreamSynchronize(dev->stream)); });
+    return guarded([&] { sync_stream(*dev); });
 }
 
 int cpde_device_info(cpde_device* dev, char* name, size_t capacity, int* compute_units) {
@@ -853,7 +886,8 @@ int cpde_buffer_alloc(cpde_device* dev, size_t bytes, void** out) {
 int cpde_buffer_free(cpde_device* dev, void* ptr) {
     return guarded([&] {
         if (!ptr) return;
-        HIP_CHECK(hipStreamSynchronize(dev->stream));
+        sync_stream(*dev);
+        ++dev->layout;
         HIP_CHECK(hipFree(ptr));
     });
 }
@@ -862,7 +896,7 @@ int cpde_buffer_upload(cpde_device* dev, void* dst, const void* src, size_t byte
     return guarded([&] {
         if (!bytes) return;
         HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream));
-        HIP_CHECK(hipStreamSynchronize(dev->stream));
+        sync_stream(*dev);
     });
 }
 
@@ -870,7 +904,7 @@ int cpde_buffer_download(cpde_device* dev, void* dst, const void* src, size_t by
     return guarded([&] {
         if (!bytes) return;
         HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream));
-        HIP_CHECK(hipStreamSynchronize(dev->stream));
+        sync_stream(*dev);
     });
 }
 
@@ -916,7 +950,8 @@ int cpde_net_create(cpde_device* dev, int layers, const int* neurons, const int*
             launch_fill(*dev, n->state[3][t], count, 0.002f);
         }
         dev->reserve_grads(T);
-        HIP_CHECK(hipStreamSynchronize(dev->stream));
+        sync_stream(*dev);
+        dev->nets.push_back(n.get());
         *out = n.release();
     });
 }
@@ -924,11 +959,14 @@ int cpde_net_create(cpde_device* dev, int layers, const int* neurons, const int*
 int cpde_net_destroy(cpde_net* net) {
     return guarded([&] {
         if (!net) return;
+        sync_stream(*net->dev);
         if (net->bound) {  // the arena's buffers go back to the network before it frees them
             swap_binding(*net, *net->bound->plan, *net->bound);
             net->bound = nullptr;
         }
-        (void)hipStreamSynchronize(net->dev->stream);
+        auto& live = net->dev->nets;
+        live.erase(std::remove(live.begin(), live.end(), static_cast<Net*>(net)), live.end());
+        ++net->dev->layout;
         for (auto& s : net->state)
             for (float* p : s) (void)hipFree(p);
         for (float* p : net->wt) (void)hipFree(p);
@@ -997,7 +1035,7 @@ int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, i
             p->fused = load_fused(*net->dev, p->tables, net->neurons, width);
             p->network = network_mode();
         }
-        HIP_CHECK(hipStreamSynchronize(net->dev->stream));
+        sync_stream(*net->dev);
         *out = p.release();
     });
 }
@@ -1006,11 +1044,12 @@ int cpde_plan_destroy(cpde_plan* plan) {
     return guarded([&] {
         if (!plan) return;
         Net& n = *plan->net;
+        sync_stream(*n.dev);
         if (n.bound && n.bound->plan == plan) {
             swap_binding(n, *plan, *n.bound);
             n.bound = nullptr;
         }
-        (void)hipStreamSynchronize(plan->net->dev->stream);
+        ++n.dev->layout;
         (void)hipFree(plan->dev_tables);
         (void)hipFree(plan->dev_rows);
         (void)hipFree(plan->epoch_partials);
@@ -1069,11 +1108,12 @@ int cpde_stacks_destroy(cpde_stacks* stacks) {
     return guarded([&] {
         if (!stacks) return;
         Net& n = *stacks->plan->net;
+        sync_stream(*n.dev);
         if (n.bound == stacks) {
             swap_binding(n, *stacks->plan, *stacks);
             n.bound = nullptr;
         }
-        (void)hipStreamSynchronize(n.dev->stream);
+        ++n.dev->layout;
         for (auto* v : {&stacks->z, &stacks->y, &stacks->g})
             for (float* q : *v) (void)hipFree(q);
         (void)hipFree(stacks->input);
@@ -1333,7 +1373,7 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
         if (summary)
             HIP_CHECK(hipMemcpyAsync(dev->host_summary, summary, sizeof(cpde_graph_summary), hipMemcpyDeviceToHost,
                                      dev->stream));
-        HIP_CHECK(hipStreamSynchronize(dev->stream));
+        sync_stream(*dev);
         if (costs && cost_out) {
             std::memcpy(cost_out, dev->host_costs, sizeof(CostStats) * costs);
             for (int i = 0; i < costs && i < int(dev->slot_fresh.size()); ++i)
@@ -1413,7 +1453,8 @@ int cpde_program_compile(cpde_device* dev, const char* source, cpde_program** ou
 int cpde_program_destroy(cpde_program* program) {
     return guarded([&] {
         if (!program) return;
-        (void)hipStreamSynchronize(program->dev->stream);
+        sync_stream(*program->dev);
+        ++program->dev->layout;
         if (program->module) (void)hipModuleUnload(program->module);
         delete program;
     });
@@ -1489,6 +1530,7 @@ int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int coun
 
 int cpde_trace_enable(cpde_device* dev, int on) {
     return guarded([&] {
+        require(!dev->capturing, "a capture is open on this device");
         dev->fold_trace();
         dev->tracing = on != 0;
         for (int k = 0; k < kTraceKinds; ++k) {
@@ -1539,6 +1581,7 @@ int cpde_jit_prepare(int rows, int variables, const int* table, int layers, cons
 int cpde_mark(cpde_device* dev, int slot) {
     return guarded([&] {
         require(slot >= 0 && slot < 8, "invalid event slot");
+        require(!dev->capturing, "a capture is open on this device");
         HIP_CHECK(hipEventRecord(dev->marks[slot], dev->stream));
     });
 }
@@ -1548,6 +1591,101 @@ int cpde_elapsed(cpde_device* dev, int from_slot, int to_slot, float* ms) {
         require(from_slot >= 0 && from_slot < 8 && to_slot >= 0 && to_slot < 8, "invalid event slot");
         HIP_CHECK(hipEventSynchronize(dev->marks[to_slot]));
         HIP_CHECK(hipEventElapsedTime(ms, dev->marks[from_slot], dev->marks[to_slot]));
+    });
+}
+
+// ---- captured epochs --------------------------------------------------------------------
+int cpde_capture_begin(cpde_device* dev) {
+    return guarded([&] {
+        require(dev, "null argument");
+        require(!dev->capturing, "a capture is already open on this device");
+        require(!dev->tracing, "tracing times every launch with events; a capture cannot hold them");
+        dev->capture_nets.clear();
+        for (Net* n : dev->nets) dev->capture_nets.push_back({n, n->active});
+        dev->capture_layout = dev->layout;
+        HIP_CHECK(hipStreamBeginCapture(dev->stream, hipStreamCaptureModeThreadLocal));
+        dev->capturing = true;
+    });
+}
+
+// The recorded calls never ran: their host bookkeeping is undone (active
+// gradient buffers back to the capture's start; the row-major weight copies
+// are rewritten before their next use).
+static void abandon_capture(Device& d) {
+    for (auto& c : d.capture_nets) {
+        c.net->active = c.active;
+        c.net->wt_current = false;
+    }
+    d.capture_nets.clear();
+}
+
+int cpde_capture_end(cpde_device* dev, int keep, cpde_replay** out) {
+    return guarded([&] {
+        require(dev, "null argument");
+        if (out) *out = nullptr;
+        require(dev->capturing, "no capture is open on this device");
+        dev->capturing = false;
+        hipGraph_t graph = nullptr;
+        const hipError_t ended = hipStreamEndCapture(dev->stream, &graph);
+        const bool intact = dev->layout == dev->capture_layout;
+        hipGraphExec_t exec = nullptr;
+        hipError_t made = hipSuccess;
+        if (keep && out && ended == hipSuccess && graph && intact)
+            made = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (!exec) {
+            abandon_capture(*dev);
+            if (!keep) return;
+            require(out != nullptr, "null output");
+            HIP_CHECK(ended);
+            HIP_CHECK(made);
+            require(intact, "device memory was released or regrown during the capture");
+            throw invalid("the capture recorded nothing");
+        }
+        auto r = std::make_unique<cpde_replay>();
+        r->dev = dev;
+        r->exec = exec;
+        r->layout = dev->layout;
+        for (auto& c : dev->capture_nets) r->nets.push_back({c.net, c.active, c.net->active, c.net->generation});
+        dev->capture_nets.clear();
+        // the recorded calls have done their host bookkeeping: their device
+        // work runs now
+        const hipError_t launched = hipGraphLaunch(exec, dev->stream);
+        if (launched != hipSuccess) {
+            (void)hipGraphExecDestroy(exec);
+            for (auto& c : r->nets) {
+                c.net->active = c.before;
+                c.net->wt_current = false;
+            }
+            HIP_CHECK(launched);
+        }
+        *out = r.release();
+    });
+}
+
+int cpde_replay_launch(cpde_replay* replay) {
+    return guarded([&] {
+        require(replay, "null argument");
+        Device& d = *replay->dev;
+        require(!d.capturing, "a capture is open on this device");
+        require(d.layout == replay->layout, "device memory was released or regrown since the capture");
+        for (const auto& c : replay->nets) {
+            require(c.net->active == c.before, "a network's active gradient buffers differ from the capture's");
+            require(c.net->generation == c.generation, "a network's stack arena changed since the capture");
+        }
+        for (const auto& c : replay->nets)
+            if (!c.net->wt_current) refresh_wt(*c.net);
+        HIP_CHECK(hipGraphLaunch(replay->exec, d.stream));
+        for (const auto& c : replay->nets) c.net->active = c.after;
+    });
+}
+
+int cpde_replay_destroy(cpde_replay* replay) {
+    return guarded([&] {
+        if (!replay) return;
+        sync_stream(*replay->dev);
+        (void)hipGraphExecDestroy(replay->exec);
+        delete replay;
     });
 }
 

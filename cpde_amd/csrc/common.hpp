@@ -201,7 +201,25 @@ struct Device {
     void reserve_costs(int costs);
     void reserve_grads(int layers);
     void reserve_scalars(int costs, int layers);
+    // Stream capture (cpde_capture_begin .. cpde_capture_end): the calls in
+    // between record their launches into a HIP graph instead of running them.
+    // A recording holds raw device pointers, so it replays only while no
+    // device memory of this device was released or regrown since (`layout`
+    // counts those events) and while each network's active gradient buffers
+    // are those it was recorded with.
+    bool capturing = false;
+    uint64_t layout = 0, capture_layout = 0;
+    std::vector<Net*> nets;  // live networks
+    struct NetCapture {
+        Net* net;
+        std::vector<int> active;
+    };
+    std::vector<NetCapture> capture_nets;  // state when the open capture began
 };
+
+// Synchronise the device's stream; refused while a capture is open (the
+// caller allocates, frees or reads back, which a recording cannot hold).
+void sync_stream(Device& d);
 
 // Grouped weight-gradient launch (one entry per transition).
 struct WgradArgs {

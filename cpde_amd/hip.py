@@ -85,6 +85,10 @@ SIGNATURES = {
     'cpde_program_destroy': (i32, [vp]),
     'cpde_cost_expression': (i32, [vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, i32]),
     'cpde_epoch_expression': (i32, [vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, i32]),
+    'cpde_capture_begin': (i32, [vp]),
+    'cpde_capture_end': (i32, [vp, i32, vp]),
+    'cpde_replay_launch': (i32, [vp]),
+    'cpde_replay_destroy': (i32, [vp]),
     'cpde_epoch_expression_fused': (i32, [vp, vp, vp]),
     'cpde_graph_execute': (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, i32]),
     'cpde_jit_prepare': (i32, [i32, i32, vp, i32, vp, i32, i32, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
@@ -217,9 +221,33 @@ class Device:
                 out[lib.cpde_trace_name(k).decode()] = (n.value, ms.value, work.value)
         return out
 
+    def capture_begin(self):
+        check(load().cpde_capture_begin(self.handle))
+
+    def capture_end(self, keep=True):
+        """End the open capture; with `keep`, a Replay of it (already run once)."""
+        h = vp()
+        check(load().cpde_capture_end(self.handle, int(keep), ctypes.byref(h) if keep else None))
+        return Replay(self, h) if keep else None
+
     def close(self):
         if self.handle:
             check(load().cpde_device_close(self.handle))
+            self.handle = None
+
+
+class Replay:
+    """A recorded sequence of launches (cpde_capture_end)."""
+
+    def __init__(self, device, handle):
+        self.device, self.handle = device, handle
+
+    def launch(self):
+        check(load().cpde_replay_launch(self.handle))
+
+    def destroy(self):
+        if self.handle:
+            check(load().cpde_replay_destroy(self.handle))
             self.handle = None
 
 

@@ -42,6 +42,7 @@ typedef struct cpde_net_s cpde_net;
 typedef struct cpde_plan_s cpde_plan;
 typedef struct cpde_program_s cpde_program;
 typedef struct cpde_stacks_s cpde_stacks;
+typedef struct cpde_replay_s cpde_replay;
 
 /* Per-cost reduction result: signed double sum and the first bad (sample,
  * component); component -1 means the objective itself
@@ -294,6 +295,29 @@ int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int coun
  * compile (cuda/expression_program.hpp:104-121), done lazily at first use. */
 int cpde_jit_prepare(int rows, int variables, const int* table, int layers, const int* neurons, int width,
                      int compute_units, const char* arch, char* log, size_t log_capacity);
+
+/* ---- captured epochs ------------------------------------------------------------- */
+/* No counterpart in the reference, whose server issues every launch of every
+ * epoch from the host.  Between cpde_capture_begin and cpde_capture_end the
+ * calls on `dev` record their launches into a HIP graph instead of running
+ * them; their host-side bookkeeping still happens.  Calls that would
+ * synchronise the device (allocation, release, read-back) are refused with
+ * CPDE_EINVAL while a capture is open, and so are tracing and marks: run a
+ * sequence once uncaptured so that its buffers exist before recording it.
+ * cpde_capture_end(keep = 1) instantiates the recording and runs it once, so
+ * the recorded calls complete as if they had run; keep = 0, or any failure,
+ * discards it and undoes the bookkeeping that depends on the device work (the
+ * active gradient buffers).  cpde_replay_launch runs the recording again on
+ * the device stream.  It is refused, without launching, once device memory
+ * of the device has been released or regrown since the capture, or when a
+ * network's active gradient buffers are not those it was recorded with (an
+ * optimizer update flips them: record one replay per parity).  Kernel
+ * arguments are fixed at capture: what a replay reads and writes are the
+ * buffers the recorded calls named, with their contents at replay time. */
+int cpde_capture_begin(cpde_device* dev);
+int cpde_capture_end(cpde_device* dev, int keep, cpde_replay** out);
+int cpde_replay_launch(cpde_replay* replay);
+int cpde_replay_destroy(cpde_replay* replay);
 
 /* ---- timing ---------------------------------------------------------------------- */
 /* Kernel tracing (no counterpart in the reference, which has no built-in
