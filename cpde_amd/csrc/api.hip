@@ -296,6 +296,14 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
     }
     t.points_per_block = std::max(1, env_int("CPDE_FUSED_POINTS", t.points_per_block));
     t.net_points_per_block = std::max(1, env_int("CPDE_NET_POINTS", npb));
+    // A chunk of several-point workgroups that leaves CUs without a second
+    // workgroup runs eight waves per workgroup: with one wave per SIMD the
+    // matrix-core and load latencies of the layer chain have nothing to hide
+    // behind.  2->128^4->1 over 729 points (three points per workgroup, 243
+    // workgroups), ms per epoch at orders 0..3: 0.0416 -> 0.0409, 0.0454 ->
+    // 0.0445, 0.0500 -> 0.0487, 0.0576 -> 0.0563.  With more workgroups than
+    // CUs it was slower (order 4, 365 workgroups: 0.0700 -> 0.0742).
+    if (width > 0 && rows <= 16 && npb > 1 && (width + npb - 1) / npb <= compute_units) t.net_threads = 512;
     t.net_threads = env_int("CPDE_NET_THREADS", t.net_threads) == 512 ? 512 : 256;
     // a composition split over lanes pays off while a point's rows fit one
     // matrix-core tile; with two tiles (R > 32) whole compositions per lane are faster
@@ -455,15 +463,14 @@ struct PartialSpace {
 // (CPDE_WGRAD_OCC; two, the kernel's occupancy, keep a second wave on every
 // SIMD to cover the other's loads and barriers).
 static int wgrad_blocks_per_cu() { return std::max(1, env_int("CPDE_WGRAD_OCC", 2)); }
-// Direct tiles per CU the split-K aims for (CPDE_WGRAD_DIRECT_OCC; two
-// measured best on 2->128^4->1 over 729 points: 29.4 us against 31.0 at three
-// and 43.7 at four).
-static int wgrad_direct_blocks_per_cu() { return std::max(1, env_int("CPDE_WGRAD_DIRECT_OCC", 2)); }
-// Direct tiles are chosen for short splits only when a split still has this
-// many columns: on 2->128^4->1 over 729 points at order 6 (512 columns per
-// split) they took the weight gradient and its reduction from 39.0 to 37.2 us;
-// at order 2 (128 columns per split) from 21.1 to 22.4 us.
-constexpr int kWgradDirectMinColumns = 256;
+// Direct tiles per CU the split-K aims for (CPDE_WGRAD_DIRECT_OCC).  One
+// measured best on 2->128^4->1 over 729 points at every derivative order
+// (fewer, longer splits: each tile's fixed cost of set-up, cross-wave sum and
+// partial rows is paid half as often, and the reduction reads half the
+// partials).  Epoch ms at orders 0..6, one tile per CU against two:
+// 0.0416/0.0416, 0.0453/0.0475, 0.0499/0.0525, 0.0575/0.0597, 0.0701/0.0721,
+// 0.0936/0.0954, 0.1033/0.1050; the Poisson graph epoch 0.0924 against 0.0943.
+static int wgrad_direct_blocks_per_cu() { return std::max(1, env_int("CPDE_WGRAD_DIRECT_OCC", 1)); }
 
 // The gradient plan of transitions [first, first + count), count at most
 // kMaxTransitions (one grouped launch and one reduction); external_splits is
@@ -506,12 +513,10 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
     int total_tiles = count_tiles();
     const int force = env_int("CPDE_WGRAD_DIRECT", -1);  // 0: LDS-staged tiles, 2: direct tiles, else chosen
     if (total_tiles > 0 && K / splits_for(total_tiles) < kWgradMinColumns) {
-        // short splits: 64x64 tiles, fed straight from global memory while a
-        // split keeps enough columns, LDS-staged otherwise
+        // short splits: 64x64 tiles fed straight from global memory (LDS-staged
+        // with CPDE_WGRAD_DIRECT=0)
         small_tiles = true;
-        direct = true;  // the split count the direct tiles would have
-        const bool long_enough = K / splits_for(count_tiles()) >= kWgradDirectMinColumns;
-        direct = force == 2 || (force != 0 && long_enough);
+        direct = force != 0;
         total_tiles = count_tiles();
     } else if (total_tiles > 0 && force == 2) {
         direct = true;  // forced on long reductions too

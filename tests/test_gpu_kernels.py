@@ -156,6 +156,7 @@ def test_epoch_matches_oracle(device, path, order, neurons, points, chunk):
 
 @pytest.mark.parametrize('order,neurons,points', [
     (4, [2, 128, 128, 1], 729),   # 64x64 tiles over short splits: direct tiles by default
+    (0, [2, 128, 128, 128, 1], 729),  # one row: 64-column splits
     (6, [2, 64, 48, 1], 300),
     (3, [2, 30, 18, 1], 101),     # widths that are not multiples of 4: scalar operand loads
     (2, [2, 80, 96, 40, 1], 2000),
