@@ -50,10 +50,19 @@ void check_hip(hipError_t status, const char* what, const char* file, int line) 
     throw device_error(buf);
 }
 
-void sync_stream(Device& d) {
+// Launch the waiting gradient reduction, if any.
+void flush_reduce(Device& d) {
+    if (!d.waiting.open) return;
+    d.waiting.open = false;
+    d.waiting.partial_end = 0;
+    launch_reduce_grouped(d, d.waiting.ra);
+}
+
+void sync_stream(Device& d, int site) {
     if (d.capturing)
         throw invalid("this call synchronises the device (it allocates, frees or reads back), which a capture "
-                      "cannot record: run it once before cpde_capture_begin");
+                      "cannot record: run it once before cpde_capture_begin (api.hip:" + std::to_string(site) + ")");
+    flush_reduce(d);
     HIP_CHECK(hipStreamSynchronize(d.stream));
 }
 
@@ -78,7 +87,7 @@ TraceScope::~TraceScope() {
 
 void Device::fold_trace() {
     if (pending.empty()) return;
-    sync_stream(*this);
+    sync_stream(*this, __LINE__);
     for (const auto& r : pending) {
         float ms = 0;
         HIP_CHECK(hipEventElapsedTime(&ms, r.start, r.stop));
@@ -101,7 +110,7 @@ void Device::reserve_scalars(int costs, int layers) {
     costs = std::max(costs, cost_capacity);
     layers = std::max(layers, grad_capacity);
     if (costs == cost_capacity && layers == grad_capacity && scalar_block) return;
-    sync_stream(*this);
+    sync_stream(*this, __LINE__);
     const size_t cost_bytes = (sizeof(CostStats) * size_t(costs) + 255) / 256 * 256;
     const size_t grad_bytes = (sizeof(GradStats) * size_t(layers) + 255) / 256 * 256;
     const size_t bytes = cost_bytes + grad_bytes + sizeof(cpde_graph_summary);
@@ -143,7 +152,7 @@ static void reserve_arena(Net& net, const Plan& p) {
         if (p.columns() * net.neurons[l] > net.capacity[l]) grow = true;
     if (!grow) return;
     require(!net.bound, "a stack set is bound to this network: unbind it before using another plan");
-    sync_stream(*net.dev);
+    sync_stream(*net.dev, __LINE__);
     ++net.dev->layout;
     for (int l = 0; l < net.layers; ++l) {
         const size_t need = std::max(net.capacity[l], p.columns() * net.neurons[l]);
@@ -213,7 +222,7 @@ static const float* activations(const Plan& p, int l) {
 static const int* plan_rows(Plan& p, const int* rows) {
     std::vector<int> map(rows, rows + p.rows);
     if (map != p.host_rows) {
-        sync_stream(*p.net->dev);
+        sync_stream(*p.net->dev, __LINE__);
         HIP_CHECK(hipMemcpy(p.dev_rows, map.data(), map.size() * sizeof(int), hipMemcpyHostToDevice));
         p.host_rows = map;
     }
@@ -449,6 +458,10 @@ struct GradientPlan {
     size_t offset[kMaxTransitions] = {};  // first partial of each transition (local index)
     double flops = 0;
     size_t total = 0;
+    // partials in the network's own buffer: the network and the end of this
+    // plan's floats there (its reduction may then wait, cpde_gradients_defer)
+    Net* net = nullptr;
+    size_t partial_end = 0;
 };
 
 // Where a gradient plan's split partials live: the network's own lazily grown
@@ -572,15 +585,35 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
                           " bytes, beyond the " + std::to_string(space.floats * sizeof(float)) +
                           " bytes of static scratch left after the cost records");
     } else {
-        if (g.total > n.partial_capacity) {
-            sync_stream(d);
+        // a waiting reduction of this network keeps the front of the buffer
+        // when this plan's partials fit behind it and it can take a second
+        // pass; otherwise it is launched, and the buffer grows so that the
+        // next pass fits behind it
+        size_t offset0 = 0, need = g.total;
+        Device::PendingReduce& w = d.waiting;
+        if (w.open) {
+            const bool same = w.net == &n && !w.ra.second;
+            if (same && w.partial_end + g.total <= n.partial_capacity) offset0 = w.partial_end;
+            else {
+                if (same) need = w.partial_end + g.total;
+                flush_reduce(d);
+            }
+        }
+        // while reductions are deferred, room for two consecutive passes side
+        // by side, taken while no capture is open (a recorded epoch finds it)
+        if (d.defer && !d.capturing) need = std::max(need, n.last_partials + g.total);
+        n.last_partials = g.total;
+        if (need > n.partial_capacity) {
+            sync_stream(d, __LINE__);
             ++d.layout;
             if (n.partials) HIP_CHECK(hipFree(n.partials));
             n.partials = nullptr;
-            HIP_CHECK(hipMalloc(&n.partials, g.total * sizeof(float)));
-            n.partial_capacity = g.total;
+            HIP_CHECK(hipMalloc(&n.partials, need * sizeof(float)));
+            n.partial_capacity = need;
         }
-        base = n.partials;
+        base = n.partials + offset0;
+        g.net = &n;
+        g.partial_end = offset0 + g.total;
     }
     w = 0;
     for (int k = 0; k < T; ++k) {
@@ -612,13 +645,71 @@ static GradientPlan network_gradients(Plan& p, int blocks, bool accumulate, cons
     return g;
 }
 
+// Whether reduction `g` can ride as the second pass of the waiting one: the
+// same network, transitions, layouts and gradient buffers, accumulating onto
+// the first pass's result, with room for its cost finishes.
+static bool joins(const Device::PendingReduce& w, const GradientPlan& g) {
+    const ReduceArgs &a = w.ra, &b = g.ra;
+    if (!w.open || w.net != g.net || !g.net || a.second || a.with_graph || !b.accumulate ||
+        a.transitions != b.transitions || a.costs + b.costs > kReduceCosts)
+        return false;
+    for (int k = 0; k < a.transitions; ++k)
+        if (a.M[k] != b.M[k] || a.N[k] != b.N[k] || a.split_minor[k] != b.split_minor[k] || a.grad[k] != b.grad[k])
+            return false;
+    return true;
+}
+
 // `update`: the reduction also applies RPROP to the group's transitions
 // (transitions [first, first + count) of `update`), whose gradients it
 // completes; the caller flips the active buffers once every group is done.
+// Otherwise, while the device defers reductions (cpde_gradients_defer), a
+// reduction of partials in the network's own buffer waits: as the second pass
+// of a waiting one when it joins it, else as the new waiting one.
 static void run_gradients(Device& d, const GradientPlan& g, Net* update = nullptr, int first = 0) {
     if (g.wa.transitions > 0) launch_wgrad_grouped(d, g.wa, g.flops);
-    if (update) launch_reduce_rprop(d, g.ra, *update, first);
-    else launch_reduce_grouped(d, g.ra);
+    if (update) {
+        flush_reduce(d);
+        launch_reduce_rprop(d, g.ra, *update, first);
+        return;
+    }
+    if (!d.defer || !g.net) {
+        flush_reduce(d);
+        launch_reduce_grouped(d, g.ra);
+        return;
+    }
+    Device::PendingReduce& w = d.waiting;
+    if (joins(w, g)) {
+        for (int k = 0; k < g.ra.transitions; ++k) {
+            w.ra.partial2[k] = g.ra.partial[k];
+            w.ra.splits2[k] = g.ra.splits[k];
+        }
+        w.ra.second = 1;
+        for (int c = 0; c < g.ra.costs; ++c) {
+            const int i = w.ra.costs++;
+            w.ra.cost_partials[i] = g.ra.cost_partials[c];
+            w.ra.cost_total[i] = g.ra.cost_total[c];
+            w.ra.cost_count[i] = g.ra.cost_count[c];
+            w.ra.cost_overwrite[i] = g.ra.cost_overwrite[c];
+        }
+        w.partial_end = g.partial_end;
+        return;
+    }
+    flush_reduce(d);
+    w.open = true;
+    w.net = g.net;
+    w.ra = g.ra;
+    w.partial_end = g.partial_end;
+}
+
+// Launch the waiting reduction when it reads `records` (which the caller is
+// about to overwrite) or finishes a cost into `slot` (which the caller is
+// about to finish into).
+static void flush_if_reads(Device& d, const CostStats* records, int slot = -1) {
+    const ReduceArgs& a = d.waiting.ra;
+    if (!d.waiting.open) return;
+    for (int c = 0; c < a.costs; ++c)
+        if (a.cost_partials[c] == records || (slot >= 0 && a.cost_total[c] == d.cost_totals + slot))
+            return flush_reduce(d);
 }
 
 // Host bookkeeping of an RPROP update launched as part of a reduction
@@ -675,18 +766,22 @@ static void refresh_wt(Net& n) {
 }
 
 // The per-workgroup cost records of a one-pass epoch.
+// Two sets, used in turn: a pass's records stay intact while the next pass on
+// the plan runs, so a waiting reduction can still finish the first pass's
+// cost (cpde_gradients_defer).
 static CostStats* epoch_records(Plan& p) {
     Device& d = *p.net->dev;
     const int blocks = epoch_blocks(p);
     if (blocks > p.epoch_capacity) {
-        sync_stream(d);
+        sync_stream(d, __LINE__);
         ++d.layout;
         if (p.epoch_partials) HIP_CHECK(hipFree(p.epoch_partials));
         p.epoch_partials = nullptr;
-        HIP_CHECK(hipMalloc(&p.epoch_partials, sizeof(CostStats) * size_t(blocks)));
+        HIP_CHECK(hipMalloc(&p.epoch_partials, 2 * sizeof(CostStats) * size_t(blocks)));
         p.epoch_capacity = blocks;
     }
-    return p.epoch_partials;
+    p.epoch_turn ^= 1;
+    return p.epoch_partials + (p.epoch_turn ? p.epoch_capacity : 0);
 }
 
 // Forward, cost and backward of one chunk in one network-fused launch of
@@ -703,6 +798,7 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostS
     int width = p.width;
     const double cols = double(p.columns());
     const int blocks = epoch_blocks(p);
+    flush_if_reads(d, records, cost_index);  // the kernel rewrites this plan's records
     NetArgsHost a = net_args(p);
     GradientPlan g = network_gradients(p, blocks, accumulate, space, a);
     // the backward half reads the row-major weight copies of every hidden
@@ -718,10 +814,11 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostS
         launch_module(d, kernel, unsigned(blocks), 1, args, unsigned(p.fused->net_threads));
     }
     if (blocks <= kMaxCostBlocks) {  // the cost's finish rides in the gradient reduction launch
-        g.ra.cost_partials = records;
-        g.ra.cost_total = d.cost_totals + cost_index;
-        g.ra.cost_count = blocks;
-        g.ra.cost_overwrite = d.take_fresh(cost_index) ? 1 : 0;
+        g.ra.costs = 1;
+        g.ra.cost_partials[0] = records;
+        g.ra.cost_total[0] = d.cost_totals + cost_index;
+        g.ra.cost_count[0] = blocks;
+        g.ra.cost_overwrite[0] = d.take_fresh(cost_index) ? 1 : 0;
     } else {
         launch_finish_cost(d, records, blocks, cost_index);
     }
@@ -865,7 +962,7 @@ int cpde_device_close(cpde_device* dev) {
 }
 
 int cpde_device_synchronize(cpde_device* dev) {
-    return guarded([&] { sync_stream(*dev); });
+    return guarded([&] { sync_stream(*dev, __LINE__); });
 }
 
 int cpde_device_info(cpde_device* dev, char* name, size_t capacity, int* compute_units) {
@@ -891,7 +988,7 @@ int cpde_buffer_alloc(cpde_device* dev, size_t bytes, void** out) {
 int cpde_buffer_free(cpde_device* dev, void* ptr) {
     return guarded([&] {
         if (!ptr) return;
-        sync_stream(*dev);
+        sync_stream(*dev, __LINE__);
         ++dev->layout;
         HIP_CHECK(hipFree(ptr));
     });
@@ -899,22 +996,25 @@ int cpde_buffer_free(cpde_device* dev, void* ptr) {
 
 int cpde_buffer_upload(cpde_device* dev, void* dst, const void* src, size_t bytes) {
     return guarded([&] {
+        flush_reduce(*dev);
         if (!bytes) return;
         HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream));
-        sync_stream(*dev);
+        sync_stream(*dev, __LINE__);
     });
 }
 
 int cpde_buffer_download(cpde_device* dev, void* dst, const void* src, size_t bytes) {
     return guarded([&] {
+        flush_reduce(*dev);
         if (!bytes) return;
         HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream));
-        sync_stream(*dev);
+        sync_stream(*dev, __LINE__);
     });
 }
 
 int cpde_buffer_copy(cpde_device* dev, void* dst, const void* src, size_t bytes) {
     return guarded([&] {
+        flush_reduce(*dev);
         if (!bytes) return;
         HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, dev->stream));
     });
@@ -955,7 +1055,7 @@ int cpde_net_create(cpde_device* dev, int layers, const int* neurons, const int*
             launch_fill(*dev, n->state[3][t], count, 0.002f);
         }
         dev->reserve_grads(T);
-        sync_stream(*dev);
+        sync_stream(*dev, __LINE__);
         dev->nets.push_back(n.get());
         *out = n.release();
     });
@@ -964,7 +1064,7 @@ int cpde_net_create(cpde_device* dev, int layers, const int* neurons, const int*
 int cpde_net_destroy(cpde_net* net) {
     return guarded([&] {
         if (!net) return;
-        sync_stream(*net->dev);
+        sync_stream(*net->dev, __LINE__);
         if (net->bound) {  // the arena's buffers go back to the network before it frees them
             swap_binding(*net, *net->bound->plan, *net->bound);
             net->bound = nullptr;
@@ -984,6 +1084,7 @@ int cpde_net_destroy(cpde_net* net) {
 
 int cpde_net_state(cpde_net* net, int transition, int buffer, float** device_ptr, int* count) {
     return guarded([&] {
+        flush_reduce(*net->dev);
         require(transition >= 0 && transition < net->layers - 1 && buffer >= 0 && buffer < 4, "invalid state buffer");
         if (buffer == 0) net->wt_current = false;  // the caller may write the weights
         if (device_ptr) *device_ptr = net->state[buffer][transition];
@@ -998,6 +1099,7 @@ int cpde_net_active(cpde_net* net, int transition) {
 
 int cpde_net_set_active(cpde_net* net, int transition, int active) {
     return guarded([&] {
+        flush_reduce(*net->dev);
         require(transition >= 0 && transition < net->layers - 1 && (active == 1 || active == 2),
                 "invalid active gradient buffer");
         net->active[transition] = active;
@@ -1040,7 +1142,7 @@ int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, i
             p->fused = load_fused(*net->dev, p->tables, net->neurons, width);
             p->network = network_mode();
         }
-        sync_stream(*net->dev);
+        sync_stream(*net->dev, __LINE__);
         *out = p.release();
     });
 }
@@ -1049,7 +1151,7 @@ int cpde_plan_destroy(cpde_plan* plan) {
     return guarded([&] {
         if (!plan) return;
         Net& n = *plan->net;
-        sync_stream(*n.dev);
+        sync_stream(*n.dev, __LINE__);
         if (n.bound && n.bound->plan == plan) {
             swap_binding(n, *plan, *n.bound);
             n.bound = nullptr;
@@ -1113,7 +1215,7 @@ int cpde_stacks_destroy(cpde_stacks* stacks) {
     return guarded([&] {
         if (!stacks) return;
         Net& n = *stacks->plan->net;
-        sync_stream(*n.dev);
+        sync_stream(*n.dev, __LINE__);
         if (n.bound == stacks) {
             swap_binding(n, *stacks->plan, *stacks);
             n.bound = nullptr;
@@ -1198,13 +1300,25 @@ int cpde_output(cpde_plan* plan, float* dest, int dest_width, const int* rows, i
 }
 
 int cpde_costs_begin(cpde_device* dev, int costs) {
-    return guarded([&] { launch_costs_begin(*dev, costs); });
+    return guarded([&] {
+        flush_reduce(*dev);
+        launch_costs_begin(*dev, costs);
+    });
+}
+
+int cpde_gradients_defer(cpde_device* dev, int on) {
+    return guarded([&] {
+        require(dev, "null argument");
+        dev->defer = on != 0;
+        if (!on) flush_reduce(*dev);
+    });
 }
 
 int cpde_cost_matching(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
                        const float* weights, int weight_samples, int offset, int valid, int cost_index, int collect,
                        int gradient) {
     return guarded([&] {
+        flush_if_reads(*plan->net->dev, nullptr, cost_index);
         Net& n = *plan->net;
         Device& d = *n.dev;
         require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
@@ -1266,6 +1380,7 @@ int cpde_epoch_matching_static(cpde_plan* plan, const float* target, int target_
                                const float* weights, int weight_samples, int offset, int valid, int cost_index,
                                int collect, int accumulate) {
     return guarded([&] {
+        flush_reduce(*plan->net->dev);
         Net& n = *plan->net;
         Device& d = *n.dev;
         if (!d.static_scratch) throw invalid("no static scratch on this device: " + d.static_scratch_error);
@@ -1292,6 +1407,7 @@ int cpde_cost_polynomial(cpde_plan* plan, const cpde_poly_term* terms, int term_
                          const float* rhs, const float* weights, int equations, int samples, int offset, int valid,
                          int cost_index, int collect, int gradient) {
     return guarded([&] {
+        flush_if_reads(*plan->net->dev, nullptr, cost_index);
         Net& n = *plan->net;
         Device& d = *n.dev;
         require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
@@ -1333,6 +1449,7 @@ int cpde_backward(cpde_plan* plan, int accumulate) {
 // ---- reductions and optimizers --------------------------------------------------------------
 int cpde_inspect_gradients(cpde_net* net) {
     return guarded([&] {
+        flush_reduce(*net->dev);
         Device& d = *net->dev;
         const int T = net->layers - 1;
         d.reserve_grads(T);
@@ -1358,6 +1475,7 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
                                 cpde_gradient_stats* gradient_out, const cpde_graph_summary* summary,
                                 cpde_graph_summary* summary_out) {
     return guarded([&] {
+        flush_reduce(*dev);
         require(costs <= dev->cost_capacity && layers <= dev->grad_capacity, "scalar slots out of range");
         require(summary == nullptr || summary_out != nullptr, "graph summary without a destination");
         const bool own_summary = summary == nullptr && summary_out != nullptr;
@@ -1378,7 +1496,7 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
         if (summary)
             HIP_CHECK(hipMemcpyAsync(dev->host_summary, summary, sizeof(cpde_graph_summary), hipMemcpyDeviceToHost,
                                      dev->stream));
-        sync_stream(*dev);
+        sync_stream(*dev, __LINE__);
         if (costs && cost_out) {
             std::memcpy(cost_out, dev->host_costs, sizeof(CostStats) * costs);
             for (int i = 0; i < costs && i < int(dev->slot_fresh.size()); ++i)
@@ -1391,26 +1509,37 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
 }
 
 int cpde_rprop(cpde_net* net) {
-    return guarded([&] { launch_rprop(*net->dev, *net); });
+    return guarded([&] {
+        flush_reduce(*net->dev);
+        launch_rprop(*net->dev, *net);
+    });
 }
 
 int cpde_adam(cpde_net* net, int step, float lr) {
     return guarded([&] {
+        flush_reduce(*net->dev);
         require(step >= 1, "Adam step must be positive");
         launch_adam(*net->dev, *net, step, lr);
     });
 }
 
 int cpde_set_steps(cpde_net* net, float value) {
-    return guarded([&] { launch_set_steps(*net->dev, *net, value); });
+    return guarded([&] {
+        flush_reduce(*net->dev);
+        launch_set_steps(*net->dev, *net, value);
+    });
 }
 
 int cpde_restore_steps(cpde_net* net, float floor_value) {
-    return guarded([&] { launch_restore_steps(*net->dev, *net, floor_value); });
+    return guarded([&] {
+        flush_reduce(*net->dev);
+        launch_restore_steps(*net->dev, *net, floor_value);
+    });
 }
 
 int cpde_zero_gradient(cpde_net* net) {
     return guarded([&] {
+        flush_reduce(*net->dev);
         std::vector<float*> p;
         std::vector<int> counts;
         for (int t = 0; t + 1 < net->layers; ++t) {
@@ -1423,6 +1552,7 @@ int cpde_zero_gradient(cpde_net* net) {
 
 int cpde_reset_optimizer(cpde_net* net) {
     return guarded([&] {
+        flush_reduce(*net->dev);
         for (int t = 0; t + 1 < net->layers; ++t) {
             net->active[t] = 1;
             for (int b = 1; b < 4; ++b) launch_fill(*net->dev, net->state[b][t], net->param_count(t), 0.0f);
@@ -1458,7 +1588,7 @@ int cpde_program_compile(cpde_device* dev, const char* source, cpde_program** ou
 int cpde_program_destroy(cpde_program* program) {
     return guarded([&] {
         if (!program) return;
-        sync_stream(*program->dev);
+        sync_stream(*program->dev, __LINE__);
         ++program->dev->layout;
         if (program->module) (void)hipModuleUnload(program->module);
         delete program;
@@ -1469,6 +1599,7 @@ int cpde_cost_expression(cpde_plan* plan, cpde_program* program, const double* f
                          const double* quadrature_weights, int samples, int offset, int valid,
                          const double* multiplier, void* scratch, int cost_index, int collect, int gradient) {
     return guarded([&] {
+        flush_if_reads(*plan->net->dev, nullptr, cost_index);
         Net& n = *plan->net;
         Device& d = *n.dev;
         require(cost_index >= 0 && cost_index < d.cost_capacity, "cost slot out of range");
@@ -1528,13 +1659,25 @@ int cpde_graph_execute(cpde_device* dev, const cpde_scalar_node* nodes, int coun
                        int gradient) {
     return guarded([&] {
         require(leaves <= dev->cost_capacity, "graph leaves exceed cost slots");
-        launch_graph(*dev, nodes, count, root, leaves, values, adjoints, multipliers, active,
-                     summary ? summary : dev->graph_summary, gradient != 0);
+        const GraphLaunch g = graph_launch(*dev, nodes, count, root, leaves, values, adjoints, multipliers, active,
+                                           summary ? summary : dev->graph_summary, gradient != 0);
+        launch_clear_fresh(*dev, leaves);
+        Device::PendingReduce& w = dev->waiting;
+        if (w.open && !w.ra.with_graph) {
+            // the graph rides in the waiting reduction, after its cost finishes
+            w.ra.with_graph = 1;
+            w.ra.graph = g;
+            flush_reduce(*dev);
+        } else {
+            flush_reduce(*dev);
+            launch_graph(*dev, g);
+        }
     });
 }
 
 int cpde_trace_enable(cpde_device* dev, int on) {
     return guarded([&] {
+        flush_reduce(*dev);
         require(!dev->capturing, "a capture is open on this device");
         dev->fold_trace();
         dev->tracing = on != 0;
@@ -1547,6 +1690,7 @@ int cpde_trace_enable(cpde_device* dev, int on) {
 
 int cpde_trace_read(cpde_device* dev, int kind, uint64_t* launches, double* total_ms, double* work) {
     return guarded([&] {
+        flush_reduce(*dev);
         require(kind >= 0 && kind < kTraceKinds, "invalid trace kind");
         dev->fold_trace();
         if (launches) *launches = dev->trace_launches[kind];
@@ -1585,6 +1729,7 @@ int cpde_jit_prepare(int rows, int variables, const int* table, int layers, cons
 
 int cpde_mark(cpde_device* dev, int slot) {
     return guarded([&] {
+        flush_reduce(*dev);
         require(slot >= 0 && slot < 8, "invalid event slot");
         require(!dev->capturing, "a capture is open on this device");
         HIP_CHECK(hipEventRecord(dev->marks[slot], dev->stream));
@@ -1605,6 +1750,7 @@ int cpde_capture_begin(cpde_device* dev) {
         require(dev, "null argument");
         require(!dev->capturing, "a capture is already open on this device");
         require(!dev->tracing, "tracing times every launch with events; a capture cannot hold them");
+        flush_reduce(*dev);
         dev->capture_nets.clear();
         for (Net* n : dev->nets) dev->capture_nets.push_back({n, n->active});
         dev->capture_layout = dev->layout;
@@ -1629,6 +1775,7 @@ int cpde_capture_end(cpde_device* dev, int keep, cpde_replay** out) {
         require(dev, "null argument");
         if (out) *out = nullptr;
         require(dev->capturing, "no capture is open on this device");
+        flush_reduce(*dev);  // recorded with the rest
         dev->capturing = false;
         hipGraph_t graph = nullptr;
         const hipError_t ended = hipStreamEndCapture(dev->stream, &graph);
@@ -1678,6 +1825,7 @@ int cpde_replay_launch(cpde_replay* replay) {
             require(c.net->active == c.before, "a network's active gradient buffers differ from the capture's");
             require(c.net->generation == c.generation, "a network's stack arena changed since the capture");
         }
+        flush_reduce(d);
         for (const auto& c : replay->nets)
             if (!c.net->wt_current) refresh_wt(*c.net);
         HIP_CHECK(hipGraphLaunch(replay->exec, d.stream));
@@ -1688,7 +1836,7 @@ int cpde_replay_launch(cpde_replay* replay) {
 int cpde_replay_destroy(cpde_replay* replay) {
     return guarded([&] {
         if (!replay) return;
-        sync_stream(*replay->dev);
+        sync_stream(*replay->dev, __LINE__);
         (void)hipGraphExecDestroy(replay->exec);
         delete replay;
     });

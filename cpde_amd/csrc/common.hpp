@@ -93,6 +93,7 @@ struct Net {
     // split-K partial buffer for the weight-gradient contraction
     float* partials = nullptr;
     size_t partial_capacity = 0;
+    size_t last_partials = 0;  // floats the previous gradient plan of the network used
     // a plan's own stack set bound in place of the arena (cpde_plan_bind); while
     // bound, the set holds the arena's pointers and the plan's own input
     struct Stacks* bound = nullptr;
@@ -122,8 +123,8 @@ struct Plan {
     float* input = nullptr;
     std::shared_ptr<FusedModule> fused;  // null: table-driven kernels
     bool network = false;                // fused: one network-wide kernel per pass
-    CostStats* epoch_partials = nullptr;  // one-pass epoch: one cost record per workgroup
-    int epoch_capacity = 0;
+    CostStats* epoch_partials = nullptr;  // one-pass epoch: one cost record per workgroup, two sets
+    int epoch_capacity = 0, epoch_turn = 0;
     // one-pass expression epochs of this plan, by program id
     std::vector<std::pair<uint64_t, std::shared_ptr<ExpressionEpoch>>> expression_epochs;
     size_t columns() const { return size_t(rows) * size_t(width); }
@@ -138,6 +139,40 @@ struct Program {
     uint64_t id = 0;     // unique per compiled program
 };
 
+// The scalar cost graph's evaluation (cost_graph::execute) as one lane runs it.
+struct GraphLaunch {
+    const cpde_scalar_node* nodes;
+    const CostStats* integrals;
+    double *values, *adjoints, *multipliers;
+    int* active;
+    cpde_graph_summary* summary;
+    int count, root, leaves, gradient;
+};
+
+constexpr int kReduceCosts = 4;  // cost finishes one reduction launch carries
+struct ReduceArgs {
+    const float* partial[kMaxTransitions];
+    float* grad[kMaxTransitions];
+    int M[kMaxTransitions], N[kMaxTransitions], splits[kMaxTransitions];
+    int begin[kMaxTransitions + 1];        // first entry of each transition (bytes accounting)
+    int block_begin[kMaxTransitions + 1];  // first block of each transition
+    int split_minor[kMaxTransitions];      // partial layout: 0 [split][entry], 1 [entry][split]
+    // a second backward pass over the same entries, in the same layout: its
+    // sum is added after the first's, so one launch reduces both passes bit
+    // for bit as two launches in turn (splits2 0: no second pass)
+    const float* partial2[kMaxTransitions];
+    int splits2[kMaxTransitions];
+    int transitions, accumulate, second;
+    // cost finishes riding in the launch: one more block finishes them in
+    // order (each as launch_finish_cost would, from at most kMaxCostBlocks
+    // records), then, with `with_graph`, evaluates the scalar graph on its
+    // first lane, which wrote the finished costs
+    const CostStats* cost_partials[kReduceCosts];
+    CostStats* cost_total[kReduceCosts];
+    int cost_count[kReduceCosts], cost_overwrite[kReduceCosts];
+    int costs, with_graph;
+    GraphLaunch graph;
+};
 // Per-launch device timing (HIP events on the library's stream), grouped by
 // kernel class.  `work` is the launch's algorithmic work: bytes for the
 // HBM-bound classes, flops for the matrix-core classes.
@@ -215,11 +250,24 @@ struct Device {
         std::vector<int> active;
     };
     std::vector<NetCapture> capture_nets;  // state when the open capture began
+    // Deferred gradient reductions (cpde_gradients_defer): a backward pass's
+    // reduction waits so that the next pass over the same network, and the
+    // scalar graph, ride in the same launch.  `partial_end` floats of the
+    // network's partial buffer belong to the waiting reduction.
+    bool defer = false;
+    struct PendingReduce {
+        bool open = false;
+        Net* net = nullptr;
+        ReduceArgs ra{};
+        size_t partial_end = 0;
+    } waiting;
 };
 
 // Synchronise the device's stream; refused while a capture is open (the
 // caller allocates, frees or reads back, which a recording cannot hold).
-void sync_stream(Device& d);
+void sync_stream(Device& d, int site = 0);
+// Launch the reduction that cpde_gradients_defer keeps waiting, if any.
+void flush_reduce(Device& d);
 
 // Grouped weight-gradient launch (one entry per transition).
 struct WgradArgs {
@@ -231,20 +279,6 @@ struct WgradArgs {
     int block_begin[kMaxTransitions + 1];
     int transitions, K, R;
     int direct;  // 1: 64x64 tiles fed straight from global memory (wgrad_direct_kernel)
-};
-struct ReduceArgs {
-    const float* partial[kMaxTransitions];
-    float* grad[kMaxTransitions];
-    int M[kMaxTransitions], N[kMaxTransitions], splits[kMaxTransitions];
-    int begin[kMaxTransitions + 1];        // first entry of each transition (bytes accounting)
-    int block_begin[kMaxTransitions + 1];  // first block of each transition
-    int split_minor[kMaxTransitions];      // partial layout: 0 [split][entry], 1 [entry][split]
-    int transitions, accumulate;
-    // optional: one more block finishes a cost from its per-block records
-    // (cost_count > 0, at most kMaxCostBlocks), as launch_finish_cost would
-    const CostStats* cost_partials;
-    CostStats* cost_total;
-    int cost_count, cost_overwrite;
 };
 // Blocks reduce_grouped_kernel uses for a transition of `count` entries.
 inline int reduce_blocks(int count, bool split_minor) { return split_minor ? (count + 3) / 4 : (count + 63) / 64; }
@@ -336,7 +370,9 @@ void launch_rprop(Device& d, Net& net);
 void launch_adam(Device& d, Net& net, int step, float lr);
 void launch_set_steps(Device& d, Net& net, float value);
 void launch_restore_steps(Device& d, Net& net, float floor_value);
-void launch_graph(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,
-                  double* adjoints, double* multipliers, int* active, cpde_graph_summary* summary, bool gradient);
+GraphLaunch graph_launch(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,
+                         double* adjoints, double* multipliers, int* active, cpde_graph_summary* summary,
+                         bool gradient);
+void launch_graph(Device& d, const GraphLaunch& g);
 
 }  // namespace cpde

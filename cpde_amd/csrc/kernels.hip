@@ -597,6 +597,7 @@ __device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int 
 // scheduling.
 __device__ void finish_cost_records(const CostStats* __restrict__ records, int count, CostStats* __restrict__ total,
                                     int overwrite);
+__device__ void run_graph(const GraphLaunch& g);
 
 // UPDATE: the lane that finishes an entry's gradient applies RPROP to it
 // (reduce_rprop_kernel), which is the reduction followed by rprop_kernel in one
@@ -604,8 +605,13 @@ __device__ void finish_cost_records(const CostStats* __restrict__ records, int c
 template <bool UPDATE>
 __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const OptimizerArgs& o) {
     __shared__ float part[4][64];
-    if (a.cost_count && int(blockIdx.x) == a.block_begin[a.transitions]) {
-        finish_cost_records(a.cost_partials, a.cost_count, a.cost_total, a.cost_overwrite);
+    if ((a.costs || a.with_graph) && int(blockIdx.x) == a.block_begin[a.transitions]) {
+        for (int c = 0; c < a.costs; ++c) {
+            if (c) __syncthreads();  // the block reduction's shared slots are reused
+            finish_cost_records(a.cost_partials[c], a.cost_count[c], a.cost_total[c], a.cost_overwrite[c]);
+        }
+        // the lane that wrote the finished costs evaluates the graph on them
+        if (a.with_graph && threadIdx.x == 0) run_graph(a.graph);
         return;
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -626,54 +632,70 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
             for (int u = 0; u < U; u += 2 * w) acc[u] += acc[u + w];
         return acc[0];
     };
+    const bool two = a.splits2[t] > 0;  // uniform over the block
     if (!a.split_minor[t]) {
         const size_t stride = size_t(count);
         const int j = local * 64 + lane;
-        float s = 0.0f;
-        if (j < count) {
-            const float* P = a.partial[t] + j;
-            float acc[U];
+        // every wave; the sum of entry j is valid on wave 0's lane
+        auto sum_major = [&](const float* base, int S) {
+            float s = 0.0f;
+            if (j < count) {
+                const float* P = base + j;
+                float acc[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) acc[u] = 0.0f;
-            for (int q = wave; q < S; q += 4 * U) {  // wave w: splits w, w + 4, ...
-                float v[U];
+                for (int u = 0; u < U; ++u) acc[u] = 0.0f;
+                for (int q = wave; q < S; q += 4 * U) {  // wave w: splits w, w + 4, ...
+                    float v[U];
 #pragma unroll
-                for (int u = 0; u < U; ++u) v[u] = P[size_t(min(q + 4 * u, S - 1)) * stride];
+                    for (int u = 0; u < U; ++u) v[u] = P[size_t(min(q + 4 * u, S - 1)) * stride];
 #pragma unroll
-                for (int u = 0; u < U; ++u) acc[u] += q + 4 * u < S ? v[u] : 0.0f;
+                    for (int u = 0; u < U; ++u) acc[u] += q + 4 * u < S ? v[u] : 0.0f;
+                }
+                s = tree(acc);
             }
-            s = tree(acc);
-        }
-        part[wave][lane] = s;
-        __syncthreads();
-        if (wave == 0 && j < count) {
+            part[wave][lane] = s;
+            __syncthreads();
             const float sum = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+            __syncthreads();  // part is reused
+            return sum;
+        };
+        const float sum = sum_major(a.partial[t], S);
+        const float sum2 = two ? sum_major(a.partial2[t], a.splits2[t]) : 0.0f;
+        if (wave == 0 && j < count) {
             const int mrow = j / N1, n = j - mrow * N1;
             const int idx = mrow + M * n;
-            const float v = a.accumulate ? a.grad[t][idx] + sum : sum;
+            float v = a.accumulate ? a.grad[t][idx] + sum : sum;
+            if (two) v = v + sum2;
             if constexpr (UPDATE) rprop_update(o, t, idx, v);
             else a.grad[t][idx] = v;
         }
     } else {
         const int j = local * 4 + wave;
         if (j >= count) return;
-        const float* P = a.partial[t] + size_t(j) * S;
-        float acc[U];
+        // the sum of entry j, valid on lane 0
+        auto sum_minor = [&](const float* base, int S) {
+            const float* P = base + size_t(j) * S;
+            float acc[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) acc[u] = 0.0f;
-        for (int q = lane; q < S + 63; q += 64 * U) {  // lane l: splits l, l + 64, ...
-            float v[U];
+            for (int u = 0; u < U; ++u) acc[u] = 0.0f;
+            for (int q = lane; q < S + 63; q += 64 * U) {  // lane l: splits l, l + 64, ...
+                float v[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) v[u] = P[min(q + 64 * u, S - 1)];
+                for (int u = 0; u < U; ++u) v[u] = P[min(q + 64 * u, S - 1)];
 #pragma unroll
-            for (int u = 0; u < U; ++u) acc[u] += q + 64 * u < S ? v[u] : 0.0f;
-        }
-        float s = tree(acc);
-        for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+                for (int u = 0; u < U; ++u) acc[u] += q + 64 * u < S ? v[u] : 0.0f;
+            }
+            float s = tree(acc);
+            for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+            return s;
+        };
+        const float s = sum_minor(a.partial[t], S);
+        const float s2 = two ? sum_minor(a.partial2[t], a.splits2[t]) : 0.0f;
         if (lane == 0) {
             const int mrow = j / N1, n = j - mrow * N1;
             const int idx = mrow + M * n;
-            const float v = a.accumulate ? a.grad[t][idx] + s : s;
+            float v = a.accumulate ? a.grad[t][idx] + s : s;
+            if (two) v = v + s2;
             if constexpr (UPDATE) rprop_update(o, t, idx, v);
             else a.grad[t][idx] = v;
         }
@@ -895,9 +917,12 @@ __device__ __forceinline__ void wgrad_direct_tile(const WgradArgs& a, int t, int
     }
 }
 
-// Direct tiles and the thin transitions' roles in one launch; three
-// workgroups per CU (33 KB of LDS each).
-__global__ __launch_bounds__(256, 3) void wgrad_direct_kernel(WgradArgs a) {
+// Direct tiles and the thin transitions' roles in one launch (33 KB of LDS
+// per workgroup).
+#ifndef CPDE_WD_MIN_BLOCKS
+#define CPDE_WD_MIN_BLOCKS 3
+#endif
+__global__ __launch_bounds__(256, CPDE_WD_MIN_BLOCKS) void wgrad_direct_kernel(WgradArgs a) {
     __shared__ __attribute__((aligned(16))) float lds[kWdLds];
     static_assert(256 * 17 <= kWdLds, "thin-transition scratch exceeds the shared LDS");
     const int b = xcd_grouped(int(blockIdx.x), int(gridDim.x));
@@ -914,6 +939,20 @@ void launch_wgrad_grouped(Device& d, const WgradArgs& a, double flops) {
     if (a.direct) hipLaunchKernelGGL(wgrad_direct_kernel, a.block_begin[a.transitions], 256, 0, d.stream, a);
     else hipLaunchKernelGGL(wgrad_grouped_kernel, a.block_begin[a.transitions], 256, 0, d.stream, a);
     HIP_CHECK(hipGetLastError());
+}
+
+// Algorithmic bytes of a reduction launch (partials read, gradient read and
+// written, `extra` more floats per entry), and its grid: one more block when
+// it finishes costs or evaluates the graph.
+static double reduce_bytes(const ReduceArgs& a, int extra) {
+    double bytes = 0;
+    for (int t = 0; t < a.transitions; ++t)
+        bytes += 4.0 * (a.begin[t + 1] - a.begin[t]) * (a.splits[t] + a.splits2[t] + (a.accumulate ? 2 : 1) + extra);
+    for (int c = 0; c < a.costs; ++c) bytes += double(sizeof(CostStats)) * (a.cost_count[c] + 2);
+    return bytes;
+}
+static unsigned reduce_grid(const ReduceArgs& a) {
+    return unsigned(a.block_begin[a.transitions] + (a.costs || a.with_graph ? 1 : 0));
 }
 
 // The reduction of a gradient group followed by RPROP on the same
@@ -934,24 +973,14 @@ void launch_reduce_rprop(Device& d, const ReduceArgs& a, Net& net, int first) {
         o.NO[k] = net.neurons[t + 1];
         o.NI[k] = net.neurons[t];
     }
-    double bytes = 0;
-    for (int t = 0; t < a.transitions; ++t)
-        bytes += 4.0 * (a.begin[t + 1] - a.begin[t]) * (a.splits[t] + (a.accumulate ? 2 : 1) + 6);
-    if (a.cost_count) bytes += double(sizeof(CostStats)) * (a.cost_count + 2);
-    TraceScope trace(d, kTraceSplitReduce, bytes);
-    hipLaunchKernelGGL(reduce_rprop_kernel, a.block_begin[a.transitions] + (a.cost_count ? 1 : 0), 256, 0, d.stream, a,
-                       o);
+    TraceScope trace(d, kTraceSplitReduce, reduce_bytes(a, 6));
+    hipLaunchKernelGGL(reduce_rprop_kernel, reduce_grid(a), 256, 0, d.stream, a, o);
     HIP_CHECK(hipGetLastError());
 }
 
 void launch_reduce_grouped(Device& d, const ReduceArgs& a) {
-    double bytes = 0;
-    for (int t = 0; t < a.transitions; ++t)
-        bytes += 4.0 * (a.begin[t + 1] - a.begin[t]) * (a.splits[t] + (a.accumulate ? 2 : 1));
-    if (a.cost_count) bytes += double(sizeof(CostStats)) * (a.cost_count + 2);
-    TraceScope trace(d, kTraceSplitReduce, bytes);
-    hipLaunchKernelGGL(reduce_grouped_kernel, a.block_begin[a.transitions] + (a.cost_count ? 1 : 0), 256, 0, d.stream,
-                       a);
+    TraceScope trace(d, kTraceSplitReduce, reduce_bytes(a, 0));
+    hipLaunchKernelGGL(reduce_grouped_kernel, reduce_grid(a), 256, 0, d.stream, a);
     HIP_CHECK(hipGetLastError());
 }
 
@@ -1596,10 +1625,13 @@ __device__ void scalar_partials(int op, double a, double b, double v, double p, 
     }
 }
 
-__global__ void graph_kernel(const cpde_scalar_node* __restrict__ nodes, int count, int root,
-                             const CostStats* __restrict__ integrals, int leaves, double* values, double* adjoints,
-                             double* multipliers, int* active, cpde_graph_summary* summary, int gradient) {
-    if (blockIdx.x || threadIdx.x) return;
+__device__ void run_graph(const GraphLaunch& g) {
+    const cpde_scalar_node* __restrict__ nodes = g.nodes;
+    const CostStats* __restrict__ integrals = g.integrals;
+    double *values = g.values, *adjoints = g.adjoints, *multipliers = g.multipliers;
+    int* active = g.active;
+    cpde_graph_summary* summary = g.summary;
+    const int count = g.count, root = g.root, leaves = g.leaves;
     summary->bad_node = -1;
     summary->value = 0;
     for (int i = 0; i < leaves; ++i) multipliers[i] = 0;
@@ -1615,7 +1647,7 @@ __global__ void graph_kernel(const cpde_scalar_node* __restrict__ nodes, int cou
         if (!isfinite(values[i]) && summary->bad_node < 0) summary->bad_node = i;
     }
     summary->value = values[root];
-    if (!gradient || summary->bad_node >= 0) return;
+    if (!g.gradient || summary->bad_node >= 0) return;
     adjoints[root] = 1;
     for (int i = count - 1; i >= 0; --i) {
         const cpde_scalar_node n = nodes[i];
@@ -1634,11 +1666,20 @@ __global__ void graph_kernel(const cpde_scalar_node* __restrict__ nodes, int cou
         if (!isfinite(multipliers[i])) summary->bad_node = root;
 }
 
-void launch_graph(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,
-                  double* adjoints, double* multipliers, int* active, cpde_graph_summary* summary, bool gradient) {
-    launch_clear_fresh(d, leaves);
-    hipLaunchKernelGGL(graph_kernel, 1, 1, 0, d.stream, nodes, count, root, d.cost_totals, leaves, values, adjoints,
-                       multipliers, active, summary, int(gradient));
+__global__ void graph_kernel(GraphLaunch g) {
+    if (blockIdx.x || threadIdx.x) return;
+    run_graph(g);
+}
+
+GraphLaunch graph_launch(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,
+                         double* adjoints, double* multipliers, int* active, cpde_graph_summary* summary,
+                         bool gradient) {
+    return GraphLaunch{nodes, d.cost_totals, values, adjoints, multipliers, active, summary,
+                       count, root, leaves, int(gradient)};
+}
+
+void launch_graph(Device& d, const GraphLaunch& g) {
+    hipLaunchKernelGGL(graph_kernel, 1, 1, 0, d.stream, g);
     HIP_CHECK(hipGetLastError());
 }
 

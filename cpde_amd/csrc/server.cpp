@@ -698,6 +698,27 @@ private:
     void prepare_costs(NetRecord& n, const std::vector<uint64_t>& ids, uint64_t ni);
     void graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord& graph, bool backward);
     bool retained_last_ = false;  // the last graph pass kept forwards in stack sets
+
+    // An epoch's backward passes over one network share their reduction
+    // launches (cpde_gradients_defer: two passes per launch, the graph riding
+    // in it); CPDE_DEFER_REDUCE=0 reduces every pass in its own launch.
+    struct DeferredReductions {
+        cpde_device* dev = nullptr;
+        DeferredReductions(cpde_device* d, bool on) {
+            const char* v = std::getenv("CPDE_DEFER_REDUCE");
+            if (on && !(v && *v && std::atoi(v) == 0)) {
+                call(cpde_gradients_defer(d, 1));
+                dev = d;
+            }
+        }
+        void finish() {
+            if (dev) call(cpde_gradients_defer(dev, 0));
+            dev = nullptr;
+        }
+        ~DeferredReductions() {
+            if (dev) (void)cpde_gradients_defer(dev, 0);
+        }
+    };
     // epochs recorded and replayed (written to CPDE_REPLAY_FILE when the server ends)
     uint64_t recorded_ = 0, replayed_ = 0;
 
@@ -933,6 +954,7 @@ void Server::validate_costs(const std::vector<cpde_cost_stats>& cs, std::vector<
 // Server::graph_pass (cuda/cpde_server.cu:273-318).
 void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord& graph, bool backward) {
     call(cpde_costs_begin(dev_, int(ids.size())));
+    DeferredReductions deferred(dev_, backward);
     bool first = true;
     int reuse = -1, last_offset = 0;
     double best_work = -1;
@@ -999,6 +1021,7 @@ void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
                      Pass{true, false, multipliers + i, 0, int(i) == reuse ? last_offset : INT_MAX, false,
                           keep[i] ? 2 : 0, ids[i]});
     }
+    deferred.finish();
 }
 
 void Server::evaluate_costs(NetRecord& n, const std::vector<uint64_t>& ids, std::vector<double>& values,
@@ -1147,23 +1170,33 @@ void Server::gradient_epoch(EpochReplays& r, NetRecord& n, bool warm, bool colle
         if (++r.refusals > 2) r.on = false;
     }
     // stack sets bound per chunk, or a device that is tracing launches: no recording
-    if (!r.on || retained_last_ || cpde_capture_begin(dev_) != CPDE_OK) {
+    if (!r.on || retained_last_) {
+        r.on = false;
+        return work();
+    }
+    if (cpde_capture_begin(dev_) != CPDE_OK) {
+        std::cerr << "cpde_server: epochs not recorded: " << cpde_last_error() << std::endl;
         r.on = false;
         return work();
     }
     bool recorded = true;
     try {
         work();
-    } catch (...) {
+    } catch (const std::exception& e) {
+        std::cerr << "cpde_server: epoch not recorded: " << e.what() << std::endl;
         recorded = false;
     }
     cpde_replay* made = nullptr;
-    if (recorded && cpde_capture_end(dev_, 1, &made) == CPDE_OK && made) {
-        r.cache[key] = made;
-        ++recorded_;
-        return;
+    if (recorded) {
+        if (cpde_capture_end(dev_, 1, &made) == CPDE_OK && made) {
+            r.cache[key] = made;
+            ++recorded_;
+            return;
+        }
+        std::cerr << "cpde_server: epoch not recorded: " << cpde_last_error() << std::endl;
+    } else {
+        (void)cpde_capture_end(dev_, 0, nullptr);
     }
-    if (!recorded) (void)cpde_capture_end(dev_, 0, nullptr);
     // nothing that was recorded ran: the chunks it activated are not in place
     n.loaded = NetRecord::Loaded{};
     n.inputs.clear();
@@ -1246,9 +1279,11 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
             if (graph) graph_pass(n, ids, *graph, true);
             else {
                 call(cpde_costs_begin(dev_, int(ids.size())));
+                DeferredReductions deferred(dev_, true);
                 bool first = true;
                 for (size_t i = 0; i < ids.size(); ++i)
                     pass(n, cost(ids[i]), int(i), first, Pass{true, collect, nullptr, 0, INT_MAX, false});
+                deferred.finish();
             }
             call(cpde_inspect_gradients(n.net));
         });

@@ -64,6 +64,7 @@ SIGNATURES = {
     'cpde_activate': (i32, [vp, vp, i32, vp, i32, i32]),
     'cpde_forward': (i32, [vp]),
     'cpde_output': (i32, [vp, vp, i32, vp, i32, i32]),
+    'cpde_gradients_defer': (i32, [vp, i32]),
     'cpde_costs_begin': (i32, [vp, i32]),
     'cpde_cost_matching': (i32, [vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32]),
     'cpde_cost_polynomial': (i32, [vp, vp, i32, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32]),

@@ -167,6 +167,17 @@ int cpde_output(cpde_plan* plan, float* dest, int dest_width, const int* rows, i
 
 /* Reset cost slots [0, costs) (Workspace::begin, cuda/reduction_kernels.cuh:149-152). */
 int cpde_costs_begin(cpde_device* dev, int costs);
+/* Deferred gradient reductions.  No counterpart in the reference, whose
+ * backward passes each end in their own accumulating GEMMs.  While on, the
+ * reduction that ends a backward pass (cpde_backward, cpde_epoch_matching,
+ * cpde_epoch_expression) waits: the next backward pass over the same network
+ * that accumulates onto it joins it, and the two are reduced in one launch,
+ * bit for bit as two launches in turn; cpde_graph_execute then rides in that
+ * launch after its cost finishes.  Every call that reads gradients, costs or
+ * the device (downloads, statistics, optimizers, synchronisation, another
+ * cost into a slot the waiting launch finishes) launches it first, and so does
+ * turning deferral off. */
+int cpde_gradients_defer(cpde_device* dev, int on);
 /* Array-matching squared loss (cuda/cost_kernels.cuh:6-35) fused with its
  * deterministic reduction into cost slot cost_index.  target: device wire data
  * [target_rows_total][target_width][n_out]; target_rows, weights: device. */

@@ -1,0 +1,81 @@
+"""Backward passes that share a reduction launch (the protocol server defers
+each pass's gradient reduction so that the next pass over the same network
+joins it, and the scalar graph rides in it) against one launch per pass
+(CPDE_DEFER_REDUCE=0): every frame and the final state byte for byte.  Cases:
+the Poisson disk graph (two leaves with known multipliers), the nested
+variation graph (value-dependent multipliers, three chunks per leaf, both with
+the one-pass epochs and with separate launches), and two expression costs
+trained without a graph."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from cpde_amd import wire, workloads as W
+from cpde_amd.build import SERVER
+
+pytestmark = pytest.mark.gpu
+
+
+def canonical(events):
+    out = []
+    for e in events:
+        item = []
+        for k in sorted(e):
+            v = e[k]
+            if isinstance(v, np.ndarray):
+                v = (v.dtype.str, v.shape, v.tobytes())
+            elif isinstance(v, (list, tuple)):
+                v = tuple(x.tobytes() if isinstance(x, np.ndarray) else x for x in v)
+            item.append((k, v))
+        out.append(tuple(item))
+    return out
+
+
+def run(env, body, trace):
+    s = wire.Session(SERVER, env=dict(os.environ, CPDE_TRACE_FILE=str(trace), **env))
+    try:
+        result = body(s)
+    finally:
+        s.close()
+    return result, json.loads(trace.read_text())
+
+
+def poisson(s):
+    pw = W.PoissonWorkload(radial=16, angular=16, boundary=64)
+    ids = pw.upload(s)
+    value, grads = s.graph_eval(ids['net'], ids['costs'], pw.graph(), gradient=True)
+    res = s.train(ids['net'], ids['costs'], 6, method=0, fresh=1, log=1, graph=pw.graph())
+    return value, [g.tobytes() for g in grads], canonical(res['events']), s.snapshot(ids['net'])
+
+
+def nested(s):
+    vw = W.VariationWorkload()
+    n, _, costs = vw.upload(s)
+    leaves = [costs['a'], costs['correction']]
+    value, grads = s.graph_eval(n, leaves, vw.nested_graph(), gradient=True)
+    res = s.train(n, leaves, 5, method=0, fresh=1, log=1, graph=vw.nested_graph())
+    return value, [g.tobytes() for g in grads], canonical(res['events']), s.snapshot(n)
+
+
+def two_costs(s):
+    vw = W.VariationWorkload()
+    n, _, costs = vw.upload(s)
+    res = s.train(n, [costs['a'], costs['free']], 5, method=0, fresh=1, log=1)
+    return canonical(res['events']), s.snapshot(n)
+
+
+@pytest.mark.parametrize('name,body,env', [
+    ('poisson', poisson, {}),
+    ('nested', nested, {}),
+    ('nested-separate', nested, {'CPDE_ONE_PASS': '0'}),
+    ('two-costs', two_costs, {}),
+])
+def test_shared_reductions_match_one_per_pass(tmp_path, name, body, env):
+    shared, t1 = run(env, body, tmp_path / 'shared.json')
+    alone, t0 = run(dict(env, CPDE_DEFER_REDUCE='0'), body, tmp_path / 'alone.json')
+    launches = [t['split_reduce'][0] for t in (t1, t0)]
+    print(f'[result] {name}: reduction launches shared {launches[0]} alone {launches[1]}', flush=True)
+    assert shared == alone
+    assert launches[0] < launches[1]
