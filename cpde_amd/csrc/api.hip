@@ -50,9 +50,18 @@ void check_hip(hipError_t status, const char* what, const char* file, int line) 
     throw device_error(buf);
 }
 
-// Launch the waiting gradient reduction, if any.
+// Launch the waiting weight-gradient launch, if any; the reduction may wait on.
+void flush_wgrad(Device& d) {
+    Device::PendingReduce& w = d.waiting;
+    if (!w.open || !w.wgrad) return;
+    w.wgrad = false;
+    launch_wgrad_grouped(d, w.wa, w.flops);
+}
+
+// Launch the waiting gradient reduction, if any, after its weight gradient.
 void flush_reduce(Device& d) {
     if (!d.waiting.open) return;
+    flush_wgrad(d);
     d.waiting.open = false;
     d.waiting.partial_end = 0;
     launch_reduce_grouped(d, d.waiting.ra);
@@ -537,8 +546,6 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
     }
     g.wa.direct = direct ? 1 : 0;
     const int tile_splits = splits_for(total_tiles);
-    g.wa.K = K;
-    g.wa.R = p.rows;
     g.wa.block_begin[0] = 0;
     g.ra.accumulate = accumulate ? 1 : 0;
     g.ra.transitions = T;
@@ -558,6 +565,8 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
             s = (K + chunk - 1) / chunk;
             g.wa.M[w] = M;
             g.wa.N[w] = N;
+            g.wa.K[w] = K;
+            g.wa.R[w] = p.rows;
             g.wa.kchunk[w] = chunk;
             g.wa.tile[w] = tile_of(k);
             g.wa.block_begin[w + 1] = g.wa.block_begin[w] + tiles * s;
@@ -663,22 +672,48 @@ static bool joins(const Device::PendingReduce& w, const GradientPlan& g) {
 // (transitions [first, first + count) of `update`), whose gradients it
 // completes; the caller flips the active buffers once every group is done.
 // Otherwise, while the device defers reductions (cpde_gradients_defer), a
-// reduction of partials in the network's own buffer waits: as the second pass
-// of a waiting one when it joins it, else as the new waiting one.
-static void run_gradients(Device& d, const GradientPlan& g, Net* update = nullptr, int first = 0) {
-    if (g.wa.transitions > 0) launch_wgrad_grouped(d, g.wa, g.flops);
-    if (update) {
+// pass's launches over partials in the network's own buffer wait: as the
+// second pass of the waiting ones when it joins them (its weight-gradient
+// tiles appended to the waiting launch's), else as the new waiting ones.
+static void run_gradients(Device& d, const GradientPlan& g, Net* update = nullptr, int first = 0,
+                          const Plan* plan = nullptr) {
+    if (update || !d.defer || !g.net) {
         flush_reduce(d);
-        launch_reduce_rprop(d, g.ra, *update, first);
-        return;
-    }
-    if (!d.defer || !g.net) {
-        flush_reduce(d);
-        launch_reduce_grouped(d, g.ra);
+        if (g.wa.transitions > 0) launch_wgrad_grouped(d, g.wa, g.flops);
+        if (update) launch_reduce_rprop(d, g.ra, *update, first);
+        else launch_reduce_grouped(d, g.ra);
         return;
     }
     Device::PendingReduce& w = d.waiting;
-    if (joins(w, g)) {
+    const bool tiles_fit = g.wa.transitions == 0 || !w.wgrad ||
+                           (w.wa.direct == g.wa.direct && w.wa.transitions + g.wa.transitions <= kMaxTransitions);
+    if (joins(w, g) && tiles_fit) {
+        if (g.wa.transitions > 0) {
+            if (!w.wgrad) {  // the waiting pass's tiles already ran
+                w.wgrad = true;
+                w.wa = g.wa;
+                w.flops = g.flops;
+            } else {
+                WgradArgs& a = w.wa;
+                const WgradArgs& b = g.wa;
+                const int base = a.block_begin[a.transitions];
+                for (int k = 0; k < b.transitions; ++k) {
+                    const int i = a.transitions + k;
+                    a.G[i] = b.G[k];
+                    a.Y[i] = b.Y[k];
+                    a.partial[i] = b.partial[k];
+                    a.M[i] = b.M[k];
+                    a.N[i] = b.N[k];
+                    a.K[i] = b.K[k];
+                    a.R[i] = b.R[k];
+                    a.kchunk[i] = b.kchunk[k];
+                    a.tile[i] = b.tile[k];
+                    a.block_begin[i + 1] = base + b.block_begin[k + 1];
+                }
+                a.transitions += b.transitions;
+                w.flops += g.flops;
+            }
+        }
         for (int k = 0; k < g.ra.transitions; ++k) {
             w.ra.partial2[k] = g.ra.partial[k];
             w.ra.splits2[k] = g.ra.splits[k];
@@ -699,6 +734,10 @@ static void run_gradients(Device& d, const GradientPlan& g, Net* update = nullpt
     w.net = g.net;
     w.ra = g.ra;
     w.partial_end = g.partial_end;
+    w.wgrad = g.wa.transitions > 0;
+    w.wa = g.wa;
+    w.flops = g.flops;
+    w.plan = plan;
 }
 
 // Launch the waiting reduction when it reads `records` (which the caller is
@@ -784,6 +823,53 @@ static CostStats* epoch_records(Plan& p) {
     return p.epoch_partials + (p.epoch_turn ? p.epoch_capacity : 0);
 }
 
+// A plan's own layer stacks (Plan::own_*), shaped as its part of the arena:
+// allocated on first use, outside captures, for plans of at most 256 MB of
+// stacks.
+static bool own_stacks(Plan& p) {
+    if (!p.own_z.empty()) return true;
+    const Net& n = *p.net;
+    if (n.dev->capturing) return false;
+    double bytes = 0;
+    for (int l = 0; l < n.layers; ++l)
+        bytes += 4.0 * p.columns() * n.neurons[l] * (1 + (n.linear[l] ? 0 : 1) + (l > 0 ? 1 : 0));
+    if (bytes > 256.0 * 1048576.0) return false;
+    std::vector<float*> z(n.layers, nullptr), y(n.layers, nullptr), g(n.layers, nullptr);
+    try {
+        for (int l = 0; l < n.layers; ++l) {
+            const size_t need = p.columns() * n.neurons[l];
+            HIP_CHECK(hipMalloc(&z[l], need * sizeof(float)));
+            if (!n.linear[l]) HIP_CHECK(hipMalloc(&y[l], need * sizeof(float)));
+            if (l > 0) HIP_CHECK(hipMalloc(&g[l], need * sizeof(float)));
+        }
+    } catch (...) {
+        for (auto* v : {&z, &y, &g})
+            for (float* q : *v) (void)hipFree(q);
+        throw;
+    }
+    p.own_z = z;
+    p.own_y = y;
+    p.own_g = g;
+    return true;
+}
+
+// The plan's own stacks in place of the network's arena for one pass.
+struct OwnStacks {
+    Net& n;
+    Plan& p;
+    bool on;
+    OwnStacks(Net& net, Plan& plan, bool swapped) : n(net), p(plan), on(swapped) {}
+    void swap() {
+        std::swap(n.z, p.own_z);
+        std::swap(n.y, p.own_y);
+        std::swap(n.g, p.own_g);
+        on = !on;
+    }
+    ~OwnStacks() {
+        if (on) swap();
+    }
+};
+
 // Forward, cost and backward of one chunk in one network-fused launch of
 // `kernel` (arguments: the network, `cost_args`, the chunk width), then the
 // cost's fixed-order finish and the weight-gradient contraction.  `records`
@@ -799,6 +885,18 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostS
     const double cols = double(p.columns());
     const int blocks = epoch_blocks(p);
     flush_if_reads(d, records, cost_index);  // the kernel rewrites this plan's records
+    // Behind a waiting weight gradient that reads another plan's stacks in the
+    // arena, this pass runs on stacks of its own, so that both passes' tiles
+    // go out in one launch; a waiting gradient this pass would overwrite goes
+    // out now.
+    OwnStacks own(n, p, false);
+    {
+        const Device::PendingReduce& w = d.waiting;
+        if (w.open && w.wgrad && w.net == &n) {
+            if (!w.ra.second && !space.base && !update && w.plan != &p && !n.bound && own_stacks(p)) own.swap();
+            else flush_wgrad(d);
+        }
+    }
     NetArgsHost a = net_args(p);
     GradientPlan g = network_gradients(p, blocks, accumulate, space, a);
     // the backward half reads the row-major weight copies of every hidden
@@ -822,7 +920,7 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostS
     } else {
         launch_finish_cost(d, records, blocks, cost_index);
     }
-    run_gradients(d, g, update ? &n : nullptr, 0);
+    run_gradients(d, g, update ? &n : nullptr, 0, &p);
     if (update) rprop_done(n);
 }
 
@@ -857,7 +955,8 @@ static void weight_gradients(Plan& p, bool accumulate) {
     const std::vector<int> none(T, 0);
     for (int first = 0; first < T; first += kMaxTransitions)
         run_gradients(*p.net->dev,
-                      plan_gradients(p, accumulate, none.data(), first, std::min(kMaxTransitions, T - first)));
+                      plan_gradients(p, accumulate, none.data(), first, std::min(kMaxTransitions, T - first)),
+                      nullptr, 0, &p);
 }
 
 static void fused_backward(Plan& p, bool accumulate) {
@@ -878,7 +977,7 @@ static void fused_backward(Plan& p, bool accumulate) {
             TraceScope trace(d, kTraceNetworkBackward, flops);
             launch_module(d, fm.network_backward, unsigned(blocks), 1, args, unsigned(fm.net_threads));
         }
-        run_gradients(d, g);
+        run_gradients(d, g, nullptr, 0, &p);
         return;
     }
     {
@@ -1161,6 +1260,8 @@ int cpde_plan_destroy(cpde_plan* plan) {
         (void)hipFree(plan->dev_rows);
         (void)hipFree(plan->epoch_partials);
         (void)hipFree(plan->input);
+        for (auto* v : {&plan->own_z, &plan->own_y, &plan->own_g})
+            for (float* q : *v) (void)hipFree(q);
         delete plan;
     });
 }
@@ -1197,6 +1298,7 @@ int cpde_stacks_create(cpde_plan* plan, cpde_stacks** out) {
 int cpde_plan_bind(cpde_plan* plan, cpde_stacks* stacks) {
     return guarded([&] {
         require(plan, "null argument");
+        flush_wgrad(*plan->net->dev);  // this call writes stacks a waiting launch may read
         Net& n = *plan->net;
         if (n.bound) {  // unbind whatever is bound: the set goes back to its own pointers
             Stacks& b = *n.bound;
@@ -1260,6 +1362,7 @@ int cpde_plan_stack_scale(cpde_plan* plan, int layer, int kind, float* row_facto
 // ---- hot path ------------------------------------------------------------------------------
 int cpde_activate(cpde_plan* plan, const float* data, int data_width, const int* rows, int offset, int valid) {
     return guarded([&] {
+        flush_wgrad(*plan->net->dev);  // this call writes stacks a waiting launch may read
         Net& n = *plan->net;
         Device& d = *n.dev;
         require(valid >= 0 && valid <= plan->width && offset >= 0 && offset + valid <= data_width,
@@ -1272,6 +1375,7 @@ int cpde_activate(cpde_plan* plan, const float* data, int data_width, const int*
 
 int cpde_forward(cpde_plan* plan) {
     return guarded([&] {
+        flush_wgrad(*plan->net->dev);  // this call writes stacks a waiting launch may read
         Net& n = *plan->net;
         Device& d = *n.dev;
         if (plan->fused) {
@@ -1318,6 +1422,7 @@ int cpde_cost_matching(cpde_plan* plan, const float* target, int target_width, c
                        const float* weights, int weight_samples, int offset, int valid, int cost_index, int collect,
                        int gradient) {
     return guarded([&] {
+        flush_wgrad(*plan->net->dev);  // this call writes stacks a waiting launch may read
         flush_if_reads(*plan->net->dev, nullptr, cost_index);
         Net& n = *plan->net;
         Device& d = *n.dev;
@@ -1407,6 +1512,7 @@ int cpde_cost_polynomial(cpde_plan* plan, const cpde_poly_term* terms, int term_
                          const float* rhs, const float* weights, int equations, int samples, int offset, int valid,
                          int cost_index, int collect, int gradient) {
     return guarded([&] {
+        flush_wgrad(*plan->net->dev);  // this call writes stacks a waiting launch may read
         flush_if_reads(*plan->net->dev, nullptr, cost_index);
         Net& n = *plan->net;
         Device& d = *n.dev;
@@ -1420,6 +1526,7 @@ int cpde_cost_polynomial(cpde_plan* plan, const cpde_poly_term* terms, int term_
 
 int cpde_scale_adjoint(cpde_plan* plan, const double* multiplier) {
     return guarded([&] {
+        flush_wgrad(*plan->net->dev);  // this call writes stacks a waiting launch may read
         Net& n = *plan->net;
         launch_scale_adjoint(*n.dev, *plan, n.g[n.layers - 1], multiplier);
     });
@@ -1427,6 +1534,7 @@ int cpde_scale_adjoint(cpde_plan* plan, const double* multiplier) {
 
 int cpde_backward(cpde_plan* plan, int accumulate) {
     return guarded([&] {
+        flush_wgrad(*plan->net->dev);  // this call writes stacks a waiting launch may read
         Net& n = *plan->net;
         Device& d = *n.dev;
         require(plan->backward, "plan has no adjoint storage");
@@ -1599,6 +1707,7 @@ int cpde_cost_expression(cpde_plan* plan, cpde_program* program, const double* f
                          const double* quadrature_weights, int samples, int offset, int valid,
                          const double* multiplier, void* scratch, int cost_index, int collect, int gradient) {
     return guarded([&] {
+        flush_wgrad(*plan->net->dev);  // this call writes stacks a waiting launch may read
         flush_if_reads(*plan->net->dev, nullptr, cost_index);
         Net& n = *plan->net;
         Device& d = *n.dev;

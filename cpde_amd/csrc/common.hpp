@@ -127,6 +127,10 @@ struct Plan {
     int epoch_capacity = 0, epoch_turn = 0;
     // one-pass expression epochs of this plan, by program id
     std::vector<std::pair<uint64_t, std::shared_ptr<ExpressionEpoch>>> expression_epochs;
+    // layer stacks of its own, in place of the network's arena while a
+    // one-pass epoch runs behind a waiting weight gradient of another plan
+    // (cpde_gradients_defer); allocated on first such use
+    std::vector<float*> own_z, own_y, own_g;
     size_t columns() const { return size_t(rows) * size_t(width); }
 };
 
@@ -139,6 +143,18 @@ struct Program {
     uint64_t id = 0;     // unique per compiled program
 };
 
+// Grouped weight-gradient launch (one entry per transition).
+struct WgradArgs {
+    const float* G[kMaxTransitions];
+    const float* Y[kMaxTransitions];
+    float* partial[kMaxTransitions];
+    int M[kMaxTransitions], N[kMaxTransitions], kchunk[kMaxTransitions];
+    int tile[kMaxTransitions];  // 128, or 64 when both sides are at most 64
+    int block_begin[kMaxTransitions + 1];
+    int K[kMaxTransitions], R[kMaxTransitions];  // columns and rows per point of each entry's pass
+    int transitions;
+    int direct;  // 1: 64x64 tiles fed straight from global memory (wgrad_direct_kernel)
+};
 // The scalar cost graph's evaluation (cost_graph::execute) as one lane runs it.
 struct GraphLaunch {
     const cpde_scalar_node* nodes;
@@ -260,26 +276,25 @@ struct Device {
         Net* net = nullptr;
         ReduceArgs ra{};
         size_t partial_end = 0;
+        // the weight-gradient launch waits too, before the reduction; it reads
+        // the stacks its passes wrote (`plan`'s, in the network's arena, for
+        // the first)
+        bool wgrad = false;
+        WgradArgs wa{};
+        double flops = 0;
+        const Plan* plan = nullptr;
     } waiting;
 };
 
 // Synchronise the device's stream; refused while a capture is open (the
 // caller allocates, frees or reads back, which a recording cannot hold).
 void sync_stream(Device& d, int site = 0);
-// Launch the reduction that cpde_gradients_defer keeps waiting, if any.
+// Launch the reduction that cpde_gradients_defer keeps waiting, if any (its
+// weight-gradient launch first).
 void flush_reduce(Device& d);
+// Launch only the waiting weight-gradient launch (the reduction may wait on).
+void flush_wgrad(Device& d);
 
-// Grouped weight-gradient launch (one entry per transition).
-struct WgradArgs {
-    const float* G[kMaxTransitions];
-    const float* Y[kMaxTransitions];
-    float* partial[kMaxTransitions];
-    int M[kMaxTransitions], N[kMaxTransitions], kchunk[kMaxTransitions];
-    int tile[kMaxTransitions];  // 128, or 64 when both sides are at most 64
-    int block_begin[kMaxTransitions + 1];
-    int transitions, K, R;
-    int direct;  // 1: 64x64 tiles fed straight from global memory (wgrad_direct_kernel)
-};
 // Blocks reduce_grouped_kernel uses for a transition of `count` entries.
 inline int reduce_blocks(int count, bool split_minor) { return split_minor ? (count + 3) / 4 : (count + 63) / 64; }
 

@@ -330,7 +330,7 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local,
     typedef float Chunk[kWgKC][LD];
     Chunk* As = reinterpret_cast<Chunk*>(lds);
     Chunk* Bs = reinterpret_cast<Chunk*>(lds + 2 * kWgKC * LD);
-    const int M = a.M[t], N = a.N[t], K = a.K;
+    const int M = a.M[t], N = a.N[t], K = a.K[t];
     const int tiles_m = (M + TILE - 1) / TILE, tiles_n = (N + TILE - 1) / TILE;
     const int tile = local % (tiles_m * tiles_n), split = local / (tiles_m * tiles_n);
     const int m0 = (tile % tiles_m) * TILE, n0 = (tile / tiles_m) * TILE;
@@ -372,7 +372,7 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local,
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[x][y][v] = 0.0f;
     float bias = 0.0f;  // tile column 0 blocks: thread tid < TILE sums G[k][m0+tid] over value rows
-    int value_col = (kbegin + a.R - 1) / a.R * a.R;  // next value-row column
+    int value_col = (kbegin + a.R[t] - 1) / a.R[t] * a.R[t];  // next value-row column
     const int wm = (TILE / 2) * (wave & 1), wn = (TILE / 2) * (wave >> 1);
     float4 ga[J], ya[J];
     stage(ga, ya, kbegin);
@@ -402,7 +402,7 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local,
         }
         if (n0 == 0 && tid < TILE) {
             const int stop = min(kend, k0 + kWgKC);
-            for (; value_col < stop; value_col += a.R) bias += As[buf][value_col - k0][tid];
+            for (; value_col < stop; value_col += a.R[t]) bias += As[buf][value_col - k0][tid];
         }
         buf ^= 1;
     }
@@ -420,7 +420,7 @@ __device__ __forceinline__ void wgrad_tile(const WgradArgs& a, int t, int local,
 }
 
 __device__ __forceinline__ void wgrad_thin(const WgradArgs& a, int t, int split, float* red) {
-    const int M = a.M[t], N = a.N[t], K = a.K, R = a.R;
+    const int M = a.M[t], N = a.N[t], K = a.K[t], R = a.R[t];
     const int kbegin = split * a.kchunk[t], kend = min(K, kbegin + a.kchunk[t]);
     const float* __restrict__ G = a.G[t];
     const float* __restrict__ Y = a.Y[t];
@@ -828,7 +828,7 @@ __device__ __forceinline__ void wd_accumulate(floatx4 (&acc)[4][4], const float*
 
 template <bool VEC>
 __device__ __forceinline__ void wgrad_direct_tile(const WgradArgs& a, int t, int local, float* lds) {
-    const int M = a.M[t], N = a.N[t], K = a.K, R = a.R;
+    const int M = a.M[t], N = a.N[t], K = a.K[t], R = a.R[t];
     const int tiles_m = (M + 63) / 64, tiles_n = (N + 63) / 64;
     const int tile = local % (tiles_m * tiles_n), split = local / (tiles_m * tiles_n);
     const int m0 = (tile % tiles_m) * 64, n0 = (tile / tiles_m) * 64;
