@@ -3,9 +3,9 @@ each pass's gradient reduction so that the next pass over the same network
 joins it, and the scalar graph rides in it) against one launch per pass
 (CPDE_DEFER_REDUCE=0): every frame and the final state byte for byte.  Cases:
 the Poisson disk graph (two leaves with known multipliers), the nested
-variation graph (value-dependent multipliers, three chunks per leaf, both with
-the one-pass epochs and with separate launches), and two expression costs
-trained without a graph."""
+variation graph (value-dependent multipliers, three chunks per leaf: with the
+one-pass epochs, with separate network launches, and on the table-driven and
+layer-fused kernels), and two expression costs trained without a graph."""
 import json
 import os
 
@@ -70,6 +70,8 @@ def two_costs(s):
     ('poisson', poisson, {}),
     ('nested', nested, {}),
     ('nested-separate', nested, {'CPDE_ONE_PASS': '0'}),
+    ('nested-table', nested, {'CPDE_FUSED': '0'}),             # table-driven kernels
+    ('nested-layer', nested, {'CPDE_FUSED': '1'}),             # layer-fused kernels
     ('two-costs', two_costs, {}),
 ])
 def test_shared_reductions_match_one_per_pass(tmp_path, name, body, env):
