@@ -59,11 +59,10 @@ CPU_SAMPLE_MACS = 3.0e9
 # read, 268,435,456 B / 262,144 KiB written.
 COPY_SCALE = (268435456 / (131084.475 * 1024), 268435456 / (262144 * 1024))
 TRAFFIC_KIB = {
-    'fourier_fit_order6': {'network_epoch': (21271.59, 134691.65), 'gemm_wgrad': (30998.85, 7740.46)},
-    'fourier_large_order6': {'network_backward': (4986304.06, 8850894.45), 'network_forward': (429759.76, 14688003.15),
-                             'gemm_wgrad': (7840131.41, 35119.54)},
+    'fourier_fit_order6': {'network_epoch': (21281.36, 134692.67), 'gemm_wgrad': (31740.74, 4077.5)},
+    'fourier_large_order6': {'network_backward': (4980058.93, 8845747.75), 'network_forward': (424046.03, 14688002.52),
+                             'gemm_wgrad': (9044857.01, 34791.09)},
 }
-
 
 @dataclass
 class Spec:

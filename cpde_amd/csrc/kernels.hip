@@ -778,27 +778,43 @@ __device__ __forceinline__ void wd_accumulate(floatx4 (&acc)[4][4], const float*
             yo += ystep;
         }
         int s0 = 0;
-#pragma unroll 1
-        for (; s0 + 2 * kWdDepth <= full; s0 += kWdDepth) {
-            // the next kWdDepth steps' loads go out first (kept at the top of
-            // the body: scheduled later, their latency would fall on the next
-            // iteration's first products)
-            float4 gn[kWdDepth], yn4[kWdDepth];
+        // two register sets in turn (no copies between them): each half of
+        // the body sends the other set's next kWdDepth steps of loads out
+        // before its own products, so a set's loads stay in flight across the
+        // other set's products
+        float4 gn[kWdDepth], yn4[kWdDepth];
+        auto fetch = [&](float4 (&gs)[kWdDepth], float4 (&ys)[kWdDepth]) {
 #pragma unroll
             for (int d = 0; d < kWdDepth; ++d) {
-                gn[d] = wd_load<VEC, MASK>(G, go, gm, M);
-                yn4[d] = wd_load<VEC, MASK>(Y, yo, yn, N);
+                gs[d] = wd_load<VEC, MASK>(G, go, gm, M);
+                ys[d] = wd_load<VEC, MASK>(Y, yo, yn, N);
                 go += gstep;
                 yo += ystep;
             }
-            __builtin_amdgcn_sched_barrier(0);
+        };
+        auto products = [&](const float4 (&gs)[kWdDepth], const float4 (&ys)[kWdDepth]) {
 #pragma unroll
-            for (int d = 0; d < kWdDepth; ++d) mma(gb[d], yb[d]);
+            for (int d = 0; d < kWdDepth; ++d) mma(gs[d], ys[d]);
+        };
+#pragma unroll 1
+        for (; s0 + 3 * kWdDepth <= full; s0 += 2 * kWdDepth) {
+            fetch(gn, yn4);
+            __builtin_amdgcn_sched_barrier(0);
+            products(gb, yb);
+            fetch(gb, yb);
+            __builtin_amdgcn_sched_barrier(0);
+            products(gn, yn4);
+        }
+        if (s0 + 2 * kWdDepth <= full) {  // one more set of steps fits before the tail
+            fetch(gn, yn4);
+            __builtin_amdgcn_sched_barrier(0);
+            products(gb, yb);
 #pragma unroll
             for (int d = 0; d < kWdDepth; ++d) {
                 gb[d] = gn[d];
                 yb[d] = yn4[d];
             }
+            s0 += kWdDepth;
         }
         // steps s0 .. s0 + kWdDepth - 1 are loaded; fewer than kWdDepth full steps follow
 #pragma unroll
