@@ -304,16 +304,19 @@ def run_server(wl, steps, warmup, trace_steps, settle_ms):
 
 
 def other_workloads(names, settle_ms):
-    """The larger configurations, a few epochs each (same step, same clock
-    settling), so that their roofline fractions come from this run too."""
+    """The other configurations (same step, same clock settling; the larger
+    ones for a few epochs), so that their roofline fractions come from this
+    run too."""
     out = {}
     for name in names:
         spec = WORKLOADS[name]
         wl = spec.make()
-        ms, device_ms, _, _, report, settled = run_direct(wl, spec.steps, spec.warmup, spec.trace_steps, settle_ms)
+        run = run_server if spec.server else run_direct
+        ms, device_ms, _, _, report, settled = run(wl, spec.steps, spec.warmup, spec.trace_steps, settle_ms)
         t_roof = wl.flops_per_epoch() / PEAK_FP32_MFMA + wl.bytes_per_epoch() / PEAK_HBM
         out[name] = {'config': describe(wl, name), 'steps': spec.steps, 'warmup': spec.warmup,
-                     'ms_per_step': round(ms, 4), 'device_ms_per_step': round(device_ms, 4),
+                     'ms_per_step': round(ms, 4),
+                     'device_ms_per_step': None if device_ms is None else round(device_ms, 4),
                      'value': round(point_rows(wl) / (ms / 1e3), 1), 'unit': 'points·derivs/s',
                      'epoch_roofline': {'t_roof_ms': round(t_roof * 1e3, 3), 'frac': round(t_roof / (ms / 1e3), 4)},
                      'roofline': roofline(report, name), 'clock_settle': settled,
@@ -390,7 +393,8 @@ def main(argv=None):
     if not args.no_cpu_baseline:
         out['cpu_baseline'] = cpu_baseline(wl)
     if args.workload == 'fourier_fit_order6' and not args.no_other_workloads:
-        out['other_workloads'] = other_workloads(['fourier_3d_order4', 'fourier_large_order6'], args.settle_ms)
+        out['other_workloads'] = other_workloads(['fourier_fit_order2', 'poisson_disk_order2', 'fourier_3d_order4',
+                                                  'fourier_large_order6'], args.settle_ms)
     print(json.dumps(out), flush=True)
     return 0
 
