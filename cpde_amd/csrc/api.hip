@@ -323,9 +323,14 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
     // CUs it was slower (order 4, 365 workgroups: 0.0700 -> 0.0742).
     if (width > 0 && rows <= 16 && npb > 1 && (width + npb - 1) / npb <= compute_units) t.net_threads = 512;
     t.net_threads = env_int("CPDE_NET_THREADS", t.net_threads) == 512 ? 512 : 256;
-    // a composition split over lanes pays off while a point's rows fit one
-    // matrix-core tile; with two tiles (R > 32) whole compositions per lane are faster
-    t.max_split = std::max(1, env_int("CPDE_NET_SPLIT", rows > 32 ? 1 : t.max_split));
+    // Whole compositions per lane, except for several-point workgroups of up
+    // to 32 rows, where a split over lanes fills the waves: on the Taylor-scaled
+    // rows of one point per workgroup the split only adds lanes that repeat the
+    // jet (2->128^4->1 over 729 points, ms per epoch with a split of two against
+    // none: order 5 (21 rows) 0.0936 / 0.0904, order 6 (28 rows) 0.1036 /
+    // 0.0992; orders 1-4, several points per workgroup, within 0.3 %).
+    const bool whole = rows > 32 || (rows > 16 && t.net_points_per_block == 1);
+    t.max_split = std::max(1, env_int("CPDE_NET_SPLIT", whole ? 1 : t.max_split));
     t.max_split_adjoint = std::max(1, env_int("CPDE_NET_SPLIT_ADJOINT", t.max_split_adjoint));
     t.forward_blocks = std::max(1, env_int("CPDE_NET_FWD_OCC", t.forward_blocks));
     t.backward_blocks = std::max(1, env_int("CPDE_NET_BWD_OCC", t.backward_blocks));

@@ -276,6 +276,32 @@ def test_network_kernels_with_eight_waves(device, monkeypatch, order, neurons, p
     run.close()
 
 
+@pytest.mark.parametrize('order,neurons,points,split', [
+    (6, [2, 128, 128, 1], 61, '2'),   # 28 rows: the scaled forward split over mirror lanes
+    (5, [2, 64, 48, 32, 1], 40, '2'),
+    (3, [2, 64, 64, 1], 300, '1'),    # several points per workgroup, whole compositions per lane
+])
+def test_network_kernels_composition_split(device, monkeypatch, order, neurons, points, split):
+    """The network kernels with the forward compositions split over lanes
+    (CPDE_NET_SPLIT=2, one point per workgroup: whole compositions are the
+    default there) and unsplit where a split is the default, against the
+    oracle."""
+    monkeypatch.setenv('CPDE_FUSED', '2')
+    monkeypatch.setenv('CPDE_NET_SPLIT', split)
+    print(f'[case] composition split order={order} neurons={neurons} points={points} split={split}', flush=True)
+    wl = small_workload(order, neurons, points)
+    run = hip.MatchingRun(device, wl)
+    run.step()
+    device.synchronize()
+    loss, grads = run.loss(), run.gradients()
+    ref_loss, ref_grads = oracle_epoch(order, tuple(neurons), points, 0)
+    print(f'[result] loss {loss!r} oracle {ref_loss!r}', flush=True)
+    assert abs(loss / ref_loss - 1) < 1e-4
+    for t, (g, r) in enumerate(zip(grads, ref_grads)):
+        assert rel_l2(g, r) < 1e-3, t
+    run.close()
+
+
 @functools.lru_cache(maxsize=None)
 def oracle_epoch(order, neurons, points, chunk):
     """The oracle's epoch of small_workload, computed once for all kernel families."""
