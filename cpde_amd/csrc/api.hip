@@ -538,15 +538,18 @@ static GradientPlan plan_gradients(Plan& p, bool accumulate, const int* external
         return std::max(1, per_cu * d.compute_units / std::max(1, tiles));
     };
     int total_tiles = count_tiles();
-    const int force = env_int("CPDE_WGRAD_DIRECT", -1);  // 0: LDS-staged tiles, 2: direct tiles, else chosen
-    if (total_tiles > 0 && K / splits_for(total_tiles) < kWgradMinColumns) {
-        // short splits: 64x64 tiles fed straight from global memory (LDS-staged
-        // with CPDE_WGRAD_DIRECT=0)
+    // 64x64 tiles fed straight from global memory, one per CU.  They beat the
+    // LDS-staged tiles on long reductions too: 2->256^4->1 over 65,536-point
+    // chunks 25.9 -> 24.8 ms of weight gradient per epoch, 3->128^5->1 over
+    // 32,768 points 1.37 -> 1.27 ms.  CPDE_WGRAD_DIRECT=0 keeps the LDS-staged
+    // tiles (128x128, or 64x64 where those splits would be short).
+    const bool staged = env_int("CPDE_WGRAD_DIRECT", -1) == 0;
+    if (total_tiles > 0 && !staged) {
         small_tiles = true;
-        direct = force != 0;
+        direct = true;
         total_tiles = count_tiles();
-    } else if (total_tiles > 0 && force == 2) {
-        direct = true;  // forced on long reductions too
+    } else if (total_tiles > 0 && K / splits_for(total_tiles) < kWgradMinColumns) {
+        small_tiles = true;
         total_tiles = count_tiles();
     }
     g.wa.direct = direct ? 1 : 0;

@@ -63,7 +63,10 @@ def test_static_epoch_refusals(device, monkeypatch):
     run.close()
     monkeypatch.delenv('CPDE_ONE_PASS')
     # 1 -> 256^6 -> 1 on the value row over four workgroups per CU of 32
-    # points: five 256x256 transitions at 25 splits need 33 MB of partials
+    # points, on the LDS-staged weight-gradient tiles: five 256x256
+    # transitions at 25 splits need 33 MB of partials (the direct tiles, one
+    # per CU, need under 8 MB here)
+    monkeypatch.setenv('CPDE_WGRAD_DIRECT', '0')
     _, cus = device.info()
     neurons = [1] + [256] * 6 + [1]
     points = 128 * cus
@@ -75,6 +78,7 @@ def test_static_epoch_refusals(device, monkeypatch):
         run.step()
     assert err.value.code == hip.EINVAL
     run.close()
+    monkeypatch.delenv('CPDE_WGRAD_DIRECT')
     loss, grads = epoch(device, wl, None, False)
     loss2, grads2 = epoch(device, wl, None, True)
     assert loss == loss2
