@@ -59,28 +59,10 @@ CPU_SAMPLE_MACS = 3.0e9
 # read, 268,435,456 B / 262,144 KiB written.
 COPY_SCALE = (268435456 / (131084.475 * 1024), 268435456 / (262144 * 1024))
 TRAFFIC_KIB = {
-    'fourier_fit_order6': {'network_epoch': (21281.36, 134692.67), 'gemm_wgrad': (31740.74, 4077.5)},
-    'fourier_large_order6': {'network_backward': (4980058.93, 8845747.75), 'network_forward': (424046.03, 14688002.52),
-                             'gemm_wgrad': (9044857.01, 34791.09)},
+    'fourier_fit_order6': {'network_epoch': (20859.94, 134919.15), 'gemm_wgrad': (31754.55, 4077.5)},
+    'fourier_large_order6': {'network_backward': (4986651.81, 8870448.64), 'network_forward': (423199.55, 14688002.1),
+                             'gemm_wgrad': (6994723.69, 4064.13)},
 }
-
-@dataclass
-class Spec:
-    make: Callable
-    steps: int          # timed epochs by default
-    warmup: int
-    trace_steps: int
-    op90: tuple | None  # (warm-ups, epochs per batch, batches) of the server timing command
-    server: bool = False
-
-
-WORKLOADS = {
-    **{f'fourier_fit_order{k}': Spec(lambda k=k: workloads.fourier_fit(k), 500, 50, 20, (20, 100, 7)) for k in range(7)},
-    'poisson_disk_order2': Spec(lambda: workloads.PoissonWorkload(), 500, 50, 20, None, server=True),
-    'fourier_3d_order4': Spec(lambda: workloads.fourier_3d(), 30, 3, 3, (3, 10, 3)),
-    'fourier_large_order6': Spec(lambda: workloads.fourier_large(), 10, 2, 2, (2, 3, 3)),
-}
-
 
 def describe(wl, name):
     if isinstance(wl, workloads.PoissonWorkload):
