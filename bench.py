@@ -64,6 +64,25 @@ TRAFFIC_KIB = {
                              'gemm_wgrad': (6994723.69, 4064.13)},
 }
 
+
+@dataclass
+class Spec:
+    make: Callable
+    steps: int          # timed epochs by default
+    warmup: int
+    trace_steps: int
+    op90: tuple | None  # (warm-ups, epochs per batch, batches) of the server timing command
+    server: bool = False
+
+
+WORKLOADS = {
+    **{f'fourier_fit_order{k}': Spec(lambda k=k: workloads.fourier_fit(k), 500, 50, 20, (20, 100, 7)) for k in range(7)},
+    'poisson_disk_order2': Spec(lambda: workloads.PoissonWorkload(), 500, 50, 20, None, server=True),
+    'fourier_3d_order4': Spec(lambda: workloads.fourier_3d(), 30, 3, 3, (3, 10, 3)),
+    'fourier_large_order6': Spec(lambda: workloads.fourier_large(), 10, 2, 2, (2, 3, 3)),
+}
+
+
 def describe(wl, name):
     if isinstance(wl, workloads.PoissonWorkload):
         return {'workload': name, 'network': '→'.join(str(n) for n in wl.neurons) + ' sigmoid',
@@ -320,7 +339,7 @@ def main(argv=None):
     ap.add_argument('--settle-ms', type=float, default=250.0,
                     help='untimed epochs for this long before the warm-ups, so the GPU leaves its idle clocks')
     ap.add_argument('--no-other-workloads', action='store_true',
-                    help='skip the larger configurations (3D order 4, 2->256^4->1 order 6) timed after the main line')
+                    help='skip the other configurations (order-2 fit, Poisson graph epoch, 3D order 4, 2->256^4->1 order 6) timed after the main line')
     ap.add_argument('--copy-calibration', action='store_true',
                     help='only run a plain 256 MiB device copy five times (the reference for HBM byte counters)')
     args = ap.parse_args(argv)
