@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the cPDE hot path -- TEST INFRASTRUCTURE ONLY.
  *
- * This library is the checker for the MI355X kernels.  Only tests/, the package's
+ * This library is the oracle for the MI355X kernels.  Only tests/, the package's
  * smoke() and bench.py's cpu_baseline leg may load it; the product path never
  * links, calls or falls back to it.
  *

@@ -1,7 +1,7 @@
 """ctypes view of the C oracle -- TEST INFRASTRUCTURE ONLY.
 
 Loaded only by tests/, the package smoke() and bench.py's cpu_baseline leg, as
-the checker; the product path never imports it.  Functions mirror
+the oracle; the product path never imports it.  Functions mirror
 oracle/cpde_oracle.h and take numpy arrays in the reference's layouts:
 stacks [row][point][neuron], weight blocks n_out x (n_in+1) column-major.
 """

@@ -6,7 +6,7 @@ schema's multi-indices.  As a truncated power series in h = x - x0 it is
 f(x0+h) = sum_alpha d^alpha f(x0) h^alpha / alpha!.  Composition with the
 sigmoid is then plain series arithmetic (exp, reciprocal), with no
 set-partition bookkeeping at all; reading the coefficients back gives every
-d^alpha sigma(z(x)) (the same idea as the reference's independent checker,
+d^alpha sigma(z(x)) (the same idea as the reference's independent audit,
 scripts/audit_cuda.py:123-226, restated here).  Complex inputs give the
 complex-step derivative of the whole map, which pins the adjoint.
 """
