@@ -323,6 +323,22 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
     // CUs it was slower (order 4, 365 workgroups: 0.0700 -> 0.0742).
     if (width > 0 && rows <= 16 && npb > 1 && (width + npb - 1) / npb <= compute_units) t.net_threads = 512;
     t.net_threads = env_int("CPDE_NET_THREADS", t.net_threads) == 512 ? 512 : 256;
+    // The waves of a workgroup share a layer's products by output tile.  Where
+    // 32x32 tiles of the narrowest hidden layer are fewer than the waves (a
+    // 128-wide layer in eight waves, a 64-wide one in four), 16-column tiles
+    // keep every wave busy.  2->128^4->1 over 729 points, ms per epoch with
+    // 32 -> 16 columns: order 0 (eight waves) 0.0412 -> 0.0353, order 1
+    // 0.0448 -> 0.0384, order 2 0.0491 -> 0.0467, order 3 0.0567 -> 0.0525;
+    // order 4 (four waves, four tiles) 0.0700 -> 0.0719, so 32 stays there.
+    // Columns that fit in 16 take 16 in any case: a 32-column tile would be
+    // half padding.
+    if (t.col_tile == 0 && t.net_points_per_block > 1 && neurons.size() >= 3) {
+        int narrowest = neurons[1];
+        for (size_t l = 1; l + 1 < neurons.size(); ++l) narrowest = std::min(narrowest, neurons[l]);
+        const int columns = t.net_points_per_block * rows;
+        const int col_tiles = (columns + 31) / 32;
+        if (columns <= 16 || (narrowest + 31) / 32 * col_tiles < t.net_threads / 64) t.col_tile = 16;
+    }
     // Whole compositions per lane, except for several-point workgroups of up
     // to 32 rows, where a split over lanes fills the waves: on the Taylor-scaled
     // rows of one point per workgroup the split only adds lanes that repeat the
