@@ -634,12 +634,12 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
     o << "#define CPDE_NET_POINTS " << net_points_per_block << "\n";
     o << "#define CPDE_NET_THREADS " << tuning.net_threads << "\n";
     o << "#define CPDE_STRIDE " << ((widest + 7) / 8 * 8 + 4) << "\n";
-    // Column tile of the network products: 16 (v_mfma_f32_16x16x4f32) when a
-    // block holds one point and every hidden width is a multiple of 16; else 32
-    // (v_mfma_f32_32x32x2f32).  Measured on 2->128^4->1 at 729 points, epoch
-    // kernel: one point per block (orders 5, 6; 21 and 28 rows) 16 is 6 and 2 %
-    // faster, and 35 rows pad to 48 columns instead of 64 (3D order 4: 11 %);
-    // several points per block (orders 2-4) 32 is 5-15 % faster.
+    // Column tile of the network products: 16 (v_mfma_f32_16x16x4f32) or 32
+    // (v_mfma_f32_32x32x2f32), as the tuning chose it; without a choice, 16 when
+    // a block holds one point.  16 needs every hidden width a multiple of 16.
+    // Measured on 2->128^4->1 at 729 points, epoch kernel: one point per block
+    // (orders 5, 6; 21 and 28 rows) 16 is 6 and 2 % faster, and 35 rows pad to
+    // 48 columns instead of 64 (3D order 4: 11 %).
     {
         bool hidden16 = true;
         for (int l = 1; l + 1 < L; ++l) hidden16 = hidden16 && neurons[l] % 16 == 0;
