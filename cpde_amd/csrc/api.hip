@@ -50,8 +50,12 @@ void check_hip(hipError_t status, const char* what, const char* file, int line) 
     throw device_error(buf);
 }
 
-// Launch the waiting weight-gradient launch, if any; the reduction may wait on.
+static void flush_held(Device& d);
+
+// Launch the held one-pass epoch and the waiting weight-gradient launch, if
+// any; the reduction may wait on.
 void flush_wgrad(Device& d) {
+    flush_held(d);
     Device::PendingReduce& w = d.waiting;
     if (!w.open || !w.wgrad) return;
     w.wgrad = false;
@@ -282,6 +286,7 @@ struct NetArgsHost {
     float* partial_out;
     float* WT[32];
     float* partial_hidden[32];
+    int block_offset, block_count;  // the pass's workgroups in the launch (count 0: the whole grid)
 };
 
 // Tuning of the fused kernels for a schema of `rows` derivative rows over chunks
@@ -894,6 +899,116 @@ struct OwnStacks {
     }
 };
 
+// The held one-pass epoch (Device::held): an expression epoch issued while
+// reductions are deferred, with everything its launch needs.
+struct HeldEpoch {
+    bool open = false;
+    Plan* plan = nullptr;
+    const Program* program = nullptr;
+    hipFunction_t kernel = nullptr;  // its own epoch kernel, to launch it alone
+    NetArgsHost a{};
+    ExpressionArgsHost e{};
+    int width = 0;
+    unsigned blocks = 0, threads = 0;
+    double flops = 0;
+};
+
+static bool epoch_pairs() { return env_int("CPDE_EPOCH_PAIRS", 1) != 0; }
+
+// Launch the held epoch alone, if one is held.
+static void flush_held(Device& d) {
+    if (!d.held || !d.held->open) return;
+    HeldEpoch& h = *d.held;
+    h.open = false;
+    void* args[] = {&h.a, &h.e, &h.width};
+    TraceScope trace(d, kTraceNetworkEpoch, h.flops);
+    launch_module(d, h.kernel, h.blocks, 1, args, h.threads);
+}
+
+// The kernel running the one-pass epochs of plans p0 (program g0) and p1
+// (program g1) in one launch (compiled once, cached on disk and per device by
+// source text, per plan pair by serial and program ids).  Null -- launch them
+// apart -- while a capture is open and it is not loaded yet (loading a module
+// is no launch to record), or when the pair does not compile or load (two
+// programs may define the same name with C linkage): the failure is kept, so
+// the pair is not tried again.
+static hipFunction_t paired_epoch(const Plan& p0, const Program& g0, Plan& p1, const Program& g1) {
+    for (const Plan::PairedEpoch& e : p1.paired_epochs)
+        if (e.partner == p0.serial && e.partner_program == g0.id && e.program == g1.id)
+            return e.epoch ? e.epoch->function : nullptr;
+    Device& d = *p1.net->dev;
+    if (d.capturing) return nullptr;
+    const FusedTuning u0 = tuning(p0.tables.rows, p0.width, d.compute_units, p0.net->neurons);
+    const FusedTuning u1 = tuning(p1.tables.rows, p1.width, d.compute_units, p1.net->neurons);
+    std::shared_ptr<ExpressionEpoch> e;
+    try {
+        const std::string src =
+            expression_pair_source(p0.tables, u0, g0.source, p1.tables, u1, g1.source, p1.net->neurons);
+        for (auto& kv : d.expression_epochs)
+            if (kv.first == src) e = kv.second;
+        if (!e) {
+            std::string log;
+            const std::vector<char> code = compile_module(src, device_arch(d.ordinal), &log);
+            auto loaded = std::make_shared<ExpressionEpoch>();
+            HIP_CHECK(hipModuleLoadData(&loaded->module, code.data()));
+            HIP_CHECK(hipModuleGetFunction(&loaded->function, loaded->module, "network_epoch_pair_k"));
+            d.expression_epochs.emplace_back(src, loaded);
+            e = loaded;
+        }
+    } catch (const std::exception&) {
+        e = nullptr;
+    }
+    p1.paired_epochs.push_back(Plan::PairedEpoch{p0.serial, g0.id, g1.id, e});
+    return e ? e->function : nullptr;
+}
+
+// Launch a one-pass expression epoch of plan p (program g; kernel arguments a,
+// e, width over `blocks` workgroups) as the reductions are deferred: held back
+// when nothing is held, or in one launch with the held epoch when that is of
+// another plan over the same network and this pass runs on stacks of its own
+// (so the two write different stacks, and different partials, as the held
+// pass's weight gradient is waiting).  False: launch it alone (the held epoch,
+// if any, has gone out).  Only epochs whose cost finish rides in the gradient
+// reduction are held, so nothing launched in between reads their records.
+static bool pair_or_hold(Plan& p, const Program* g, hipFunction_t kernel, NetArgsHost& a, ExpressionArgsHost* e,
+                         int width, int blocks, double flops, bool own) {
+    Device& d = *p.net->dev;
+    const unsigned threads = unsigned(p.fused->net_threads);
+    if (d.held && d.held->open) {
+        HeldEpoch& h = *d.held;
+        const hipFunction_t pair = g && epoch_pairs() && own && h.plan != &p && h.plan->net == p.net &&
+                                           h.threads == threads
+                                       ? paired_epoch(*h.plan, *h.program, p, *g)
+                                       : nullptr;
+        if (pair) {
+            h.open = false;
+            h.a.block_offset = 0;
+            h.a.block_count = int(h.blocks);
+            a.block_offset = int(h.blocks);
+            a.block_count = blocks;
+            void* args[] = {&h.a, &h.e, &h.width, &a, e, &width};
+            TraceScope trace(d, kTraceNetworkEpoch, h.flops + flops);
+            launch_module(d, pair, h.blocks + unsigned(blocks), 1, args, threads);
+            return true;
+        }
+        flush_held(d);
+    }
+    if (!g || !epoch_pairs() || !d.defer || blocks > kMaxCostBlocks) return false;
+    if (!d.held) d.held = std::make_shared<HeldEpoch>();
+    HeldEpoch& h = *d.held;
+    h.open = true;
+    h.plan = &p;
+    h.program = g;
+    h.kernel = kernel;
+    h.a = a;
+    h.e = *e;
+    h.width = width;
+    h.blocks = unsigned(blocks);
+    h.threads = threads;
+    h.flops = flops;
+    return true;
+}
+
 // Forward, cost and backward of one chunk in one network-fused launch of
 // `kernel` (arguments: the network, `cost_args`, the chunk width), then the
 // cost's fixed-order finish and the weight-gradient contraction.  `records`
@@ -901,13 +1016,17 @@ struct OwnStacks {
 // weight-gradient split partials go.  Everything that can be refused is
 // checked before the first launch.
 static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostStats* records, int cost_index,
-                           bool accumulate, PartialSpace space = {}, bool update = false) {
+                           bool accumulate, PartialSpace space = {}, bool update = false,
+                           const Program* program = nullptr) {
     Net& n = *p.net;
     Device& d = *n.dev;
     const int L = n.layers;
     int width = p.width;
     const double cols = double(p.columns());
     const int blocks = epoch_blocks(p);
+    // a held epoch this one cannot join goes out before anything of this one
+    if (d.held && d.held->open && (!program || !epoch_pairs() || d.held->plan == &p || d.held->plan->net != &n))
+        flush_held(d);
     flush_if_reads(d, records, cost_index);  // the kernel rewrites this plan's records
     // Behind a waiting weight gradient that reads another plan's stacks in the
     // arena, this pass runs on stacks of its own, so that both passes' tiles
@@ -931,7 +1050,9 @@ static void one_pass_epoch(Plan& p, hipFunction_t kernel, void* cost_args, CostS
     double flops = 0;
     for (int t = 0; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
     for (int t = 1; t + 1 < L; ++t) flops += 2.0 * n.neurons[t] * n.neurons[t + 1] * cols;
-    {
+    // an expression epoch (`program`) may wait for, or join, another plan's
+    if (!pair_or_hold(p, program, kernel, a, static_cast<ExpressionArgsHost*>(cost_args), width, blocks, flops,
+                      own.on)) {
         TraceScope trace(d, kTraceNetworkEpoch, flops);
         launch_module(d, kernel, unsigned(blocks), 1, args, unsigned(p.fused->net_threads));
     }
@@ -1237,7 +1358,9 @@ int cpde_plan_create(cpde_net* net, int rows, int variables, const int* table, i
     return guarded([&] {
         require(net && table && out, "null argument");
         require(width > 0, "invalid chunk size");
+        static std::atomic<uint64_t> serials{0};
         auto p = std::make_unique<cpde_plan>();
+        p->serial = ++serials;
         p->net = net;
         p->rows = rows;
         p->variables = variables;
@@ -1422,6 +1545,7 @@ int cpde_output(cpde_plan* plan, float* dest, int dest_width, const int* rows, i
         Net& n = *plan->net;
         Device& d = *n.dev;
         require(valid >= 0 && valid <= plan->width && offset + valid <= dest_width, "invalid chunk range");
+        flush_wgrad(d);  // the outputs of a held epoch
         launch_output(d, dest, n.z[n.layers - 1], dest_width, n.neurons.back(), plan_rows(*plan, rows), plan->rows,
                       plan->width, offset, valid);
     });
@@ -1775,7 +1899,7 @@ int cpde_epoch_expression(cpde_plan* plan, cpde_program* program, const double* 
         const hipFunction_t kernel = expression_epoch(*plan, *program);
         CostStats* records = epoch_records(*plan);
         ExpressionArgsHost e{fields, quadrature_weights, multiplier, records, samples, offset, valid, collect != 0};
-        one_pass_epoch(*plan, kernel, &e, records, cost_index, accumulate != 0);
+        one_pass_epoch(*plan, kernel, &e, records, cost_index, accumulate != 0, {}, false, program);
     });
 }
 

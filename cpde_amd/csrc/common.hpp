@@ -131,6 +131,14 @@ struct Plan {
     // one-pass epoch runs behind a waiting weight gradient of another plan
     // (cpde_gradients_defer); allocated on first such use
     std::vector<float*> own_z, own_y, own_g;
+    uint64_t serial = 0;  // unique among the plans of the process
+    // one-pass expression epochs of this plan launched together with the held
+    // epoch of another plan (that plan's serial and program, this plan's program)
+    struct PairedEpoch {
+        uint64_t partner, partner_program, program;
+        std::shared_ptr<ExpressionEpoch> epoch;
+    };
+    std::vector<PairedEpoch> paired_epochs;
     size_t columns() const { return size_t(rows) * size_t(width); }
 };
 
@@ -198,6 +206,9 @@ enum TraceKind {
     kTraceFusedForward, kTraceFusedBackward, kTraceFusedOutput, kTraceNetworkForward, kTraceNetworkBackward,
     kTraceNetworkEpoch, kTraceKinds
 };
+// A one-pass epoch launch held back so that the next one can share it (api.hip).
+struct HeldEpoch;
+
 struct TraceRecord {
     int kind;
     double work;
@@ -284,6 +295,10 @@ struct Device {
         double flops = 0;
         const Plan* plan = nullptr;
     } waiting;
+    // While deferring, a one-pass expression epoch is held back and launched
+    // together with the next one of another plan over the same network, or
+    // alone before anything else is launched that depends on it.
+    std::shared_ptr<HeldEpoch> held;
 };
 
 // Synchronise the device's stream; refused while a capture is open (the
@@ -329,6 +344,9 @@ bool mirror_symmetric(const Tables& t);
 std::string fused_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning);
 std::string expression_epoch_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning,
                                     const std::string& program);
+std::string expression_pair_source(const Tables& t0, const FusedTuning& u0, const std::string& program0,
+                                   const Tables& t1, const FusedTuning& u1, const std::string& program1,
+                                   const std::vector<int>& neurons);
 // The one-pass epoch kernel of one expression program on one network module.
 struct ExpressionEpoch {
     hipModule_t module = nullptr;

@@ -18,6 +18,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -695,7 +696,7 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
        << "#else\n"
        << "    float* const S = T;\n"
        << "#endif\n"
-       << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n"
+       << "    const int p0 = net_block(a) * kNPB, npts = min(kNPB, points - p0);\n"
        << prefetch << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
        << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
        << "    __syncthreads();\n";
@@ -722,7 +723,7 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     // network-fused forward and backward, one call per layer with its widths;
     // the one-pass epoch runs both with the matching cost between them
     std::ostringstream fwd, bwd;
-    fwd << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n";
+    fwd << "    const int p0 = net_block(a) * kNPB, npts = min(kNPB, points - p0);\n";
     for (int t = 1; t + 2 < L; ++t)
         fwd << "    net_transpose<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ");\n";
     fwd << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
@@ -748,7 +749,7 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
       << tiles << fwd.str() << "}\n";
     o << "extern \"C\" __global__ __launch_bounds__(" << nt << ", " << tuning.backward_blocks
       << ") void network_backward_k(NetArgs a, int points) {\n"
-      << tiles << "    const int p0 = blockIdx.x * kNPB, npts = min(kNPB, points - p0);\n" << bwd.str() << "}\n";
+      << tiles << "    const int p0 = net_block(a) * kNPB, npts = min(kNPB, points - p0);\n" << bwd.str() << "}\n";
     {
         const int NO = neurons[L - 1];
         const std::string prefetch =
@@ -790,6 +791,54 @@ std::string expression_epoch_source(const Tables& t, const std::vector<int>& neu
     o << "extern \"C\" __global__ __launch_bounds__(" << tuning.net_threads << ", " << tuning.backward_blocks
       << ") void network_epoch_expression_k(NetArgs a, ExpressionArgs e, int points) {\n" << epoch_body(neurons, "", cost)
       << "}\n";
+    return o.str();
+}
+
+// Two one-pass expression epochs over one network in one launch: each leaf's
+// program, tuning macros, compositions and device code in a namespace of its
+// own (its macros undefined after it, so the next leaf defines its own; the
+// program's kernel named `expression` renamed per leaf), and a
+// kernel whose workgroups below the second leaf's block offset run the first
+// leaf's epoch and the rest the second's.  Both leaves need the same threads
+// per workgroup.
+std::string expression_pair_source(const Tables& t0, const FusedTuning& u0, const std::string& program0,
+                                   const Tables& t1, const FusedTuning& u1, const std::string& program1,
+                                   const std::vector<int>& neurons) {
+    if (u0.net_threads != u1.net_threads) throw std::runtime_error("paired epochs need equal workgroup sizes");
+    std::ostringstream o;
+    const int L = int(neurons.size()), NO = neurons[L - 1];
+    o << "// generated: two one-pass epochs of expression costs in one launch\n";
+    const std::string cost = "    net_expression<" + std::to_string(NO) + ">(a, e, " + std::to_string(L - 1) +
+                             ", S, p0, npts, O, O + kNNC * " + std::to_string(NO) + ");\n";
+    for (int leaf = 0; leaf < 2; ++leaf) {
+        std::ostringstream part;
+        // the program's stand-alone cost kernel has C linkage, which the
+        // namespace does not scope: each leaf's gets a name of its own
+        part << "#define expression cpde_leaf" << leaf << "_expression\n"
+             << (leaf ? program1 : program0) << "\n#undef expression\n#define CPDE_EXPRESSION_EPOCH 1\n";
+        emit_prologue(part, leaf ? t1 : t0, neurons, leaf ? u1 : u0);
+        part << "__device__ __forceinline__ void epoch(const NetArgs& a, const ExpressionArgs& e, int points) {\n"
+             << epoch_body(neurons, "", cost) << "}\n";
+        const std::string text = part.str();
+        o << "namespace cpde_leaf" << leaf << " {\n" << text << "}  // namespace cpde_leaf" << leaf << "\n";
+        std::istringstream lines(text);
+        std::string line;
+        while (std::getline(lines, line)) {
+            const size_t at = line.find_first_not_of(" \t");
+            if (at == std::string::npos || line.compare(at, 7, "#define") != 0) continue;
+            std::istringstream words(line.substr(at + 7));
+            std::string name;
+            words >> name;
+            o << "#undef " << name << "\n";
+        }
+    }
+    o << "extern \"C\" __global__ __launch_bounds__(" << u0.net_threads << ", "
+      << std::max(u0.backward_blocks, u1.backward_blocks)
+      << ") void network_epoch_pair_k(cpde_leaf0::NetArgs a0, cpde_leaf0::ExpressionArgs e0, int points0,"
+         " cpde_leaf1::NetArgs a1, cpde_leaf1::ExpressionArgs e1, int points1) {\n"
+         "    if (int(blockIdx.x) < a1.block_offset) cpde_leaf0::epoch(a0, e0, points0);\n"
+         "    else cpde_leaf1::epoch(a1, e1, points1);\n"
+         "}\n";
     return o.str();
 }
 

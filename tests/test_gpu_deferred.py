@@ -5,7 +5,9 @@ joins it, and the scalar graph rides in it) against one launch per pass
 the Poisson disk graph (two leaves with known multipliers), the nested
 variation graph (value-dependent multipliers, three chunks per leaf: with the
 one-pass epochs, with separate network launches, and on the table-driven and
-layer-fused kernels), and two expression costs trained without a graph."""
+layer-fused kernels), and two expression costs trained without a graph.
+The same cases check one-pass expression epochs of two plans that share one
+launch against separate launches."""
 import json
 import os
 
@@ -81,3 +83,18 @@ def test_shared_reductions_match_one_per_pass(tmp_path, name, body, env):
     print(f'[result] {name}: reduction launches shared {launches[0]} alone {launches[1]}', flush=True)
     assert shared == alone
     assert launches[0] < launches[1]
+
+
+@pytest.mark.parametrize('name,body', [('poisson', poisson), ('nested', nested), ('two-costs', two_costs)])
+def test_paired_epochs_match_separate_launches(tmp_path, name, body):
+    """One-pass expression epochs of two plans in one launch (the first held
+    back while reductions are deferred) against each in its own launch
+    (CPDE_EPOCH_PAIRS=0): every frame and the final state byte for byte, and
+    on the Poisson graph half the network-epoch launches."""
+    paired, t1 = run({}, body, tmp_path / 'paired.json')
+    alone, t0 = run({'CPDE_EPOCH_PAIRS': '0'}, body, tmp_path / 'alone.json')
+    launches = [t['network_epoch'][0] for t in (t1, t0)]
+    print(f'[result] {name}: network epoch launches paired {launches[0]} alone {launches[1]}', flush=True)
+    assert paired == alone
+    if name == 'poisson':
+        assert launches[0] < launches[1]
