@@ -1178,6 +1178,7 @@ int cpde_device_open(int ordinal, cpde_device** out) {
         }
         HIP_CHECK(hipMalloc(&d->cost_blocks, sizeof(CostStats) * kMaxCostBlocks));
         for (auto& e : d->marks) HIP_CHECK(hipEventCreate(&e));
+        HIP_CHECK(hipEventCreateWithFlags(&d->copied, hipEventDisableTiming));
         d->reserve_scalars(8, 8);
         HIP_CHECK(hipHostMalloc(&d->host_summary, sizeof(cpde_graph_summary), hipHostMallocDefault));
         *out = d.release();
@@ -1195,6 +1196,7 @@ int cpde_device_close(cpde_device* dev) {
         }
         (void)hipStreamSynchronize(dev->stream);
         for (auto& e : dev->marks) (void)hipEventDestroy(e);
+        if (dev->copied) (void)hipEventDestroy(dev->copied);
         for (auto& e : dev->event_pool) (void)hipEventDestroy(e);
         (void)hipFree(dev->cost_blocks);
         (void)hipFree(dev->scalar_block);
@@ -1761,6 +1763,46 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
         if (layers && gradient_out) std::memcpy(gradient_out, dev->host_grads, sizeof(GradStats) * layers);
         if (summary) *summary_out = *dev->host_summary;
         if (own_summary) *summary_out = *dev->host_graph_summary;
+    });
+}
+
+int cpde_scalars_download_rprop(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
+                                cpde_gradient_stats* gradient_out, cpde_graph_summary* summary_out, cpde_net* net,
+                                int* updated) {
+    return guarded([&] {
+        require(dev && net && updated, "null argument");
+        require(net->dev == dev, "network of another device");
+        require(!dev->capturing, "this call reads back, which a capture cannot record");
+        require(costs >= 0 && costs <= 64, "at most 64 cost slots");
+        require(costs <= dev->cost_capacity && layers == net->layers - 1 && layers <= dev->grad_capacity,
+                "scalar slots out of range");
+        flush_reduce(*dev);
+        // one copy over costs, gradient totals and (with a graph) the summary slot
+        const size_t bytes = summary_out ? dev->scalar_bytes
+                                         : size_t(reinterpret_cast<char*>(dev->grad_totals + layers) -
+                                                  static_cast<char*>(dev->scalar_block));
+        HIP_CHECK(hipMemcpyAsync(dev->host_block, dev->scalar_block, bytes, hipMemcpyDeviceToHost, dev->stream));
+        HIP_CHECK(hipEventRecord(dev->copied, dev->stream));
+        unsigned long long fresh = 0;
+        for (int i = 0; i < costs && i < int(dev->slot_fresh.size()); ++i)
+            if (dev->slot_fresh[i]) fresh |= 1ull << i;
+        UpdateGuard guard{dev->cost_totals, costs, fresh, dev->grad_totals, layers,
+                          summary_out ? dev->graph_summary : nullptr};
+        launch_rprop(*dev, *net, &guard);  // behind the copy, which the host waits for alone
+        HIP_CHECK(hipEventSynchronize(dev->copied));
+        if (costs && cost_out) {
+            std::memcpy(cost_out, dev->host_costs, sizeof(CostStats) * costs);
+            for (int i = 0; i < costs; ++i)
+                if ((fresh >> i) & 1ull) cost_out[i] = cpde_cost_stats{0.0, INT32_MAX, INT32_MAX};
+        }
+        if (layers && gradient_out) std::memcpy(gradient_out, dev->host_grads, sizeof(GradStats) * layers);
+        if (summary_out) *summary_out = *dev->host_graph_summary;
+        // the rule on the bytes the kernel read: the buffers switch where it updated
+        guard.costs = dev->host_costs;
+        guard.grads = dev->host_grads;
+        guard.graph = summary_out ? dev->host_graph_summary : nullptr;
+        *updated = update_accepted(guard) ? 1 : 0;
+        if (*updated) rprop_done(*net);
     });
 }
 

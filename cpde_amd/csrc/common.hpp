@@ -49,6 +49,30 @@ struct GradStats {
     unsigned long long nonfinite;
     int first, pad_;
 };
+// Whether a training epoch's update is accepted -- the rule the protocol
+// server applies before it updates (cuda/cpde_server.cu:394-410): every cost
+// finite and without a bad sample (the slots in the `fresh` mask, not written
+// this epoch, count as clean), the graph, if any, without a bad node, every
+// gradient finite.  One rule for the host and the device, so that an update
+// launched before the host has looked decides as the host will.
+struct UpdateGuard {
+    const CostStats* costs = nullptr;
+    int cost_count = 0;
+    unsigned long long fresh = 0;
+    const GradStats* grads = nullptr;
+    int grad_count = 0;
+    const cpde_graph_summary* graph = nullptr;
+};
+__host__ __device__ inline bool update_accepted(const UpdateGuard& g) {
+    for (int c = 0; c < g.cost_count; ++c) {
+        if ((g.fresh >> c) & 1ull) continue;
+        if (g.costs[c].bad_sample != 0x7fffffff || !__builtin_isfinite(g.costs[c].value)) return false;
+    }
+    if (g.graph && g.graph->bad_node >= 0) return false;
+    for (int t = 0; t < g.grad_count; ++t)
+        if (g.grads[t].nonfinite != 0) return false;
+    return true;
+}
 static_assert(sizeof(CostStats) == sizeof(cpde_cost_stats), "cost stats layout");
 static_assert(sizeof(GradStats) == sizeof(cpde_gradient_stats), "gradient stats layout");
 
@@ -242,6 +266,7 @@ struct Device {
     size_t scalar_bytes = 0;
     int cost_capacity = 0, grad_capacity = 0;
     hipEvent_t marks[8] = {};
+    hipEvent_t copied = nullptr;  // the scalar download of cpde_scalars_download_rprop
     // tracing
     bool tracing = false;
     std::vector<hipEvent_t> event_pool;
@@ -399,7 +424,10 @@ void launch_output_forward(Device& d, const float* W, const float* Y, float* Z, 
 void launch_wgrad_grouped(Device& d, const WgradArgs& a, double flops);
 void launch_reduce_grouped(Device& d, const ReduceArgs& a);
 void launch_reduce_rprop(Device& d, const ReduceArgs& a, Net& net, int first);
-void launch_rprop(Device& d, Net& net);
+// RPROP over every transition, then the switch of the active gradient
+// buffers; with `guard`, the update applies only where the rule accepts the
+// epoch, and the switch is left to the caller.
+void launch_rprop(Device& d, Net& net, const UpdateGuard* guard = nullptr);
 void launch_adam(Device& d, Net& net, int step, float lr);
 void launch_set_steps(Device& d, Net& net, float value);
 void launch_restore_steps(Device& d, Net& net, float floor_value);

@@ -542,6 +542,9 @@ struct OptimizerArgs {
     int begin[kMaxTransitions + 1];
     int block_begin[kMaxTransitions + 1];  // blocks of kOptimizerThreads entries, per transition
     int transitions;
+    // guarded: update only if the epoch's scalars pass the acceptance rule
+    UpdateGuard guard;
+    int guarded;
 };
 
 constexpr int kOptimizerThreads = 256;
@@ -1500,6 +1503,7 @@ __device__ __forceinline__ bool entry_of(const OptimizerArgs& a, int& t, int& j)
 
 // One lane per entry: the gradient already reduced into the active buffer.
 __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs a) {
+    if (a.guarded && !update_accepted(a.guard)) return;  // the same on every lane of the grid
     int t, j;
     if (entry_of(a, t, j)) rprop_update(a, t, j, a.Ga[t][j]);
 }
@@ -1562,12 +1566,17 @@ static void for_transition_groups(Net& net, F launch) {
     }
 }
 
-void launch_rprop(Device& d, Net& net) {
-    for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
+void launch_rprop(Device& d, Net& net, const UpdateGuard* guard) {
+    for_transition_groups(net, [&](OptimizerArgs a, int blocks) {
+        if (guard) {
+            a.guard = *guard;
+            a.guarded = 1;
+        }
         TraceScope trace(d, kTraceOptimizer, 28.0 * a.begin[a.transitions]);  // 4 reads, 3 writes per entry
         hipLaunchKernelGGL(rprop_kernel, blocks, kOptimizerThreads, 0, d.stream, a);
         HIP_CHECK(hipGetLastError());
     });
+    if (guard) return;  // the caller switches the buffers once it knows whether the update applied
     for (auto& act : net.active) act = act == 1 ? 2 : 1;
     net.wt_current = true;
 }

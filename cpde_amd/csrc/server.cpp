@@ -747,6 +747,8 @@ private:
         return v && *v && std::atoi(v) != 0;
     }
     void gradient_epoch(EpochReplays& r, NetRecord& n, bool warm, bool collect, const std::function<void()>& work);
+    void download_rprop(NetRecord& n, int costs, int layers, std::vector<cpde_cost_stats>& cs,
+                        std::vector<cpde_gradient_stats>& gs, GraphRecord* graph, int& updated);
     void download(int costs, int layers, std::vector<cpde_cost_stats>& cs, std::vector<cpde_gradient_stats>& gs,
                   GraphRecord* graph = nullptr);
     void validate_costs(const std::vector<cpde_cost_stats>& cs, std::vector<double>& values, bool before_update);
@@ -930,6 +932,18 @@ void Server::download(int costs, int layers, std::vector<cpde_cost_stats>& cs, s
                                          nullptr, &graph->host));
     else
         call(cpde_scalars_download(dev_, costs, cs.data(), layers, gs.data()));
+    cs.resize(costs);
+    gs.resize(layers);
+}
+
+// download(), with the network's RPROP update launched behind the copy; it
+// applies only if the epoch passes the checks that train() makes next.
+void Server::download_rprop(NetRecord& n, int costs, int layers, std::vector<cpde_cost_stats>& cs,
+                            std::vector<cpde_gradient_stats>& gs, GraphRecord* graph, int& updated) {
+    cs.resize(std::max(costs, 1));
+    gs.resize(std::max(layers, 1));
+    call(cpde_scalars_download_rprop(dev_, costs, cs.data(), layers, gs.data(), graph ? &graph->host : nullptr, n.net,
+                                     &updated));
     cs.resize(costs);
     gs.resize(layers);
 }
@@ -1287,7 +1301,12 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
             }
             call(cpde_inspect_gradients(n.net));
         });
-        download(int(ids.size()), layers, cs, gs, graph.get());
+        // RPROP goes out behind the download and applies only if the checks
+        // below pass (the library applies the same rule to the same scalars)
+        const bool fused_update = method == 0 && ids.size() <= 64;
+        int updated = 0;
+        if (fused_update) download_rprop(n, int(ids.size()), layers, cs, gs, graph.get(), updated);
+        else download(int(ids.size()), layers, cs, gs, graph.get());
         bool bad_gradient = false;
         for (const auto& g : gs) bad_gradient = bad_gradient || g.nonfinite_count != 0;
         if (bad_gradient || (diagnostics && ((completed + 1) % diagnostics == 0 || completed + 1 == epochs))) {
@@ -1307,7 +1326,8 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
                 throw Rejected(("non-finite weight gradient in layer " + std::to_string(t) + ", flattened index " +
                                 std::to_string(gs[t].first_nonfinite) + "; no optimizer update performed for this iteration")
                                    .c_str());
-        if (method == 0) call(cpde_rprop(n.net));
+        if (fused_update) require(updated == 1, "the update was not applied although the epoch passed its checks");
+        else if (method == 0) call(cpde_rprop(n.net));
         else {
             require(n.adam_step < uint64_t(INT_MAX), "Adam counter exceeds supported range");
             call(cpde_adam(n.net, int(++n.adam_step), n.learning_rate));

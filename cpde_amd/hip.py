@@ -77,6 +77,7 @@ SIGNATURES = {
     'cpde_scalars_download': (i32, [vp, i32, vp, i32, vp]),
     'cpde_scalars_download_graph': (i32, [vp, i32, vp, i32, vp, vp, vp]),
     'cpde_rprop': (i32, [vp]),
+    'cpde_scalars_download_rprop': (i32, [vp, i32, vp, i32, vp, vp, vp, vp]),
     'cpde_adam': (i32, [vp, i32, f32]),
     'cpde_set_steps': (i32, [vp, f32]),
     'cpde_restore_steps': (i32, [vp, f32]),
@@ -290,6 +291,17 @@ class Net:
 
     def rprop(self):
         check(load().cpde_rprop(self.handle))
+
+    def download_rprop(self, costs):
+        """The scalar download with RPROP behind it (no graph): cost and
+        gradient totals, and whether the update applied."""
+        layers = len(self.neurons) - 1
+        c = (CostStats * max(costs, 1))()
+        g = (GradientStats * layers)()
+        updated = i32()
+        check(load().cpde_scalars_download_rprop(self.device.handle, costs, ctypes.cast(c, vp), layers,
+                                                 ctypes.cast(g, vp), None, self.handle, ctypes.byref(updated)))
+        return list(c)[:costs], list(g), updated.value
 
     def adam(self, step, lr):
         check(load().cpde_adam(self.handle, step, lr))

@@ -250,6 +250,18 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
 /* RPROP over every transition, then switch the active gradient buffer
  * (Resile_k + switch_active, cuda/derivative_kernels_v4.cu:752-778). */
 int cpde_rprop(cpde_net* net);
+/* The training epoch's scalar download and its RPROP update in one call
+ * (cuda/cpde_server.cu:394-410, the download, the checks and Resile_k): the
+ * copy of `costs` cost totals, the gradient totals of every transition and,
+ * with summary_out, the device's graph summary, as
+ * cpde_scalars_download_graph; the update launched behind the copy, which is
+ * all the host waits for.  The update applies, and the active gradient buffers
+ * switch, only if every cost is finite with no bad sample, the graph has no
+ * bad node and every gradient is finite -- the checks after which the server
+ * updates -- and *updated says whether it did.  costs <= 64. */
+int cpde_scalars_download_rprop(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
+                                cpde_gradient_stats* gradient_out, cpde_graph_summary* summary_out, cpde_net* net,
+                                int* updated);
 /* Adam step `step` (>= 1) with learning rate lr (ADAM_k, :780-799). */
 int cpde_adam(cpde_net* net, int step, float lr);
 /* Set every step to value and clear both histories (Set_Resile_k, :825-832). */

@@ -4,7 +4,8 @@
   are written through the state pointers so that every RPROP transition is
   taken (growth x1.2, rollback x0.5, plain step, zero gradient, a step
   rejected at |w| > 20, float products that underflow to zero, infinities),
-  then cpde_rprop / cpde_set_steps / cpde_restore_steps / cpde_adam run once
+  then cpde_rprop / cpde_set_steps / cpde_restore_steps / cpde_adam (and
+  cpde_scalars_download_rprop, which updates only on clean scalars) run once
   and must match the oracle bit for bit (the oracle's optimizers are pinned
   against the reference server's trajectories in test_oracle_optimizer.py).
 * The protocol server against the reference server's optimizer trajectories
@@ -88,6 +89,43 @@ def test_rprop_every_transition_bit_exact(device, net):
         np.testing.assert_array_equal(net.state(t, 3), rS)
         np.testing.assert_array_equal(net.state(t, act), rga)
         np.testing.assert_array_equal(net.state(t, 3 - act), rgi)
+
+
+def test_download_rprop_updates_only_on_clean_scalars(device, net):
+    """cpde_scalars_download_rprop: with every gradient finite, the weights,
+    steps, both gradient buffers and the buffer switch of cpde_rprop, bit for
+    bit against the oracle, and updated = 1; with infinite gradient entries
+    (the crafted states' own), nothing changes and updated = 0 -- the state a
+    rejected epoch keeps."""
+    T = len(NEURONS) - 1
+    for clean in (True, False):
+        states = []
+        for t in range(T):
+            count = NEURONS[t + 1] * (NEURONS[t] + 1)
+            st = crafted(count, 300 + t)
+            if clean:
+                st[2][~np.isfinite(st[2])] = np.float32(1.5)
+            load_state(net, t, *st)
+            states.append((net.active(t), st))
+        net.inspect_gradients()
+        _, grads, updated = net.download_rprop(0)
+        device.synchronize()
+        nonfinite = sum(g.nonfinite_count for g in grads)
+        print(f'[case] download_rprop clean={clean}: non-finite gradient entries {nonfinite}, updated {updated}',
+              flush=True)
+        assert updated == (1 if clean else 0)
+        assert (nonfinite == 0) == clean
+        for t, (act, (W_, S, ga, gi)) in enumerate(states):
+            if clean:
+                rW, rS, rga, rgi = oracle.rprop(W_, S, ga, gi)
+                assert net.active(t) == 3 - act
+            else:
+                rW, rS, rga, rgi = W_, S, ga, gi
+                assert net.active(t) == act
+            np.testing.assert_array_equal(net.state(t, 0), rW)
+            np.testing.assert_array_equal(net.state(t, 3), rS)
+            np.testing.assert_array_equal(net.state(t, act), rga)
+            np.testing.assert_array_equal(net.state(t, 3 - act), rgi)
 
 
 @pytest.mark.parametrize('mode', ['set', 'restore'])
