@@ -1766,43 +1766,72 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
     });
 }
 
-int cpde_scalars_download_rprop(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
-                                cpde_gradient_stats* gradient_out, cpde_graph_summary* summary_out, cpde_net* net,
-                                int* updated) {
+int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net) {
     return guarded([&] {
-        require(dev && net && updated, "null argument");
+        require(dev && net, "null argument");
         require(net->dev == dev, "network of another device");
-        require(!dev->capturing, "this call reads back, which a capture cannot record");
+        require(!dev->issued.open, "an issued update is not resolved yet");
         require(costs >= 0 && costs <= 64, "at most 64 cost slots");
         require(costs <= dev->cost_capacity && layers == net->layers - 1 && layers <= dev->grad_capacity,
                 "scalar slots out of range");
         flush_reduce(*dev);
         // one copy over costs, gradient totals and (with a graph) the summary slot
-        const size_t bytes = summary_out ? dev->scalar_bytes
-                                         : size_t(reinterpret_cast<char*>(dev->grad_totals + layers) -
-                                                  static_cast<char*>(dev->scalar_block));
+        const size_t bytes = with_graph ? dev->scalar_bytes
+                                        : size_t(reinterpret_cast<char*>(dev->grad_totals + layers) -
+                                                 static_cast<char*>(dev->scalar_block));
         HIP_CHECK(hipMemcpyAsync(dev->host_block, dev->scalar_block, bytes, hipMemcpyDeviceToHost, dev->stream));
         HIP_CHECK(hipEventRecord(dev->copied, dev->stream));
         unsigned long long fresh = 0;
         for (int i = 0; i < costs && i < int(dev->slot_fresh.size()); ++i)
             if (dev->slot_fresh[i]) fresh |= 1ull << i;
-        UpdateGuard guard{dev->cost_totals, costs, fresh, dev->grad_totals, layers,
-                          summary_out ? dev->graph_summary : nullptr};
-        launch_rprop(*dev, *net, &guard);  // behind the copy, which the host waits for alone
+        const UpdateGuard guard{dev->cost_totals, costs, fresh, dev->grad_totals, layers,
+                                with_graph ? dev->graph_summary : nullptr};
+        launch_rprop(*dev, *net, &guard);
+        const bool wt_current = net->wt_current;
+        rprop_done(*net);  // in expectation; cpde_update_resolve switches back if the rule rejects the epoch
+        dev->issued = Device::IssuedUpdate{true, net, costs, layers, with_graph != 0, wt_current, fresh};
+    });
+}
+
+int cpde_update_resolve(cpde_device* dev, cpde_cost_stats* cost_out, cpde_gradient_stats* gradient_out,
+                        cpde_graph_summary* summary_out, int* updated) {
+    return guarded([&] {
+        require(dev && updated, "null argument");
+        require(dev->issued.open, "no issued update");
+        Device::IssuedUpdate u = dev->issued;
+        dev->issued.open = false;
         HIP_CHECK(hipEventSynchronize(dev->copied));
-        if (costs && cost_out) {
-            std::memcpy(cost_out, dev->host_costs, sizeof(CostStats) * costs);
-            for (int i = 0; i < costs; ++i)
-                if ((fresh >> i) & 1ull) cost_out[i] = cpde_cost_stats{0.0, INT32_MAX, INT32_MAX};
+        if (u.costs && cost_out) {
+            std::memcpy(cost_out, dev->host_costs, sizeof(CostStats) * u.costs);
+            for (int i = 0; i < u.costs; ++i)
+                if ((u.fresh >> i) & 1ull) cost_out[i] = cpde_cost_stats{0.0, INT32_MAX, INT32_MAX};
         }
-        if (layers && gradient_out) std::memcpy(gradient_out, dev->host_grads, sizeof(GradStats) * layers);
-        if (summary_out) *summary_out = *dev->host_graph_summary;
-        // the rule on the bytes the kernel read: the buffers switch where it updated
-        guard.costs = dev->host_costs;
-        guard.grads = dev->host_grads;
-        guard.graph = summary_out ? dev->host_graph_summary : nullptr;
+        if (gradient_out) std::memcpy(gradient_out, dev->host_grads, sizeof(GradStats) * u.layers);
+        if (u.graph && summary_out) *summary_out = *dev->host_graph_summary;
+        // the rule on the bytes the kernel read
+        const UpdateGuard guard{dev->host_costs, u.costs, u.fresh, dev->host_grads, u.layers,
+                                u.graph ? dev->host_graph_summary : nullptr};
         *updated = update_accepted(guard) ? 1 : 0;
-        if (*updated) rprop_done(*net);
+        if (!*updated) {  // the update did not apply: the buffers switch back
+            rprop_done(*u.net);
+            u.net->wt_current = u.wt_current;
+        }
+    });
+}
+
+int cpde_scalars_download_rprop(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
+                                cpde_gradient_stats* gradient_out, cpde_graph_summary* summary_out, cpde_net* net,
+                                int* updated) {
+    if (int code = cpde_update_issue(dev, costs, layers, summary_out ? 1 : 0, net)) return code;
+    return cpde_update_resolve(dev, cost_out, gradient_out, summary_out, updated);
+}
+
+int cpde_gradients_discard(cpde_device* dev) {
+    return guarded([&] {
+        require(dev, "null argument");
+        if (dev->held) dev->held->open = false;
+        dev->waiting = Device::PendingReduce{};
+        dev->defer = false;
     });
 }
 

@@ -266,7 +266,17 @@ struct Device {
     size_t scalar_bytes = 0;
     int cost_capacity = 0, grad_capacity = 0;
     hipEvent_t marks[8] = {};
-    hipEvent_t copied = nullptr;  // the scalar download of cpde_scalars_download_rprop
+    hipEvent_t copied = nullptr;  // the scalar download of an issued update
+    // An update issued (cpde_update_issue) and not yet resolved: the copied
+    // scalars' layout, and the network whose buffers switched in expectation.
+    struct IssuedUpdate {
+        bool open = false;
+        Net* net = nullptr;
+        int costs = 0, layers = 0;
+        bool graph = false;
+        bool wt_current = false;  // the network's before the issue
+        unsigned long long fresh = 0;
+    } issued;
     // tracing
     bool tracing = false;
     std::vector<hipEvent_t> event_pool;

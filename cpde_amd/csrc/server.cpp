@@ -569,8 +569,9 @@ public:
         if (dev_ && !trace_file_.empty()) write_trace();
         if (const char* path = std::getenv("CPDE_REPLAY_FILE")) {
             if (std::FILE* f = std::fopen(path, "w")) {
-                std::fprintf(f, "{\"recorded\": %llu, \"replayed\": %llu}\n", (unsigned long long)recorded_,
-                             (unsigned long long)replayed_);
+                std::fprintf(f, "{\"recorded\": %llu, \"replayed\": %llu, \"ahead\": %llu}\n",
+                             (unsigned long long)recorded_, (unsigned long long)replayed_,
+                             (unsigned long long)ahead_);
                 std::fclose(f);
             }
         }
@@ -719,8 +720,9 @@ private:
             if (dev) (void)cpde_gradients_defer(dev, 0);
         }
     };
-    // epochs recorded and replayed (written to CPDE_REPLAY_FILE when the server ends)
-    uint64_t recorded_ = 0, replayed_ = 0;
+    // epochs recorded and replayed, and first halves sent ahead of the previous
+    // epoch's checks (written to CPDE_REPLAY_FILE when the server ends)
+    uint64_t recorded_ = 0, replayed_ = 0, ahead_ = 0;
 
     // Captured epochs (CPDE_REPLAY=1): from the second epoch of a training call
     // on, an epoch's gradient work (its passes, the graph and the gradient
@@ -749,6 +751,11 @@ private:
     void gradient_epoch(EpochReplays& r, NetRecord& n, bool warm, bool collect, const std::function<void()>& work);
     void download_rprop(NetRecord& n, int costs, int layers, std::vector<cpde_cost_stats>& cs,
                         std::vector<cpde_gradient_stats>& gs, GraphRecord* graph, int& updated);
+    // A training epoch in two halves: its passes up to the deferred gradient
+    // launches, then the graph, those launches and the gradient statistics.
+    bool halves_apply(const std::vector<uint64_t>& ids, const GraphRecord* graph);
+    void first_half(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord* graph, bool collect);
+    void second_half(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord* graph);
     void download(int costs, int layers, std::vector<cpde_cost_stats>& cs, std::vector<cpde_gradient_stats>& gs,
                   GraphRecord* graph = nullptr);
     void validate_costs(const std::vector<cpde_cost_stats>& cs, std::vector<double>& values, bool before_update);
@@ -946,6 +953,59 @@ void Server::download_rprop(NetRecord& n, int costs, int layers, std::vector<cpd
                                      &updated));
     cs.resize(costs);
     gs.resize(layers);
+}
+
+// Whether train() may run its RPROP epochs in halves and send the next
+// epoch's first half before this epoch's scalars are back
+// (CPDE_EPOCH_HALVES=0: never).  Everything the first half launches writes
+// scratch only -- stacks, cost records, partials -- while the deferred
+// gradient launches wait, so a rejected epoch can drop the next one's first
+// half and keep its state: that needs deferred reductions and passes that
+// all run in the first half (no graph, or a graph whose leaves all have known
+// multipliers, at least one of which writes the gradient).
+bool Server::halves_apply(const std::vector<uint64_t>& ids, const GraphRecord* graph) {
+    const char* v = std::getenv("CPDE_EPOCH_HALVES");
+    const char* d = std::getenv("CPDE_DEFER_REDUCE");
+    if ((v && *v && std::atoi(v) == 0) || (d && *d && std::atoi(d) == 0) || ids.size() > 64) return false;
+    if (!graph) return true;
+    bool written = false;
+    for (size_t i = 0; i < ids.size(); ++i) {
+        if (!graph->schedule[i].known) return false;
+        CostRecord& c = cost(ids[i]);
+        written = written || (graph->schedule[i].value != 0 && c.input && c.has_gradient && data(c.input).samples > 0);
+    }
+    return written;
+}
+
+// The first half: the passes of graph_pass (every multiplier known) or of the
+// plain cost list, their reductions left waiting.
+void Server::first_half(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord* graph, bool collect) {
+    call(cpde_costs_begin(dev_, int(ids.size())));
+    call(cpde_gradients_defer(dev_, 1));
+    bool first = true;
+    if (graph) {
+        retained_last_ = false;
+        const double* fixed = graph->fixed.as<double>();
+        for (size_t i = 0; i < ids.size(); ++i) {
+            const bool immediate = graph->schedule[i].value != 0;
+            pass(n, cost(ids[i]), int(i), first,
+                 Pass{immediate, true, immediate ? fixed + i : nullptr, 0, INT_MAX, false, 0, ids[i]});
+        }
+    } else {
+        for (size_t i = 0; i < ids.size(); ++i)
+            pass(n, cost(ids[i]), int(i), first, Pass{true, collect, nullptr, 0, INT_MAX, false});
+    }
+}
+
+// The second half: the graph (riding in the waiting reduction), the gradient
+// launches, the statistics.
+void Server::second_half(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord* graph) {
+    if (graph)
+        call(cpde_graph_execute(dev_, graph->dev_nodes.as<cpde_scalar_node>(), int(graph->nodes.size()), graph->root,
+                                int(ids.size()), graph->values.as<double>(), graph->adjoints.as<double>(),
+                                graph->multipliers.as<double>(), graph->active.as<int>(), nullptr, 1));
+    call(cpde_gradients_defer(dev_, 0));
+    call(cpde_inspect_gradients(n.net));
 }
 
 // Server::validate_costs (cuda/cpde_server.cu:341-352).
@@ -1287,26 +1347,66 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
     };
     EpochReplays replays;
     replays.on = replay_enabled() && epochs >= 4;
-    while (completed < epochs && !stop.load()) {
-        const bool collect = (log && (completed + 1) % log == 0) || completed + 1 == epochs;
-        gradient_epoch(replays, n, completed > 0, collect, [&] {
-            if (graph) graph_pass(n, ids, *graph, true);
-            else {
-                call(cpde_costs_begin(dev_, int(ids.size())));
-                DeferredReductions deferred(dev_, true);
-                bool first = true;
-                for (size_t i = 0; i < ids.size(); ++i)
-                    pass(n, cost(ids[i]), int(i), first, Pass{true, collect, nullptr, 0, INT_MAX, false});
-                deferred.finish();
-            }
-            call(cpde_inspect_gradients(n.net));
-        });
+    // RPROP epochs in halves: the next epoch's first half goes out behind this
+    // epoch's update, before its scalars are back, unless the host acts on the
+    // device between the two (evaluation, snapshot, step restoration, the
+    // end); a stop request then takes effect one update later.  If the checks
+    // reject this epoch, the next one's first half is dropped.
+    const bool halves = method == 0 && !replays.on && halves_apply(ids, graph.get());
+    bool ahead = false;  // the next epoch's first half is out
+    struct Ahead {
+        cpde_device* dev;
+        bool& on;
+        ~Ahead() {
+            if (on) (void)cpde_gradients_discard(dev);
+        }
+    } ahead_guard{dev_, ahead};
+    auto collect_at = [&](uint64_t done) { return (log && (done + 1) % log == 0) || done + 1 == epochs; };
+    while (completed < epochs && (ahead || !stop.load())) {
+        const bool collect = collect_at(completed);
         // RPROP goes out behind the download and applies only if the checks
         // below pass (the library applies the same rule to the same scalars)
         const bool fused_update = method == 0 && ids.size() <= 64;
         int updated = 0;
-        if (fused_update) download_rprop(n, int(ids.size()), layers, cs, gs, graph.get(), updated);
-        else download(int(ids.size()), layers, cs, gs, graph.get());
+        if (halves) {
+            if (!ahead) first_half(n, ids, graph.get(), collect);
+            ahead = false;
+            second_half(n, ids, graph.get());
+            call(cpde_update_issue(dev_, int(ids.size()), layers, graph ? 1 : 0, n.net));
+            const uint64_t next = completed + 1;
+            const bool acts = next == epochs || (eval && next % eval == 0) || (save && next % save == 0) ||
+                              (restore_every && (n.updates + 1) % restore_every == 0) || stop.load();
+            if (!acts) {
+                try {
+                    ahead = true;
+                    first_half(n, ids, graph.get(), collect_at(next));
+                    ++ahead_;
+                } catch (...) {
+                    (void)cpde_update_resolve(dev_, nullptr, nullptr, nullptr, &updated);
+                    throw;
+                }
+            }
+            cs.resize(std::max<size_t>(ids.size(), 1));
+            gs.resize(std::max(layers, 1));
+            call(cpde_update_resolve(dev_, cs.data(), gs.data(), graph ? &graph->host : nullptr, &updated));
+            cs.resize(ids.size());
+            gs.resize(layers);
+        } else {
+            gradient_epoch(replays, n, completed > 0, collect, [&] {
+                if (graph) graph_pass(n, ids, *graph, true);
+                else {
+                    call(cpde_costs_begin(dev_, int(ids.size())));
+                    DeferredReductions deferred(dev_, true);
+                    bool first = true;
+                    for (size_t i = 0; i < ids.size(); ++i)
+                        pass(n, cost(ids[i]), int(i), first, Pass{true, collect, nullptr, 0, INT_MAX, false});
+                    deferred.finish();
+                }
+                call(cpde_inspect_gradients(n.net));
+            });
+            if (fused_update) download_rprop(n, int(ids.size()), layers, cs, gs, graph.get(), updated);
+            else download(int(ids.size()), layers, cs, gs, graph.get());
+        }
         bool bad_gradient = false;
         for (const auto& g : gs) bad_gradient = bad_gradient || g.nonfinite_count != 0;
         if (bad_gradient || (diagnostics && ((completed + 1) % diagnostics == 0 || completed + 1 == epochs))) {
@@ -1342,7 +1442,7 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
         n.remaining = epochs - completed;
         // the absolute update count survives short calls and checkpoints
         if (restore_every && n.updates % restore_every == 0) call(cpde_restore_steps(n.net, restore_step));
-        const bool last = completed == epochs || stop.load();
+        const bool last = completed == epochs || (!ahead && stop.load());
         if (collect) report(0);
         if (eval && (completed % eval == 0 || last)) {
             evaluate_costs(n, ids, values, graph.get());

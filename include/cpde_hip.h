@@ -251,17 +251,32 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
  * (Resile_k + switch_active, cuda/derivative_kernels_v4.cu:752-778). */
 int cpde_rprop(cpde_net* net);
 /* The training epoch's scalar download and its RPROP update in one call
- * (cuda/cpde_server.cu:394-410, the download, the checks and Resile_k): the
- * copy of `costs` cost totals, the gradient totals of every transition and,
- * with summary_out, the device's graph summary, as
- * cpde_scalars_download_graph; the update launched behind the copy, which is
- * all the host waits for.  The update applies, and the active gradient buffers
- * switch, only if every cost is finite with no bad sample, the graph has no
- * bad node and every gradient is finite -- the checks after which the server
- * updates -- and *updated says whether it did.  costs <= 64. */
+ * (cuda/cpde_server.cu:394-410, the download, the checks and Resile_k):
+ * cpde_update_issue, then cpde_update_resolve. */
 int cpde_scalars_download_rprop(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
                                 cpde_gradient_stats* gradient_out, cpde_graph_summary* summary_out, cpde_net* net,
                                 int* updated);
+/* The first half of that call: the copy of `costs` cost totals, the gradient
+ * totals of every transition (layers = the network's transitions) and, with
+ * with_graph, the device's graph summary, to the device's host block; then
+ * RPROP behind the copy, which applies only if every cost is finite with no
+ * bad sample, the graph has no bad node and every gradient is finite -- the
+ * checks after which the server updates.  The active gradient buffers switch
+ * now, in expectation, so that calls made before the resolution (the next
+ * epoch's first passes) write the next gradient where it belongs.  costs <= 64;
+ * one issued update per device at a time. */
+int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net);
+/* The second half: wait for the copy alone, hand out the scalars (as
+ * cpde_scalars_download_graph does) and say whether the update applied; where
+ * it did not, the buffers switch back. */
+int cpde_update_resolve(cpde_device* dev, cpde_cost_stats* cost_out, cpde_gradient_stats* gradient_out,
+                        cpde_graph_summary* summary_out, int* updated);
+/* Drop the held one-pass epoch and the waiting weight-gradient and reduction
+ * launches without launching them, and stop deferring (cpde_gradients_defer):
+ * for passes issued ahead of a check that then rejected the epoch before them.
+ * Such passes write scratch only (stacks, records, partials), so nothing of
+ * the network's state changes. */
+int cpde_gradients_discard(cpde_device* dev);
 /* Adam step `step` (>= 1) with learning rate lr (ADAM_k, :780-799). */
 int cpde_adam(cpde_net* net, int step, float lr);
 /* Set every step to value and clear both histories (Set_Resile_k, :825-832). */

@@ -7,7 +7,9 @@ variation graph (value-dependent multipliers, three chunks per leaf: with the
 one-pass epochs, with separate network launches, and on the table-driven and
 layer-fused kernels), and two expression costs trained without a graph.
 The same cases check one-pass expression epochs of two plans that share one
-launch against separate launches."""
+launch against separate launches, and RPROP epochs in halves (the next
+epoch's first passes sent before this epoch's scalars are back) against whole
+epochs, with an epoch rejected after the next one's first half went out."""
 import json
 import os
 
@@ -98,3 +100,44 @@ def test_paired_epochs_match_separate_launches(tmp_path, name, body):
     assert paired == alone
     if name == 'poisson':
         assert launches[0] < launches[1]
+
+
+def run_counted(env, body, counts):
+    s = wire.Session(SERVER, env=dict(os.environ, CPDE_REPLAY_FILE=str(counts), **env))
+    try:
+        result = body(s)
+    finally:
+        s.close()
+    return result, json.loads(counts.read_text())
+
+
+def rejected_at_epoch_one(s):
+    """u = w x + b on one point, x = 1e30, w = 0, b = 1, cost u^2, RPROP: epoch
+    0 is clean (objective 1, dE/dw 2e30); its update moves w by a step, so
+    epoch 1's objective overflows and the epoch is rejected -- after epoch 1's
+    first passes went out behind epoch 0's update."""
+    n = s.network([1, 1], [1, 1], [np.array([0.0, 1.0], np.float32)])
+    d = s.data(np.array([[[1e30]]], np.float32), np.array([[0, 0]], np.int32))
+    c = s.polynomial_cost(n, d, [0], 1, [[0, 0, -1]], np.ones((1, 1), np.float32), np.zeros((1, 1), np.float32),
+                          np.ones((1, 1), np.float32))
+    with pytest.raises(wire.ServerError) as err:
+        s.train(n, [c], 4, method=0, fresh=1, log=1, diagnostics=1)
+    return str(err.value), canonical(err.value.events), s.snapshot(n)
+
+
+@pytest.mark.parametrize('name,body', [('poisson', poisson), ('two-costs', two_costs),
+                                       ('rejected', rejected_at_epoch_one)])
+def test_epochs_in_halves_match_whole_epochs(tmp_path, name, body):
+    """RPROP training with each epoch's first passes sent before the previous
+    epoch's scalars are back (its update guarded on the device) against whole
+    epochs (CPDE_EPOCH_HALVES=0): every frame, the final state and, for a
+    rejected epoch, the error byte for byte; first halves were sent ahead."""
+    halves, c1 = run_counted({}, body, tmp_path / 'halves.json')
+    whole, c0 = run_counted({'CPDE_EPOCH_HALVES': '0'}, body, tmp_path / 'whole.json')
+    print(f'[result] {name}: first halves sent ahead {c1["ahead"]} (whole epochs {c0["ahead"]})', flush=True)
+    if name == 'rejected':
+        print(f'[result] {name}: {halves[0]}', flush=True)
+        meta, _ = wire.decode_state(bytes(halves[2]))
+        assert meta['updates'] == 1
+    assert halves == whole
+    assert c1['ahead'] > 0 and c0['ahead'] == 0

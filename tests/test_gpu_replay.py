@@ -80,7 +80,7 @@ def test_replayed_epochs_match_launched(tmp_path, name, body):
     replayed, counts = run({'CPDE_REPLAY': '1'}, tmp_path, body)
     launched, none = run({}, tmp_path, body)
     print(f'[result] {name}: recorded {counts["recorded"]} replayed {counts["replayed"]}', flush=True)
-    assert none == {'recorded': 0, 'replayed': 0}
+    assert (none['recorded'], none['replayed']) == (0, 0)
     assert counts['replayed'] > 0
     assert replayed == launched
 
