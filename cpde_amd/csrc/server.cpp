@@ -1354,13 +1354,18 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
     // reject this epoch, the next one's first half is dropped.
     const bool halves = method == 0 && !replays.on && halves_apply(ids, graph.get());
     bool ahead = false;  // the next epoch's first half is out
+    // leaving early: a first half sent ahead is dropped, waiting launches of
+    // this epoch's go out (deferral ends, as DeferredReductions ends it)
     struct Ahead {
         cpde_device* dev;
         bool& on;
+        bool used;
         ~Ahead() {
+            if (!used) return;
             if (on) (void)cpde_gradients_discard(dev);
+            else (void)cpde_gradients_defer(dev, 0);
         }
-    } ahead_guard{dev_, ahead};
+    } ahead_guard{dev_, ahead, halves};
     auto collect_at = [&](uint64_t done) { return (log && (done + 1) % log == 0) || done + 1 == epochs; };
     while (completed < epochs && (ahead || !stop.load())) {
         const bool collect = collect_at(completed);
