@@ -301,8 +301,8 @@ struct NetArgsHost {
 // than one point did.  That needs whole columns per composition lane (hidden
 // widths above 64) and hidden widths that are multiples of 16.  Measured:
 // 3->128^5->1 over 32,768 points 6.87 -> 5.79 ms per epoch, 2->256^4->1 over
-// 65,536-point chunks 102.8 -> 95.4 ms; at 729 points (config 2, under one
-// workgroup per CU either way) two points per workgroup were slower.
+// 65,536-point chunks 102.8 -> 95.4 ms; 2->128^4->1 at 729 points (under one
+// workgroup per CU either way): two points per workgroup were slower.
 static FusedTuning tuning(int rows, int width, int compute_units, const std::vector<int>& neurons) {
     FusedTuning t;
     int npb = rows <= 16 ? 32 / rows : 1;

@@ -37,5 +37,5 @@ def test_workload_table_and_epoch_roofline():
                                     'fourier_3d_order4', 'fourier_large_order6'}
     wl = bench.WORKLOADS['fourier_fit_order6'].make()
     t_roof = wl.flops_per_epoch() / bench.PEAK_FP32_MFMA + wl.bytes_per_epoch() / bench.PEAK_HBM
-    assert abs(t_roof * 1e6 - 64.83) < 0.05   # config 2's T_roof
+    assert abs(t_roof * 1e6 - 64.83) < 0.05   # T_roof of the 729-point order-6 fit
     assert bench.WORKLOADS['poisson_disk_order2'].server

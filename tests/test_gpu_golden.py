@@ -2,7 +2,7 @@
 through the C ABI, on the layer-fused (schema-specialised) kernels and on the
 table-driven kernels.
 
-Bars (order 6): loss relative error <= 1e-4; every
+Bars (the parity tolerances, order 6): loss relative error <= 1e-4; every
 derivative output row and every weight gradient relative L2 <= 1e-3.  RPROP:
 after one update from a fresh optimizer state, every weight whose reference
 gradient exceeds 1e-3 of the largest must be bit-identical to the reference's.

@@ -11,8 +11,8 @@
 * The protocol server against the reference server's optimizer trajectories
   (tests/golden/optimizer.npz): per epoch from the reference's own state, and
   free running.  RPROP weights and steps must be bit-identical wherever the
-  gradient is sure (above 1e-3 of its largest entry): the north star's
-  "sign decisions bit-exact wherever the gradient exceeds the tolerance".
+  gradient is sure (above 1e-3 of its largest entry): sign decisions
+  bit-exact wherever the gradient exceeds the tolerance.
 """
 import numpy as np
 import pytest
