@@ -1766,9 +1766,11 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
     });
 }
 
-int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net) {
+int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net, int method, int step,
+                      float lr) {
     return guarded([&] {
         require(dev && net, "null argument");
+        require(method == 0 || (method == 1 && step >= 1), "method 0 (RPROP) or 1 (Adam, step >= 1)");
         require(net->dev == dev, "network of another device");
         require(!dev->issued.open, "an issued update is not resolved yet");
         require(costs >= 0 && costs <= 64, "at most 64 cost slots");
@@ -1786,10 +1788,14 @@ int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, c
             if (dev->slot_fresh[i]) fresh |= 1ull << i;
         const UpdateGuard guard{dev->cost_totals, costs, fresh, dev->grad_totals, layers,
                                 with_graph ? dev->graph_summary : nullptr};
-        launch_rprop(*dev, *net, &guard);
         const bool wt_current = net->wt_current;
-        rprop_done(*net);  // in expectation; cpde_update_resolve switches back if the rule rejects the epoch
-        dev->issued = Device::IssuedUpdate{true, net, costs, layers, with_graph != 0, wt_current, fresh};
+        if (method == 0) {
+            launch_rprop(*dev, *net, &guard);
+            rprop_done(*net);  // in expectation; cpde_update_resolve switches back if the rule rejects the epoch
+        } else {
+            launch_adam(*dev, *net, step, lr, &guard);
+        }
+        dev->issued = Device::IssuedUpdate{true, net, costs, layers, with_graph != 0, method == 0, wt_current, fresh};
     });
 }
 
@@ -1812,8 +1818,8 @@ int cpde_update_resolve(cpde_device* dev, cpde_cost_stats* cost_out, cpde_gradie
         const UpdateGuard guard{dev->host_costs, u.costs, u.fresh, dev->host_grads, u.layers,
                                 u.graph ? dev->host_graph_summary : nullptr};
         *updated = update_accepted(guard) ? 1 : 0;
-        if (!*updated) {  // the update did not apply: the buffers switch back
-            rprop_done(*u.net);
+        if (!*updated) {  // the update did not apply: RPROP's buffers switch back
+            if (u.rprop) rprop_done(*u.net);
             u.net->wt_current = u.wt_current;
         }
     });
@@ -1822,7 +1828,7 @@ int cpde_update_resolve(cpde_device* dev, cpde_cost_stats* cost_out, cpde_gradie
 int cpde_scalars_download_rprop(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
                                 cpde_gradient_stats* gradient_out, cpde_graph_summary* summary_out, cpde_net* net,
                                 int* updated) {
-    if (int code = cpde_update_issue(dev, costs, layers, summary_out ? 1 : 0, net)) return code;
+    if (int code = cpde_update_issue(dev, costs, layers, summary_out ? 1 : 0, net, 0, 0, 0.0f)) return code;
     return cpde_update_resolve(dev, cost_out, gradient_out, summary_out, updated);
 }
 

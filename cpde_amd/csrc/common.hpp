@@ -274,6 +274,7 @@ struct Device {
         Net* net = nullptr;
         int costs = 0, layers = 0;
         bool graph = false;
+        bool rprop = true;        // RPROP (buffers switched in expectation), else Adam
         bool wt_current = false;  // the network's before the issue
         unsigned long long fresh = 0;
     } issued;
@@ -438,7 +439,8 @@ void launch_reduce_rprop(Device& d, const ReduceArgs& a, Net& net, int first);
 // buffers; with `guard`, the update applies only where the rule accepts the
 // epoch, and the switch is left to the caller.
 void launch_rprop(Device& d, Net& net, const UpdateGuard* guard = nullptr);
-void launch_adam(Device& d, Net& net, int step, float lr);
+// Adam step `step`; with `guard`, only where the rule accepts the epoch.
+void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* guard = nullptr);
 void launch_set_steps(Device& d, Net& net, float value);
 void launch_restore_steps(Device& d, Net& net, float floor_value);
 GraphLaunch graph_launch(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,

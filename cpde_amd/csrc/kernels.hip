@@ -1512,6 +1512,7 @@ __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs 
 __global__ __launch_bounds__(kOptimizerThreads) void adam_kernel(OptimizerArgs a, float lr, float beta1, float beta2,
                                                                   float beta1t, float beta2t) {
 #pragma clang fp contract(off)
+    if (a.guarded && !update_accepted(a.guard)) return;  // the same on every lane of the grid
     int t, j;
     if (entry_of(a, t, j)) {
         const float g = a.Ga[t][j];
@@ -1581,10 +1582,14 @@ void launch_rprop(Device& d, Net& net, const UpdateGuard* guard) {
     net.wt_current = true;
 }
 
-void launch_adam(Device& d, Net& net, int step, float lr) {
+void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* guard) {
     const float b1 = 0.9f, b2 = 0.999f;
     const float b1t = std::pow(b1, float(step)), b2t = std::pow(b2, float(step));
-    for_transition_groups(net, [&](const OptimizerArgs& a, int blocks) {
+    for_transition_groups(net, [&](OptimizerArgs a, int blocks) {
+        if (guard) {
+            a.guard = *guard;
+            a.guarded = 1;
+        }
         hipLaunchKernelGGL(adam_kernel, blocks, kOptimizerThreads, 0, d.stream, a, lr, b1, b2, b1t, b2t);
         HIP_CHECK(hipGetLastError());
     });

@@ -955,7 +955,7 @@ void Server::download_rprop(NetRecord& n, int costs, int layers, std::vector<cpd
     gs.resize(layers);
 }
 
-// Whether train() may run its RPROP epochs in halves and send the next
+// Whether train() may run its epochs in halves and send the next
 // epoch's first half before this epoch's scalars are back
 // (CPDE_EPOCH_HALVES=0: never).  Everything the first half launches writes
 // scratch only -- stacks, cost records, partials -- while the deferred
@@ -1347,12 +1347,12 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
     };
     EpochReplays replays;
     replays.on = replay_enabled() && epochs >= 4;
-    // RPROP epochs in halves: the next epoch's first half goes out behind this
+    // Epochs in halves: the next epoch's first half goes out behind this
     // epoch's update, before its scalars are back, unless the host acts on the
     // device between the two (evaluation, snapshot, step restoration, the
     // end); a stop request then takes effect one update later.  If the checks
     // reject this epoch, the next one's first half is dropped.
-    const bool halves = method == 0 && !replays.on && halves_apply(ids, graph.get());
+    const bool halves = !replays.on && halves_apply(ids, graph.get());
     bool ahead = false;  // the next epoch's first half is out
     // leaving early: a first half sent ahead is dropped, waiting launches of
     // this epoch's go out (deferral ends, as DeferredReductions ends it)
@@ -1377,7 +1377,9 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
             if (!ahead) first_half(n, ids, graph.get(), collect);
             ahead = false;
             second_half(n, ids, graph.get());
-            call(cpde_update_issue(dev_, int(ids.size()), layers, graph ? 1 : 0, n.net));
+            require(method == 0 || n.adam_step < uint64_t(INT_MAX), "Adam counter exceeds supported range");
+            call(cpde_update_issue(dev_, int(ids.size()), layers, graph ? 1 : 0, n.net, method,
+                                   method == 1 ? int(n.adam_step + 1) : 0, n.learning_rate));
             const uint64_t next = completed + 1;
             const bool acts = next == epochs || (eval && next % eval == 0) || (save && next % save == 0) ||
                               (restore_every && (n.updates + 1) % restore_every == 0) || stop.load();
@@ -1431,8 +1433,10 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
                 throw Rejected(("non-finite weight gradient in layer " + std::to_string(t) + ", flattened index " +
                                 std::to_string(gs[t].first_nonfinite) + "; no optimizer update performed for this iteration")
                                    .c_str());
-        if (fused_update) require(updated == 1, "the update was not applied although the epoch passed its checks");
-        else if (method == 0) call(cpde_rprop(n.net));
+        if (halves || fused_update) {  // the update went out behind the download
+            require(updated == 1, "the update was not applied although the epoch passed its checks");
+            if (method == 1) ++n.adam_step;
+        } else if (method == 0) call(cpde_rprop(n.net));
         else {
             require(n.adam_step < uint64_t(INT_MAX), "Adam counter exceeds supported range");
             call(cpde_adam(n.net, int(++n.adam_step), n.learning_rate));

@@ -78,7 +78,7 @@ SIGNATURES = {
     'cpde_scalars_download_graph': (i32, [vp, i32, vp, i32, vp, vp, vp]),
     'cpde_rprop': (i32, [vp]),
     'cpde_scalars_download_rprop': (i32, [vp, i32, vp, i32, vp, vp, vp, vp]),
-    'cpde_update_issue': (i32, [vp, i32, i32, i32, vp]),
+    'cpde_update_issue': (i32, [vp, i32, i32, i32, vp, i32, i32, f32]),
     'cpde_update_resolve': (i32, [vp, vp, vp, vp, vp]),
     'cpde_gradients_discard': (i32, [vp]),
     'cpde_adam': (i32, [vp, i32, f32]),

@@ -258,17 +258,20 @@ int cpde_scalars_download_rprop(cpde_device* dev, int costs, cpde_cost_stats* co
                                 int* updated);
 /* The first half of that call: the copy of `costs` cost totals, the gradient
  * totals of every transition (layers = the network's transitions) and, with
- * with_graph, the device's graph summary, to the device's host block; then
- * RPROP behind the copy, which applies only if every cost is finite with no
- * bad sample, the graph has no bad node and every gradient is finite -- the
- * checks after which the server updates.  The active gradient buffers switch
- * now, in expectation, so that calls made before the resolution (the next
- * epoch's first passes) write the next gradient where it belongs.  costs <= 64;
- * one issued update per device at a time. */
-int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net);
+ * with_graph, the device's graph summary, to the device's host block; then the
+ * update behind the copy -- method 0 RPROP, 1 Adam step `step` with rate lr
+ * (ADAM_k, cuda/derivative_kernels_v4.cu:780-799) -- which applies only if
+ * every cost is finite with no bad sample, the graph has no bad node and every
+ * gradient is finite: the checks after which the server updates.  RPROP's
+ * active gradient buffers switch now, in expectation, so that calls made
+ * before the resolution (the next epoch's first passes) write the next
+ * gradient where it belongs.  costs <= 64; one issued update per device at a
+ * time. */
+int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net, int method, int step,
+                      float lr);
 /* The second half: wait for the copy alone, hand out the scalars (as
  * cpde_scalars_download_graph does) and say whether the update applied; where
- * it did not, the buffers switch back. */
+ * it did not, RPROP's buffers switch back. */
 int cpde_update_resolve(cpde_device* dev, cpde_cost_stats* cost_out, cpde_gradient_stats* gradient_out,
                         cpde_graph_summary* summary_out, int* updated);
 /* Drop the held one-pass epoch and the waiting weight-gradient and reduction

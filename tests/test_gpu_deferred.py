@@ -7,7 +7,7 @@ variation graph (value-dependent multipliers, three chunks per leaf: with the
 one-pass epochs, with separate network launches, and on the table-driven and
 layer-fused kernels), and two expression costs trained without a graph.
 The same cases check one-pass expression epochs of two plans that share one
-launch against separate launches, and RPROP epochs in halves (the next
+launch against separate launches, and training epochs in halves (the next
 epoch's first passes sent before this epoch's scalars are back) against whole
 epochs, with an epoch rejected after the next one's first half went out."""
 import json
@@ -111,31 +111,47 @@ def run_counted(env, body, counts):
     return result, json.loads(counts.read_text())
 
 
-def rejected_at_epoch_one(s):
-    """u = w x + b on one point, x = 1e30, w = 0, b = 1, cost u^2, RPROP: epoch
-    0 is clean (objective 1, dE/dw 2e30); its update moves w by a step, so
-    epoch 1's objective overflows and the epoch is rejected -- after epoch 1's
-    first passes went out behind epoch 0's update."""
-    n = s.network([1, 1], [1, 1], [np.array([0.0, 1.0], np.float32)])
-    d = s.data(np.array([[[1e30]]], np.float32), np.array([[0, 0]], np.int32))
-    c = s.polynomial_cost(n, d, [0], 1, [[0, 0, -1]], np.ones((1, 1), np.float32), np.zeros((1, 1), np.float32),
-                          np.ones((1, 1), np.float32))
-    with pytest.raises(wire.ServerError) as err:
-        s.train(n, [c], 4, method=0, fresh=1, log=1, diagnostics=1)
-    return str(err.value), canonical(err.value.events), s.snapshot(n)
+def rejected_at_epoch_one(method):
+    """u = w x + b on one point, w = 0, b = 1, cost (k u)^2: epoch 0 is clean;
+    its update moves w, so epoch 1 overflows and is rejected -- after epoch
+    1's first passes went out behind epoch 0's update.  RPROP: x = 1e30, k = 1
+    (epoch 0: dE/dw 2e30; epoch 1's objective overflows).  Adam: x = 1e22,
+    k^2 = 5e-4 (epoch 0: dE/dw 1e19, whose square Adam's second moment still
+    holds; a first step of about lr makes epoch 1's dE/dw about -1e39)."""
+    x, k = (1e30, 1.0) if method == 0 else (1e22, np.sqrt(5e-4))
+
+    def body(s):
+        n = s.network([1, 1], [1, 1], [np.array([0.0, 1.0], np.float32)])
+        d = s.data(np.array([[[x]]], np.float32), np.array([[0, 0]], np.int32))
+        c = s.polynomial_cost(n, d, [0], 1, [[0, 0, -1]], np.full((1, 1), k, np.float32),
+                              np.zeros((1, 1), np.float32), np.ones((1, 1), np.float32))
+        with pytest.raises(wire.ServerError) as err:
+            s.train(n, [c], 4, method=method, fresh=1, lr=0.01, log=1, diagnostics=1)
+        return str(err.value), canonical(err.value.events), s.snapshot(n)
+    return body
+
+
+def two_costs_adam(s):
+    vw = W.VariationWorkload()
+    n, _, costs = vw.upload(s)
+    res = s.train(n, [costs['a'], costs['free']], 5, method=1, fresh=1, lr=0.01, log=1)
+    return canonical(res['events']), s.snapshot(n)
 
 
 @pytest.mark.parametrize('name,body', [('poisson', poisson), ('two-costs', two_costs),
-                                       ('rejected', rejected_at_epoch_one)])
+                                       ('two-costs-adam', two_costs_adam),
+                                       ('rejected', rejected_at_epoch_one(0)),
+                                       ('rejected-adam', rejected_at_epoch_one(1))])
 def test_epochs_in_halves_match_whole_epochs(tmp_path, name, body):
-    """RPROP training with each epoch's first passes sent before the previous
-    epoch's scalars are back (its update guarded on the device) against whole
-    epochs (CPDE_EPOCH_HALVES=0): every frame, the final state and, for a
-    rejected epoch, the error byte for byte; first halves were sent ahead."""
+    """Training (RPROP and Adam) with each epoch's first passes sent before
+    the previous epoch's scalars are back (its update guarded on the device)
+    against whole epochs (CPDE_EPOCH_HALVES=0): every frame, the final state
+    and, for a rejected epoch, the error byte for byte; first halves were sent
+    ahead."""
     halves, c1 = run_counted({}, body, tmp_path / 'halves.json')
     whole, c0 = run_counted({'CPDE_EPOCH_HALVES': '0'}, body, tmp_path / 'whole.json')
     print(f'[result] {name}: first halves sent ahead {c1["ahead"]} (whole epochs {c0["ahead"]})', flush=True)
-    if name == 'rejected':
+    if name.startswith('rejected'):
         print(f'[result] {name}: {halves[0]}', flush=True)
         meta, _ = wire.decode_state(bytes(halves[2]))
         assert meta['updates'] == 1
