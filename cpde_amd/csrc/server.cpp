@@ -697,7 +697,8 @@ private:
     void bind_retained(NetRecord& n, uint64_t id, cpde_plan* plan, int chunk);
     void pass(NetRecord& n, CostRecord& c, int slot, bool& first, const Pass& how);
     void prepare_costs(NetRecord& n, const std::vector<uint64_t>& ids, uint64_t ni);
-    void graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord& graph, bool backward);
+    void graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord& graph, bool backward,
+                    bool leave_waiting = false);
     bool retained_last_ = false;  // the last graph pass kept forwards in stack sets
 
     // An epoch's backward passes over one network share their reduction
@@ -716,6 +717,8 @@ private:
             if (dev) call(cpde_gradients_defer(dev, 0));
             dev = nullptr;
         }
+        // the waiting launches stay waiting for the caller, who ends deferral
+        void release() { dev = nullptr; }
         ~DeferredReductions() {
             if (dev) (void)cpde_gradients_defer(dev, 0);
         }
@@ -755,7 +758,7 @@ private:
     // launches, then the graph, those launches and the gradient statistics.
     bool halves_apply(const std::vector<uint64_t>& ids, const GraphRecord* graph);
     void first_half(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord* graph, bool collect);
-    void second_half(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord* graph);
+    void second_half(NetRecord& n);
     void download(int costs, int layers, std::vector<cpde_cost_stats>& cs, std::vector<cpde_gradient_stats>& gs,
                   GraphRecord* graph = nullptr);
     void validate_costs(const std::vector<cpde_cost_stats>& cs, std::vector<double>& values, bool before_update);
@@ -958,52 +961,40 @@ void Server::download_rprop(NetRecord& n, int costs, int layers, std::vector<cpd
 // Whether train() may run its epochs in halves and send the next
 // epoch's first half before this epoch's scalars are back
 // (CPDE_EPOCH_HALVES=0: never).  Everything the first half launches writes
-// scratch only -- stacks, cost records, partials -- while the deferred
-// gradient launches wait, so a rejected epoch can drop the next one's first
-// half and keep its state: that needs deferred reductions and passes that
-// all run in the first half (no graph, or a graph whose leaves all have known
-// multipliers, at least one of which writes the gradient).
+// scratch only -- stacks, cost records, partials, the graph's values and
+// multipliers -- while the deferred gradient launches wait, so a rejected
+// epoch can drop the next one's first half and keep its state.  That needs
+// deferred reductions and, with a graph, a leaf that writes the gradient (a
+// graph pass with none zeroes it instead, which is state).
 bool Server::halves_apply(const std::vector<uint64_t>& ids, const GraphRecord* graph) {
     const char* v = std::getenv("CPDE_EPOCH_HALVES");
     const char* d = std::getenv("CPDE_DEFER_REDUCE");
     if ((v && *v && std::atoi(v) == 0) || (d && *d && std::atoi(d) == 0) || ids.size() > 64) return false;
     if (!graph) return true;
-    bool written = false;
-    for (size_t i = 0; i < ids.size(); ++i) {
-        if (!graph->schedule[i].known) return false;
+    for (size_t i = 0; i < ids.size(); ++i) {  // graph_pass's test for a leaf that writes the gradient
         CostRecord& c = cost(ids[i]);
-        written = written || (graph->schedule[i].value != 0 && c.input && c.has_gradient && data(c.input).samples > 0);
+        const bool runs = !graph->schedule[i].known || graph->schedule[i].value != 0;
+        if (runs && c.input && c.has_gradient && data(c.input).samples > 0) return true;
     }
-    return written;
+    return false;
 }
 
-// The first half: the passes of graph_pass (every multiplier known) or of the
-// plain cost list, their reductions left waiting.
+// The first half: the graph pass (the graph itself included) or the plain
+// cost list's passes, their gradient launches left waiting.
 void Server::first_half(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord* graph, bool collect) {
+    if (graph) {
+        graph_pass(n, ids, *graph, true, true);
+        return;
+    }
     call(cpde_costs_begin(dev_, int(ids.size())));
     call(cpde_gradients_defer(dev_, 1));
     bool first = true;
-    if (graph) {
-        retained_last_ = false;
-        const double* fixed = graph->fixed.as<double>();
-        for (size_t i = 0; i < ids.size(); ++i) {
-            const bool immediate = graph->schedule[i].value != 0;
-            pass(n, cost(ids[i]), int(i), first,
-                 Pass{immediate, true, immediate ? fixed + i : nullptr, 0, INT_MAX, false, 0, ids[i]});
-        }
-    } else {
-        for (size_t i = 0; i < ids.size(); ++i)
-            pass(n, cost(ids[i]), int(i), first, Pass{true, collect, nullptr, 0, INT_MAX, false});
-    }
+    for (size_t i = 0; i < ids.size(); ++i)
+        pass(n, cost(ids[i]), int(i), first, Pass{true, collect, nullptr, 0, INT_MAX, false});
 }
 
-// The second half: the graph (riding in the waiting reduction), the gradient
-// launches, the statistics.
-void Server::second_half(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord* graph) {
-    if (graph)
-        call(cpde_graph_execute(dev_, graph->dev_nodes.as<cpde_scalar_node>(), int(graph->nodes.size()), graph->root,
-                                int(ids.size()), graph->values.as<double>(), graph->adjoints.as<double>(),
-                                graph->multipliers.as<double>(), graph->active.as<int>(), nullptr, 1));
+// The second half: the waiting gradient launches, the statistics.
+void Server::second_half(NetRecord& n) {
     call(cpde_gradients_defer(dev_, 0));
     call(cpde_inspect_gradients(n.net));
 }
@@ -1025,8 +1016,11 @@ void Server::validate_costs(const std::vector<cpde_cost_stats>& cs, std::vector<
     }
 }
 
-// Server::graph_pass (cuda/cpde_server.cu:273-318).
-void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord& graph, bool backward) {
+// Server::graph_pass (cuda/cpde_server.cu:273-318).  `leave_waiting`: the
+// deferred gradient launches (with the graph riding in the reduction, where it
+// does) are left waiting for the caller.
+void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord& graph, bool backward,
+                        bool leave_waiting) {
     call(cpde_costs_begin(dev_, int(ids.size())));
     DeferredReductions deferred(dev_, backward);
     bool first = true;
@@ -1095,7 +1089,8 @@ void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
                      Pass{true, false, multipliers + i, 0, int(i) == reuse ? last_offset : INT_MAX, false,
                           keep[i] ? 2 : 0, ids[i]});
     }
-    deferred.finish();
+    if (leave_waiting) deferred.release();
+    else deferred.finish();
 }
 
 void Server::evaluate_costs(NetRecord& n, const std::vector<uint64_t>& ids, std::vector<double>& values,
@@ -1376,7 +1371,7 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
         if (halves) {
             if (!ahead) first_half(n, ids, graph.get(), collect);
             ahead = false;
-            second_half(n, ids, graph.get());
+            second_half(n);
             require(method == 0 || n.adam_step < uint64_t(INT_MAX), "Adam counter exceeds supported range");
             call(cpde_update_issue(dev_, int(ids.size()), layers, graph ? 1 : 0, n.net, method,
                                    method == 1 ? int(n.adam_step + 1) : 0, n.learning_rate));

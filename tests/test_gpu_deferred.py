@@ -138,7 +138,7 @@ def two_costs_adam(s):
     return canonical(res['events']), s.snapshot(n)
 
 
-@pytest.mark.parametrize('name,body', [('poisson', poisson), ('two-costs', two_costs),
+@pytest.mark.parametrize('name,body', [('poisson', poisson), ('nested', nested), ('two-costs', two_costs),
                                        ('two-costs-adam', two_costs_adam),
                                        ('rejected', rejected_at_epoch_one(0)),
                                        ('rejected-adam', rejected_at_epoch_one(1))])
