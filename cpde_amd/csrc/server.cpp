@@ -1379,13 +1379,15 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
             const bool acts = next == epochs || (eval && next % eval == 0) || (save && next % save == 0) ||
                               (restore_every && (n.updates + 1) % restore_every == 0) || stop.load();
             if (!acts) {
+                ahead = true;
                 try {
-                    ahead = true;
                     first_half(n, ids, graph.get(), collect_at(next));
                     ++ahead_;
                 } catch (...) {
-                    (void)cpde_update_resolve(dev_, nullptr, nullptr, nullptr, &updated);
-                    throw;
+                    // dropped; the next iteration sends it whole, after this
+                    // epoch is counted, where whole epochs would have failed
+                    (void)cpde_gradients_discard(dev_);
+                    ahead = false;
                 }
             }
             cs.resize(std::max<size_t>(ids.size(), 1));
