@@ -173,10 +173,12 @@ int cpde_costs_begin(cpde_device* dev, int costs);
  * cpde_epoch_expression) waits: the next backward pass over the same network
  * that accumulates onto it joins it, and the two are reduced in one launch,
  * bit for bit as two launches in turn; cpde_graph_execute then rides in that
- * launch after its cost finishes.  Every call that reads gradients, costs or
- * the device (downloads, statistics, optimizers, synchronisation, another
- * cost into a slot the waiting launch finishes) launches it first, and so does
- * turning deferral off. */
+ * launch after its cost finishes.  A one-pass expression epoch is held back
+ * too, and the next one of another plan over the same network shares its
+ * launch.  Every call that reads gradients, costs or the device (downloads,
+ * statistics, optimizers, synchronisation, another cost into a slot the
+ * waiting launch finishes) launches them first, and so does turning deferral
+ * off. */
 int cpde_gradients_defer(cpde_device* dev, int on);
 /* Array-matching squared loss (cuda/cost_kernels.cuh:6-35) fused with its
  * deterministic reduction into cost slot cost_index.  target: device wire data
@@ -274,8 +276,9 @@ int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, c
  * it did not, RPROP's buffers switch back. */
 int cpde_update_resolve(cpde_device* dev, cpde_cost_stats* cost_out, cpde_gradient_stats* gradient_out,
                         cpde_graph_summary* summary_out, int* updated);
-/* Drop the held one-pass epoch and the waiting weight-gradient and reduction
- * launches without launching them, and stop deferring (cpde_gradients_defer):
+/* No counterpart in the reference (it has no deferred launches).  Drop the
+ * held one-pass epoch and the waiting weight-gradient and reduction launches
+ * without launching them, and stop deferring (cpde_gradients_defer):
  * for passes issued ahead of a check that then rejected the epoch before them.
  * Such passes write scratch only (stacks, records, partials), so nothing of
  * the network's state changes. */
