@@ -1177,6 +1177,8 @@ int cpde_device_open(int ordinal, cpde_device** out) {
             else d->static_scratch_error = std::string("hipGetSymbolAddress failed: ") + hipGetErrorString(status);
         }
         HIP_CHECK(hipMalloc(&d->cost_blocks, sizeof(CostStats) * kMaxCostBlocks));
+        HIP_CHECK(hipMalloc(&d->update_verdict, sizeof(int)));
+        HIP_CHECK(hipMemset(d->update_verdict, 0, sizeof(int)));
         for (auto& e : d->marks) HIP_CHECK(hipEventCreate(&e));
         HIP_CHECK(hipEventCreateWithFlags(&d->copied, hipEventDisableTiming));
         d->reserve_scalars(8, 8);
@@ -1199,6 +1201,7 @@ int cpde_device_close(cpde_device* dev) {
         if (dev->copied) (void)hipEventDestroy(dev->copied);
         for (auto& e : dev->event_pool) (void)hipEventDestroy(e);
         (void)hipFree(dev->cost_blocks);
+        (void)hipFree(dev->update_verdict);
         (void)hipFree(dev->scalar_block);
         (void)hipHostFree(dev->host_block);
         (void)hipHostFree(dev->host_summary);

@@ -220,6 +220,10 @@ struct ReduceArgs {
     int cost_count[kReduceCosts], cost_overwrite[kReduceCosts];
     int costs, with_graph;
     GraphLaunch graph;
+    // non-null: the gradient stores happen only if *gate is nonzero (the
+    // verdict of an update issued and not yet resolved, cpde_update_issue);
+    // cost finishes and the graph run either way
+    const int* gate;
 };
 // Per-launch device timing (HIP events on the library's stream), grouped by
 // kernel class.  `work` is the launch's algorithmic work: bytes for the
@@ -267,6 +271,8 @@ struct Device {
     int cost_capacity = 0, grad_capacity = 0;
     hipEvent_t marks[8] = {};
     hipEvent_t copied = nullptr;  // the scalar download of an issued update
+    // the guarded update's verdict (1 applied, 0 not), written by its kernel
+    int* update_verdict = nullptr;
     // An update issued (cpde_update_issue) and not yet resolved: the copied
     // scalars' layout, and the network whose buffers switched in expectation.
     struct IssuedUpdate {

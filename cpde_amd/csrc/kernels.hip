@@ -542,10 +542,21 @@ struct OptimizerArgs {
     int begin[kMaxTransitions + 1];
     int block_begin[kMaxTransitions + 1];  // blocks of kOptimizerThreads entries, per transition
     int transitions;
-    // guarded: update only if the epoch's scalars pass the acceptance rule
+    // guarded: update only if the epoch's scalars pass the acceptance rule;
+    // the first lane of the grid leaves the verdict in *verdict (if non-null)
     UpdateGuard guard;
     int guarded;
+    int* verdict;
 };
+
+// The guarded update's rule, the same on every lane of the grid; the first
+// lane records it for the reductions that wait on it (ReduceArgs::gate).
+__device__ __forceinline__ bool update_applies(const OptimizerArgs& a) {
+    if (!a.guarded) return true;
+    const bool ok = update_accepted(a.guard);
+    if (a.verdict && blockIdx.x == 0 && threadIdx.x == 0) *a.verdict = ok ? 1 : 0;
+    return ok;
+}
 
 constexpr int kOptimizerThreads = 256;
 
@@ -670,7 +681,7 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
             float v = a.accumulate ? a.grad[t][idx] + sum : sum;
             if (two) v = v + sum2;
             if constexpr (UPDATE) rprop_update(o, t, idx, v);
-            else a.grad[t][idx] = v;
+            else if (!a.gate || *a.gate) a.grad[t][idx] = v;
         }
     } else {
         const int j = local * 4 + wave;
@@ -700,7 +711,7 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
             float v = a.accumulate ? a.grad[t][idx] + s : s;
             if (two) v = v + s2;
             if constexpr (UPDATE) rprop_update(o, t, idx, v);
-            else a.grad[t][idx] = v;
+            else if (!a.gate || *a.gate) a.grad[t][idx] = v;
         }
     }
 }
@@ -997,9 +1008,26 @@ void launch_reduce_rprop(Device& d, const ReduceArgs& a, Net& net, int first) {
     HIP_CHECK(hipGetLastError());
 }
 
+// Whether reduction `a` writes the gradient buffers of the network whose
+// update is issued and not yet resolved (cpde_update_issue).
+static bool into_issued_update(const Device& d, const ReduceArgs& a) {
+    if (!d.issued.open || !d.issued.net) return false;
+    const Net& n = *d.issued.net;
+    for (int k = 0; k < a.transitions; ++k)
+        for (size_t t = 0; t < n.state[1].size(); ++t)
+            if (a.grad[k] == n.state[1][t] || a.grad[k] == n.state[2][t]) return true;
+    return false;
+}
+
+// A reduction launched while an update is issued (the next epoch's first
+// half, sent before this epoch's scalars are back) into that network's
+// gradient stores only if the update applied: a rejected epoch leaves every
+// state buffer as whole epochs leave it.
 void launch_reduce_grouped(Device& d, const ReduceArgs& a) {
     TraceScope trace(d, kTraceSplitReduce, reduce_bytes(a, 0));
-    hipLaunchKernelGGL(reduce_grouped_kernel, reduce_grid(a), 256, 0, d.stream, a);
+    ReduceArgs b = a;
+    b.gate = into_issued_update(d, a) ? d.update_verdict : nullptr;
+    hipLaunchKernelGGL(reduce_grouped_kernel, reduce_grid(b), 256, 0, d.stream, b);
     HIP_CHECK(hipGetLastError());
 }
 
@@ -1503,7 +1531,7 @@ __device__ __forceinline__ bool entry_of(const OptimizerArgs& a, int& t, int& j)
 
 // One lane per entry: the gradient already reduced into the active buffer.
 __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs a) {
-    if (a.guarded && !update_accepted(a.guard)) return;  // the same on every lane of the grid
+    if (!update_applies(a)) return;
     int t, j;
     if (entry_of(a, t, j)) rprop_update(a, t, j, a.Ga[t][j]);
 }
@@ -1512,7 +1540,7 @@ __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs 
 __global__ __launch_bounds__(kOptimizerThreads) void adam_kernel(OptimizerArgs a, float lr, float beta1, float beta2,
                                                                   float beta1t, float beta2t) {
 #pragma clang fp contract(off)
-    if (a.guarded && !update_accepted(a.guard)) return;  // the same on every lane of the grid
+    if (!update_applies(a)) return;
     int t, j;
     if (entry_of(a, t, j)) {
         const float g = a.Ga[t][j];
@@ -1572,6 +1600,7 @@ void launch_rprop(Device& d, Net& net, const UpdateGuard* guard) {
         if (guard) {
             a.guard = *guard;
             a.guarded = 1;
+            a.verdict = d.update_verdict;
         }
         TraceScope trace(d, kTraceOptimizer, 28.0 * a.begin[a.transitions]);  // 4 reads, 3 writes per entry
         hipLaunchKernelGGL(rprop_kernel, blocks, kOptimizerThreads, 0, d.stream, a);
@@ -1589,6 +1618,7 @@ void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* gua
         if (guard) {
             a.guard = *guard;
             a.guarded = 1;
+            a.verdict = d.update_verdict;
         }
         hipLaunchKernelGGL(adam_kernel, blocks, kOptimizerThreads, 0, d.stream, a, lr, b1, b2, b1t, b2t);
         HIP_CHECK(hipGetLastError());

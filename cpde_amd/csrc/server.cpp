@@ -694,6 +694,8 @@ private:
         uint64_t id = 0;
     };
     bool retention_fits(NetRecord& n, CostRecord& c, double& budget);
+    static double stack_set_bytes(const NetRecord& n, const CostRecord& c);
+    double retained_elsewhere(NetRecord& n, const std::vector<uint64_t>& ids);
     void bind_retained(NetRecord& n, uint64_t id, cpde_plan* plan, int chunk);
     void pass(NetRecord& n, CostRecord& c, int slot, bool& first, const Pass& how);
     void prepare_costs(NetRecord& n, const std::vector<uint64_t>& ids, uint64_t ni);
@@ -875,7 +877,6 @@ bool Server::retention_fits(NetRecord& n, CostRecord& c, double& budget) {
     if (!c.input || !c.has_gradient || !c.has_components) return false;
     const int samples = data(c.input).samples;
     const double chunks = std::ceil(double(samples) / c.width);
-    double floats = 0;
     const double columns = double(c.width) * c.schema.rows;
     if (c.kind == 2) {
         int fused = 0;
@@ -884,13 +885,33 @@ bool Server::retention_fits(NetRecord& n, CostRecord& c, double& budget) {
         for (size_t l = 0; l + 1 < n.neurons.size(); ++l) macs += double(n.neurons[l]) * n.neurons[l + 1];
         if (fused && macs * columns < std::ldexp(1.0, 28)) return false;
     }
-    for (size_t l = 0; l < n.neurons.size(); ++l)
-        floats += columns * n.neurons[l] * (1 + (n.linear[l] ? 0 : 1) + (l > 0 ? 1 : 0));
-    floats += columns * n.neurons[0];  // the chunk's input
-    const double bytes = chunks * floats * sizeof(float);
+    const double bytes = chunks * stack_set_bytes(n, c);
     if (bytes > budget) return false;
     budget -= bytes;
     return true;
+}
+
+// One chunk's stack set: per layer y, and z or u where the layer composes,
+// and g past the input layer; plus the chunk's input.
+double Server::stack_set_bytes(const NetRecord& n, const CostRecord& c) {
+    const double columns = double(c.width) * c.schema.rows;
+    double floats = columns * n.neurons[0];
+    for (size_t l = 0; l < n.neurons.size(); ++l)
+        floats += columns * n.neurons[l] * (1 + (n.linear[l] ? 0 : 1) + (l > 0 ? 1 : 0));
+    return floats * sizeof(float);
+}
+
+// Bytes of stack sets the network holds for costs outside `ids`: they stay
+// allocated through this pass, so they come off the retention budget.
+double Server::retained_elsewhere(NetRecord& n, const std::vector<uint64_t>& ids) {
+    double bytes = 0;
+    for (const auto& kv : n.retained) {
+        if (std::find(ids.begin(), ids.end(), kv.first) != ids.end()) continue;
+        auto it = costs_.find(kv.first);
+        if (it == costs_.end()) continue;
+        bytes += double(kv.second.sets.size()) * stack_set_bytes(n, *it->second);
+    }
+    return bytes;
 }
 
 void Server::bind_retained(NetRecord& n, uint64_t id, cpde_plan* plan, int chunk) {
@@ -960,12 +981,16 @@ void Server::download_rprop(NetRecord& n, int costs, int layers, std::vector<cpd
 
 // Whether train() may run its epochs in halves and send the next
 // epoch's first half before this epoch's scalars are back
-// (CPDE_EPOCH_HALVES=0: never).  Everything the first half launches writes
-// scratch only -- stacks, cost records, partials, the graph's values and
-// multipliers -- while the deferred gradient launches wait, so a rejected
-// epoch can drop the next one's first half and keep its state.  That needs
-// deferred reductions and, with a graph, a leaf that writes the gradient (a
-// graph pass with none zeroes it instead, which is state).
+// (CPDE_EPOCH_HALVES=0: never).  The first half writes stacks, cost records,
+// partials and the graph's values and multipliers, all scratch, while its
+// last gradient launches wait.  Reductions it must launch early (the graph
+// riding in one, a third pass, a cost slot finished twice) store into the
+// gradient buffers only if the update issued before them applied: the
+// update's kernel leaves its verdict on the device and those reductions read
+// it.  So a rejected epoch drops the next one's first half and keeps every
+// state buffer as whole epochs keep it.  That needs deferred reductions and,
+// with a graph, a leaf that writes the gradient (a graph pass with none
+// zeroes it instead, unconditionally).
 bool Server::halves_apply(const std::vector<uint64_t>& ids, const GraphRecord* graph) {
     const char* v = std::getenv("CPDE_EPOCH_HALVES");
     const char* d = std::getenv("CPDE_DEFER_REDUCE");
@@ -1039,7 +1064,7 @@ void Server::graph_pass(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
             written = runs && c.input && c.has_gradient && data(c.input).samples > 0;
         }
         if (!written) call(cpde_zero_gradient(n.net));
-        double budget = retain_budget_mb() * 1048576.0;
+        double budget = retain_budget_mb() * 1048576.0 - retained_elsewhere(n, ids);
         for (size_t i = 0; i < ids.size(); ++i)
             if (!graph.schedule[i].known && retention_fits(n, cost(ids[i]), budget)) keep[i] = retained_last_ = true;
         // run the most expensive leaf with an unknown multiplier and no

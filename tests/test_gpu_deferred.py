@@ -131,6 +131,41 @@ def rejected_at_epoch_one(method):
     return body
 
 
+SQUARE = ([(1, 0, 0), (7, 0, -1)], [0.0, 2.0])  # u ** 2 (scalar ops Component 1, Power 7)
+
+
+def rejected_integrals(method, layout):
+    """u = w x + b (w = 0, b = 1) under integral costs q u**2: epoch 0 is clean;
+    its update moves w, so epoch 1's dE/dw = 2 u q x overflows in fp32 and is
+    rejected, after epoch 2's first half went out behind epoch 1's update.
+    That first half launches reductions before its scalars are back:
+      * 'graph': two leaves summed by a graph, which rides in the reduction
+        and launches it;
+      * 'chunks': one leaf over three samples in one-sample chunks, whose third
+        backward pass launches the first two's reduction.
+    RPROP: x = 1e30, q = 1.  Adam: x = 1e22 and q = 5e-4 / samples, so that
+    epoch 0's dE/dw is 1e19, whose square Adam's second moment still holds,
+    and a first step of about lr gives epoch 1 a dE/dw of about -1e39."""
+    samples = 2 if layout == 'graph' else 3
+    x, q = (1e30, 1.0) if method == 0 else (1e22, 5e-4 / samples)
+
+    def body(s):
+        n = s.network([1, 1], [1, 1], [np.array([0.0, 1.0], np.float32)])
+        table = np.array([[0, 0]], np.int32)
+        if layout == 'graph':
+            ds = [s.data(np.array([[[x]]], np.float32), table) for _ in range(2)]
+            costs = [s.integral_cost(n, d, *SQUARE, np.zeros((0, 1)), [q]) for d in ds]
+            graph = W.PoissonWorkload.graph()
+        else:
+            d = s.data(np.full((1, 1, 3), x, np.float32), table)
+            costs = [s.integral_cost(n, d, *SQUARE, np.zeros((0, 3)), [q] * 3, chunk=1)]
+            graph = None
+        with pytest.raises(wire.ServerError) as err:
+            s.train(n, costs, 6, method=method, fresh=1, lr=0.01, log=1, diagnostics=1, graph=graph)
+        return str(err.value), canonical(err.value.events), s.snapshot(n)
+    return body
+
+
 def two_costs_adam(s):
     vw = W.VariationWorkload()
     n, _, costs = vw.upload(s)
@@ -141,13 +176,17 @@ def two_costs_adam(s):
 @pytest.mark.parametrize('name,body', [('poisson', poisson), ('nested', nested), ('two-costs', two_costs),
                                        ('two-costs-adam', two_costs_adam),
                                        ('rejected', rejected_at_epoch_one(0)),
-                                       ('rejected-adam', rejected_at_epoch_one(1))])
+                                       ('rejected-adam', rejected_at_epoch_one(1)),
+                                       ('rejected-graph', rejected_integrals(0, 'graph')),
+                                       ('rejected-graph-adam', rejected_integrals(1, 'graph')),
+                                       ('rejected-chunks', rejected_integrals(0, 'chunks')),
+                                       ('rejected-chunks-adam', rejected_integrals(1, 'chunks'))])
 def test_epochs_in_halves_match_whole_epochs(tmp_path, name, body):
     """Training (RPROP and Adam) with each epoch's first passes sent before
     the previous epoch's scalars are back (its update guarded on the device)
     against whole epochs (CPDE_EPOCH_HALVES=0): every frame, the final state
-    and, for a rejected epoch, the error byte for byte; first halves were sent
-    ahead."""
+    (all four buffers of every transition) and, for a rejected epoch, the
+    error byte for byte; first halves were sent ahead."""
     halves, c1 = run_counted({}, body, tmp_path / 'halves.json')
     whole, c0 = run_counted({'CPDE_EPOCH_HALVES': '0'}, body, tmp_path / 'whole.json')
     print(f'[result] {name}: first halves sent ahead {c1["ahead"]} (whole epochs {c0["ahead"]})', flush=True)
@@ -157,3 +196,45 @@ def test_epochs_in_halves_match_whole_epochs(tmp_path, name, body):
         assert meta['updates'] == 1
     assert halves == whole
     assert c1['ahead'] > 0 and c0['ahead'] == 0
+
+
+def test_stop_with_halves_leaves_the_state_of_whole_epochs(tmp_path):
+    """op 99 sent on the first report of a long call with nothing that keeps
+    the next first half back (no saves, evaluations or restores): the call
+    stops after some small number of epochs k -- one more than whole epochs
+    would run when the next epoch's first half was already out, as if the
+    stop had arrived during that epoch -- and the state is byte for byte that
+    of k whole epochs (the metadata's remaining count aside)."""
+    def stopped(s):
+        vw = W.VariationWorkload()
+        n, _, costs = vw.upload(s)
+
+        def on_event(session, ev):
+            if ev['kind'] == 6 and not getattr(session, '_stop_sent', False):
+                session._stop_sent = True
+                session.stop()
+        res = s.train(n, [costs['a'], costs['correction']], 100000, method=0, fresh=1, log=1,
+                      graph=vw.nested_graph(), on_event=on_event)
+        return res['completed'], res['stopped'], s.snapshot(n)
+
+    (k, flag, blob), counts = run_counted({}, stopped, tmp_path / 'stopped.json')
+    print(f'[result] stopped after {k} epochs, first halves sent ahead {counts["ahead"]}', flush=True)
+    assert flag == 1 and 1 <= k < 100000
+    meta, _ = wire.decode_state(bytes(blob))
+    assert meta['updates'] == k
+
+    def whole(s):
+        vw = W.VariationWorkload()
+        n, _, costs = vw.upload(s)
+        res = s.train(n, [costs['a'], costs['correction']], k, method=0, fresh=1, log=1, graph=vw.nested_graph())
+        return res['completed'], s.snapshot(n)
+
+    (k0, blob0), _ = run_counted({'CPDE_EPOCH_HALVES': '0'}, whole, tmp_path / 'whole.json')
+    assert k0 == k
+    (m1, l1), (m0, l0) = wire.decode_state(bytes(blob)), wire.decode_state(bytes(blob0))
+    assert m1.pop('remaining') == 100000 - k and m0.pop('remaining') == 0
+    assert m1 == m0
+    for a, b in zip(l1, l0):
+        assert a['active'] == b['active']
+        for x, y in zip(a['buffers'], b['buffers']):
+            assert x.tobytes() == y.tobytes()
