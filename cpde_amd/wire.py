@@ -1,11 +1,18 @@
 """Client for the cPDE stdin/stdout frame protocol.
 
-Frames are ``uint64 LE length`` (counting the 4-byte kind) + ``uint32 kind`` +
-payload; arrays are ``uint64 count`` + raw little-endian elements and strings
-are ``uint64 length`` + bytes (cuda/protocol.hpp:10-51).  Request layouts follow
-the server's parsers in cuda/cpde_server.cu:436-555 and the training request in
-cuda/cpde_server.cu:364-371.  Replies are kind 0 (result) or kind 1 (string
-error); training also streams event frames of kinds 2-6.
+Transport (cuda/protocol.hpp:36-51): a frame is a little-endian u64 byte count
+(the 4-byte kind included), a u32 kind and the payload.  Inside a payload,
+scalars are little-endian fixed-width values, a vector is a u64 element count
+followed by the raw elements, and a string is a u64 byte count followed by the
+bytes (cuda/protocol.hpp:10-34).  Request layouts follow the server's parsers
+(cuda/cpde_server.cu:436-555, the training request :364-371).  Replies are
+kind 0 (result) or kind 1 (error string); training also streams event frames
+of kinds 2-6.
+
+Payloads are described, not hand-assembled: ``encode`` turns a sequence of
+``(tag, value)`` fields into bytes and ``Cursor`` reads tagged fields back, both
+from one table of field tags.  The snapshot blob is read and written from the
+field table ``STATE_HEADER``.
 
 This module drives any executable that speaks the protocol: the MI355X server
 built from this package, or the reference CPU server used as the oracle.
@@ -29,6 +36,154 @@ CAP_CPU, CAP_PROBE = 32, 64
 CONSTANT, COMPONENT, FIELD, ADD, SUB, MUL, DIV, POWER, NEG, EXP, LOG, SQRT, SIN, COS, TANH = range(15)
 LEAF, ATTACH = 1, 15
 
+# ----------------------------------------------------------------------------- field tags
+# fixed-width scalars, by tag
+_FIXED = {tag: struct.Struct('<' + code) for tag, code in
+          (('i32', 'i'), ('u32', 'I'), ('u64', 'Q'), ('f32', 'f'), ('f64', 'd'))}
+# counted vectors, by tag: element dtype (little-endian)
+_COUNTED = {'i32[]': np.dtype('<i4'), 'u64[]': np.dtype('<u8'), 'f32[]': np.dtype('<f4'), 'f64[]': np.dtype('<f8')}
+_COUNT = _FIXED['u64']
+FRAME_HEAD = struct.Struct('<QI')  # byte count (kind included), kind
+MAX_FRAME = 4 * 1024 ** 3
+
+
+def _counted(values, dtype):
+    a = np.asarray(values, dtype=dtype).ravel()
+    return _COUNT.pack(a.size) + a.tobytes()
+
+
+def _field_bytes(tag, value):
+    fixed = _FIXED.get(tag)
+    if fixed is not None:
+        return fixed.pack(value)
+    dtype = _COUNTED.get(tag)
+    if dtype is not None:
+        return _counted(value, dtype)
+    if tag == 'str':
+        b = value.encode('utf-8') if isinstance(value, str) else bytes(value)
+        return _COUNT.pack(len(b)) + b
+    if tag == 'raw':
+        return bytes(value)
+    raise ValueError(f'unknown field tag {tag!r}')
+
+
+def encode(*fields):
+    """Payload bytes of ``(tag, value)`` fields, in order.  Tags: i32, u32, u64,
+    f32, f64 (scalars); i32[], u64[], f32[], f64[] (counted vectors); str
+    (counted UTF-8); raw (bytes as they are)."""
+    return b''.join(_field_bytes(tag, value) for tag, value in fields)
+
+
+class Cursor:
+    """Reads tagged fields from a payload front to back; ``finish`` checks that
+    nothing is left over."""
+
+    __slots__ = ('_view', '_at')
+
+    def __init__(self, payload):
+        self._view = memoryview(payload)
+        self._at = 0
+
+    def _span(self, n):
+        start, stop = self._at, self._at + n
+        if stop > len(self._view):
+            raise RuntimeError(f'response ends after {len(self._view)} bytes, {stop} needed')
+        self._at = stop
+        return start
+
+    def read(self, tag):
+        fixed = _FIXED.get(tag)
+        if fixed is not None:
+            return fixed.unpack_from(self._view, self._span(fixed.size))[0]
+        dtype = _COUNTED.get(tag)
+        if dtype is not None:
+            n = self.read('u64')
+            start = self._span(n * dtype.itemsize)
+            return np.frombuffer(self._view, dtype=dtype, count=n, offset=start).astype(dtype.newbyteorder('='))
+        if tag == 'str':
+            n = self.read('u64')
+            start = self._span(n)
+            return bytes(self._view[start:start + n]).decode('utf-8', 'replace')
+        raise ValueError(f'unknown field tag {tag!r}')
+
+    def read_all(self, *tags):
+        return tuple(self.read(tag) for tag in tags)
+
+    def blob(self, n):
+        start = self._span(n)
+        return bytes(self._view[start:start + n])
+
+    def rest(self):
+        return self.blob(len(self._view) - self._at)
+
+    def finish(self):
+        if self._at != len(self._view):
+            raise RuntimeError(f'{len(self._view) - self._at} unread bytes at the end of a response')
+
+
+# ----------------------------------------------------------------------------- snapshot blob
+# The state blob header (cuda/cpde_server.cu:193-198), field by field; the
+# version must be 1.  After it, per transition: i32 active gradient buffer,
+# then four f32 vectors W, G1, G2, step/m (:199-206).
+STATE_HEADER = (('version', 'u32'), ('neurons', 'i32[]'), ('linear', 'i32[]'), ('optimizer', 'i32'),
+                ('updates', 'u64'), ('adam_step', 'u64'), ('stage_done', 'u64'), ('remaining', 'u64'),
+                ('learning_rate', 'f32'), ('initial_step', 'f32'), ('stage', 'str'))
+STATE_BUFFERS = 4
+
+
+def read_metadata(cursor):
+    meta = {name: cursor.read(tag) for name, tag in STATE_HEADER}
+    if meta.pop('version') != 1:
+        raise ValueError('unsupported state version')
+    meta['neurons'], meta['linear'] = meta['neurons'].tolist(), meta['linear'].tolist()
+    return meta
+
+
+def decode_state(blob):
+    """A snapshot blob: (metadata dict, per transition {'active', 'buffers'})."""
+    c = Cursor(blob)
+    meta = read_metadata(c)
+    layers = [dict(active=c.read('i32'), buffers=[c.read('f32[]') for _ in range(STATE_BUFFERS)])
+              for _ in range(len(meta['neurons']) - 1)]
+    c.finish()
+    return meta, layers
+
+
+def encode_state(meta, layers):
+    values = dict(meta, version=1)
+    fields = [(tag, values[name]) for name, tag in STATE_HEADER]
+    for layer in layers:
+        fields.append(('i32', layer['active']))
+        fields.extend(('f32[]', b) for b in layer['buffers'])
+    return encode(*fields)
+
+
+def graph_bytes(nodes, constants, root):
+    """Cost-graph trailer: i32[] (op, a, b) per node, f64[] constants, i32 root."""
+    return encode(('i32[]', np.asarray(nodes, np.int32)), ('f64[]', constants), ('i32', root))
+
+
+# ----------------------------------------------------------------------------- events
+# Training event frames (cuda/cpde_server.cu:364-435): kind -> field table.
+_REPORT = (('completed', 'u64'), ('updates', 'u64'), ('after', 'i32'), ('values', 'f64[]'))
+_EVENTS = {2: _REPORT, 6: _REPORT + (('total', 'f64'),), 4: (('cost', 'u64'), ('outputs', 'f32[]'))}
+_LAYER_DIAGNOSTICS = (('sq', 'f64'), ('max', 'f64'), ('nonfinite', 'u64'), ('first', 'i32'))
+
+
+def _event(kind, c):
+    if kind in _EVENTS:
+        ev = {name: c.read(tag) for name, tag in _EVENTS[kind]}
+    elif kind == 3:
+        return dict(kind=3, blob=c.rest())
+    elif kind == 5:
+        ev = dict(epoch=c.read('u64'), updates=c.read('u64'))
+        ev['layers'] = [{name: c.read(tag) for name, tag in _LAYER_DIAGNOSTICS} for _ in range(c.read('i32'))]
+    else:
+        raise RuntimeError(f'unexpected training event {kind}')
+    c.finish()
+    ev['kind'] = kind
+    return ev
+
 
 class ServerError(RuntimeError):
     """A kind-1 reply: a validation or numerical error; the server stays usable.
@@ -37,102 +192,6 @@ class ServerError(RuntimeError):
     def __init__(self, message, events=()):
         super().__init__(message)
         self.events = list(events)
-
-
-class Writer:
-    def __init__(self):
-        self.parts = []
-
-    def put(self, fmt, value):
-        self.parts.append(struct.pack('<' + fmt, value))
-        return self
-
-    def array(self, value, dtype):
-        a = np.ascontiguousarray(value, dtype=np.dtype(dtype).newbyteorder('<'))
-        self.put('Q', a.size)
-        self.parts.append(a.tobytes())
-        return self
-
-    def string(self, value):
-        b = value.encode('utf-8') if isinstance(value, str) else bytes(value)
-        self.put('Q', len(b))
-        self.parts.append(b)
-        return self
-
-    def raw(self, b):
-        self.parts.append(bytes(b))
-        return self
-
-    def bytes(self):
-        return b''.join(self.parts)
-
-
-class Reader:
-    def __init__(self, data):
-        self.data, self.pos = data, 0
-
-    def take(self, n):
-        if self.pos + n > len(self.data):
-            raise RuntimeError('truncated response')
-        v = self.data[self.pos:self.pos + n]
-        self.pos += n
-        return v
-
-    def get(self, fmt):
-        return struct.unpack('<' + fmt, self.take(struct.calcsize('<' + fmt)))[0]
-
-    def array(self, dtype):
-        dt = np.dtype(dtype).newbyteorder('<')
-        n = self.get('Q')
-        return np.frombuffer(self.take(n * dt.itemsize), dtype=dt).copy()
-
-    def string(self):
-        return self.take(self.get('Q')).decode('utf-8', 'replace')
-
-    def end(self):
-        if self.pos != len(self.data):
-            raise RuntimeError('unexpected response fields')
-
-
-def decode_metadata(r):
-    """State blob header (cuda/cpde_server.cu:193-198)."""
-    if r.get('I') != 1:
-        raise ValueError('unsupported state version')
-    neurons, linear = r.array('i4').tolist(), r.array('i4').tolist()
-    return dict(neurons=neurons, linear=linear, optimizer=r.get('i'), updates=r.get('Q'),
-                adam_step=r.get('Q'), stage_done=r.get('Q'), remaining=r.get('Q'),
-                learning_rate=r.get('f'), initial_step=r.get('f'), stage=r.string())
-
-
-def decode_state(blob):
-    """Full snapshot blob: metadata, then per layer ``i32 act_grad`` and four f32
-    buffers W, G1, G2, step (cuda/cpde_server.cu:199-206)."""
-    r = Reader(blob)
-    meta = decode_metadata(r)
-    layers = []
-    for _ in range(len(meta['neurons']) - 1):
-        active = r.get('i')
-        layers.append(dict(active=active, buffers=[r.array('f4') for _ in range(4)]))
-    r.end()
-    return meta, layers
-
-
-def encode_state(meta, layers):
-    w = Writer().put('I', 1).array(meta['neurons'], 'i4').array(meta['linear'], 'i4')
-    w.put('i', meta['optimizer'])
-    for key in ('updates', 'adam_step', 'stage_done', 'remaining'):
-        w.put('Q', meta[key])
-    w.put('f', meta['learning_rate']).put('f', meta['initial_step']).string(meta['stage'])
-    for layer in layers:
-        w.put('i', layer['active'])
-        for b in layer['buffers']:
-            w.array(b, 'f4')
-    return w.bytes()
-
-
-def graph_bytes(nodes, constants, root):
-    """Cost-graph trailer: i32[] (op,a,b) per node, f64[] constants, i32 root."""
-    return Writer().array(np.asarray(nodes, np.int32).ravel(), 'i4').array(constants, 'f8').put('i', root).bytes()
 
 
 class Session:
@@ -149,8 +208,8 @@ class Session:
         threading.Thread(target=self._drain_out, daemon=True).start()
         self.closed = False
         r = self.request(1)
-        self.protocol, self.version, self.capabilities = r.string(), r.get('i'), r.get('I')
-        r.end()
+        self.protocol, self.version, self.capabilities = r.read_all('str', 'i32', 'u32')
+        r.finish()
 
     # ----------------------------------------------------------------- transport
     def _drain_err(self):
@@ -158,28 +217,28 @@ class Session:
             self.stderr_lines.append(line.decode('utf-8', 'replace').rstrip())
 
     def _read_exact(self, n):
-        chunks = []
-        while n:
-            part = self.proc.stdout.read(n)
-            if not part:
+        buf = bytearray(n)
+        view, got = memoryview(buf), 0
+        while got < n:
+            k = self.proc.stdout.readinto(view[got:])
+            if not k:
                 raise RuntimeError('server stopped: ' + '\n'.join(self.stderr_lines))
-            chunks.append(part)
-            n -= len(part)
-        return b''.join(chunks)
+            got += k
+        return bytes(buf)
 
     def _drain_out(self):
         try:
             while True:
-                size = struct.unpack('<Q', self._read_exact(8))[0]
-                if not 4 <= size <= 4 * 1024 ** 3:
+                size = _COUNT.unpack(self._read_exact(_COUNT.size))[0]
+                if not 4 <= size <= MAX_FRAME:
                     raise RuntimeError('invalid response frame')
                 payload = self._read_exact(size)
-                self._responses.put((struct.unpack_from('<I', payload)[0], Reader(payload[4:])))
+                self._responses.put((_FIXED['u32'].unpack_from(payload)[0], Cursor(payload[4:])))
         except BaseException as e:  # noqa: BLE001 - surfaced to the waiting request
             self._responses.put(e)
 
     def send(self, op, body=b''):
-        frame = struct.pack('<QI', len(body) + 4, op) + body
+        frame = FRAME_HEAD.pack(len(body) + 4, op) + bytes(body)
         view = memoryview(frame)
         while view:
             n = self.proc.stdin.write(view)
@@ -199,14 +258,22 @@ class Session:
         return v
 
     def request(self, op, body=b''):
+        """Send one request; the reply's Cursor (kind 0), or ServerError (kind 1)."""
         with self._lock:
             self.send(op, body)
             kind, r = self.receive()
             if kind == 1:
-                raise ServerError(r.string())
+                raise ServerError(r.read('str'))
             if kind != 0:
                 raise RuntimeError(f'unexpected response kind {kind}')
             return r
+
+    def call(self, op, fields, *reply):
+        """A request from ``fields`` whose reply is exactly the ``reply`` tags."""
+        r = self.request(op, encode(*fields))
+        out = r.read_all(*reply)
+        r.finish()
+        return out[0] if len(out) == 1 else out
 
     def close(self):
         if self.closed:
@@ -239,109 +306,75 @@ class Session:
         a = np.asarray(samples, np.float32)
         t = np.asarray(table, np.int32)
         d, h, w = a.shape
-        body = Writer().put('i', d).put('i', h).put('i', w).put('i', t.shape[1] - 1)
-        body.array(t, 'i4').array(a.transpose(0, 2, 1), 'f4')
-        r = self.request(2, body.bytes())
-        i = r.get('Q')
-        r.end()
-        return i
+        return self.call(2, [('i32', d), ('i32', h), ('i32', w), ('i32', t.shape[1] - 1), ('i32[]', t),
+                             ('f32[]', a.transpose(0, 2, 1))], 'u64')
 
     def network(self, neurons, linear, weights):
         """op 3. ``weights[l]`` is n_out x (n_in+1) column-major with the bias last."""
-        body = Writer().array(neurons, 'i4').array(linear, 'i4')
-        for w in weights:
-            body.array(np.asarray(w, np.float32).ravel(), 'f4')
-        r = self.request(3, body.bytes())
-        i = r.get('Q')
-        r.end()
-        return i
+        fields = [('i32[]', neurons), ('i32[]', linear)] + [('f32[]', w) for w in weights]
+        return self.call(3, fields, 'u64')
 
     def eval(self, net, data, chunk=0):
-        r = self.request(4, Writer().put('Q', net).put('Q', data).put('i', chunk).bytes())
-        i = r.get('Q')
-        r.end()
-        return i
+        return self.call(4, [('u64', net), ('u64', data), ('i32', chunk)], 'u64')
 
     def download(self, data):
         """op 5: the whole storage, [row][sample][channel] flattened."""
-        r = self.request(5, Writer().put('Q', data).bytes())
-        a = r.array('f4')
-        r.end()
-        return a
+        return self.call(5, [('u64', data)], 'f32[]')
 
     def download_shaped(self, data, rows, channels, samples):
         return self.download(data).reshape(rows, samples, channels).transpose(0, 2, 1)
 
     def replace(self, data, samples):
         a = np.asarray(samples, np.float32)
-        self.request(6, Writer().put('Q', data).array(a.transpose(0, 2, 1), 'f4').bytes()).end()
+        self.call(6, [('u64', data), ('f32[]', a.transpose(0, 2, 1))])
 
     def matching_cost(self, net, inputs, targets, rows, target_rows, weights, weight_samples=1, chunk=0):
         """op 7 kind 0.  ``weights`` is (rows, weight_samples, outputs)."""
-        body = Writer().put('Q', net).put('Q', inputs).put('Q', targets).put('i', 0).put('i', chunk)
-        body.array(rows, 'i4').array(target_rows, 'i4').put('i', weight_samples)
-        body.array(np.asarray(weights, np.float32).ravel(), 'f4')
-        r = self.request(7, body.bytes())
-        i = r.get('Q')
-        r.end()
-        return i
+        return self.call(7, [('u64', net), ('u64', inputs), ('u64', targets), ('i32', 0), ('i32', chunk),
+                             ('i32[]', rows), ('i32[]', target_rows), ('i32', weight_samples),
+                             ('f32[]', weights)], 'u64')
 
     def polynomial_cost(self, net, inputs, rows, equations, terms, coeffs, rhs, weights, chunk=0):
         """op 7 kind 1: sparse linear/quadratic residuals."""
-        body = Writer().put('Q', net).put('Q', inputs).put('Q', 0).put('i', 1).put('i', chunk)
-        body.array(rows, 'i4').put('i', equations).array(np.asarray(terms, np.int32).ravel(), 'i4')
-        body.array(coeffs, 'f4').array(rhs, 'f4').array(weights, 'f4')
-        r = self.request(7, body.bytes())
-        i = r.get('Q')
-        r.end()
-        return i
+        return self.call(7, [('u64', net), ('u64', inputs), ('u64', 0), ('i32', 1), ('i32', chunk),
+                             ('i32[]', rows), ('i32', equations), ('i32[]', terms), ('f32[]', coeffs),
+                             ('f32[]', rhs), ('f32[]', weights)], 'u64')
 
     def integral_cost(self, net, inputs, nodes, constants, fields, quadrature_weights, chunk=0):
         """op 12: expression IR (op,a,b) with double constants; ``fields`` is
         (F, samples) double; returns the cost id."""
         f = np.asarray(fields, np.float64)
         qw = np.asarray(quadrature_weights, np.float64)
-        samples = qw.size
-        body = Writer().put('Q', net).put('Q', inputs).put('i', chunk).put('i', samples)
-        body.array(np.asarray(nodes, np.int32).ravel(), 'i4').array(constants, 'f8')
-        body.put('i', f.shape[0] if f.size else 0).array(f.ravel(), 'f8').array(qw, 'f8')
-        r = self.request(12, body.bytes())
-        i = r.get('Q')
-        r.end()
-        return i
+        return self.call(12, [('u64', net), ('u64', inputs), ('i32', chunk), ('i32', qw.size),
+                              ('i32[]', np.asarray(nodes, np.int32)), ('f64[]', constants),
+                              ('i32', f.shape[0] if f.size else 0), ('f64[]', f), ('f64[]', qw)], 'u64')
 
     def inspect(self, cost, compile=False):
-        r = self.request(13, Writer().put('Q', cost).put('i', int(compile)).bytes())
-        src, log = r.string(), r.string()
-        r.end()
-        return src, log
+        return self.call(13, [('u64', cost), ('i32', int(compile))], 'str', 'str')
 
     def graph_eval(self, net, costs, graph, gradient=False, layers=0):
-        body = Writer().put('Q', net).array(costs, 'u8').put('i', int(gradient)).raw(graph)
-        r = self.request(14, body.bytes())
-        value = r.get('d')
-        grads = None
-        if gradient:
-            grads = [r.array('f4') for _ in range(r.get('i'))]
-        r.end()
+        r = self.request(14, encode(('u64', net), ('u64[]', costs), ('i32', int(gradient)), ('raw', graph)))
+        value = r.read('f64')
+        grads = [r.read('f32[]') for _ in range(r.read('i32'))] if gradient else None
+        r.finish()
         return value, grads
 
     def snapshot(self, net):
-        return self.request(9, Writer().put('Q', net).bytes()).data
+        return self.request(9, encode(('u64', net))).rest()
 
     def restore(self, net, blob):
-        self.request(10, Writer().put('Q', net).raw(blob).bytes()).end()
+        self.call(10, [('u64', net), ('raw', blob)])
 
     def close_object(self, kind, ident):
-        self.request(11, Writer().put('i', kind).put('Q', ident).bytes()).end()
+        self.call(11, [('i32', kind), ('u64', ident)])
 
     def timing(self, net, cost, warm=20, iterations=100, batches=7, layers=0):
         """op 90 (benchmark command): returns wall ms, device ms, loss, gradients."""
-        body = Writer().put('Q', net).put('Q', cost).put('i', warm).put('i', iterations).put('i', batches)
-        r = self.request(90, body.bytes())
-        wall, gpu, loss = r.array('f8'), r.array('f8'), r.get('d')
-        grads = [r.array('f4') for _ in range(layers)]
-        r.end()
+        r = self.request(90, encode(('u64', net), ('u64', cost), ('i32', warm), ('i32', iterations),
+                                    ('i32', batches)))
+        wall, gpu, loss = r.read_all('f64[]', 'f64[]', 'f64')
+        grads = [r.read('f32[]') for _ in range(layers)]
+        r.finish()
         return dict(wall_ms=wall, gpu_ms=gpu, loss=loss, gradients=grads)
 
     def train(self, net, costs, epochs, method=0, fresh=0, steps=0.0, moments=0, lr=0.0, verbose=0,
@@ -350,46 +383,26 @@ class Session:
         """op 8 (or op 15 with a graph).  Returns the event list and final result.
         ``on_event(session, event)`` is called for every event frame as it
         arrives (e.g. to send op 99 from there)."""
-        w = Writer().put('Q', net).array(costs, 'u8').put('Q', epochs).put('i', method).put('i', fresh)
-        w.put('f', steps).put('i', moments).put('f', lr)
-        for v in (verbose, log, eval_every, outputs, save):
-            w.put('i', v)
-        w.string(stage).put('i', diagnostics)
+        fields = [('u64', net), ('u64[]', costs), ('u64', epochs), ('i32', method), ('i32', fresh), ('f32', steps),
+                  ('i32', moments), ('f32', lr), ('i32', verbose), ('i32', log), ('i32', eval_every),
+                  ('i32', outputs), ('i32', save), ('str', stage), ('i32', diagnostics)]
         if graph is not None:
-            w.raw(graph)
+            fields.append(('raw', graph))
         if restore_every:
-            w.put('Q', restore_every).put('f', restore_step)
+            fields += [('u64', restore_every), ('f32', restore_step)]
         events = []
         with self._lock:
-            self.send(15 if graph is not None else 8, w.bytes())
+            self.send(15 if graph is not None else 8, encode(*fields))
             while True:
                 kind, r = self.receive()
                 if kind == 1:
-                    raise ServerError(r.string(), events)
-                if kind in (2, 6):
-                    ev = dict(kind=kind, completed=r.get('Q'), updates=r.get('Q'), after=r.get('i'),
-                              values=r.array('f8'))
-                    if kind == 6:
-                        ev['total'] = r.get('d')
-                    r.end()
-                elif kind == 3:
-                    ev = dict(kind=3, blob=r.data)
-                elif kind == 4:
-                    ev = dict(kind=4, cost=r.get('Q'), outputs=r.array('f4'))
-                    r.end()
-                elif kind == 5:
-                    ev = dict(kind=5, epoch=r.get('Q'), updates=r.get('Q'))
-                    n = r.get('i')
-                    ev['layers'] = [dict(sq=r.get('d'), max=r.get('d'), nonfinite=r.get('Q'), first=r.get('i'))
-                                    for _ in range(n)]
-                    r.end()
-                elif kind == 0:
-                    completed, stopped = r.get('Q'), r.get('i')
-                    meta = decode_metadata(Reader(r.take(r.get('Q'))))
-                    r.end()
+                    raise ServerError(r.read('str'), events)
+                if kind == 0:
+                    completed, stopped = r.read_all('u64', 'i32')
+                    meta = read_metadata(Cursor(r.blob(r.read('u64'))))
+                    r.finish()
                     return dict(completed=completed, stopped=stopped, metadata=meta, events=events)
-                else:
-                    raise RuntimeError(f'unexpected training event {kind}')
+                ev = _event(kind, r)
                 events.append(ev)
                 if on_event is not None:
                     on_event(self, ev)

@@ -14,10 +14,7 @@ The named workloads are:
   * ``poisson_disk``: 2->64^3->1, 64 Gauss-Legendre radii x 64 angles interior
     quadrature plus 256 boundary points, residual u_xx+u_yy+f;
   * ``fourier_3d``: 3->128^5->1 on a 32^3 grid, all mixed partials through order 4;
-  * ``fourier_large``: 2->256^4->1 on a 512x512 grid, order 6, chunked;
-  * ``reference_benchmark(order)``: the reference's published Fourier benchmark
-    workload (scripts/benchmark_fourier_performance.py:20-38 and the Python
-    initialiser cpde/api.py:277-280), used to pin the published losses.
+  * ``fourier_large``: 2->256^4->1 on a 512x512 grid, order 6, chunked.
 """
 from __future__ import annotations
 
@@ -70,15 +67,6 @@ def xavier_weights(neurons, seed=3407):
     return out
 
 
-def reference_init(neurons, seed):
-    """The reference Python initialiser: U(+-2/sqrt(fan_in)) weights column-major,
-    then U(+-0.1) biases (cpde/api.py:277-280)."""
-    rng = np.random.default_rng(seed)
-    return [np.concatenate((rng.uniform(-2 / np.sqrt(w), 2 / np.sqrt(w), h * w),
-                            rng.uniform(-.1, .1, h))).astype(np.float32)
-            for w, h in zip(neurons, neurons[1:])]
-
-
 def linear_flags(neurons):
     return [1] + [0] * (len(neurons) - 2) + [1]
 
@@ -114,22 +102,48 @@ def uniform_grid(n, dims):
 
 
 class MatchingWorkload:
-    """Everything a matching-cost run needs, in protocol layouts."""
+    """Everything a matching-cost run needs, in protocol layouts.
 
-    def __init__(self, name, neurons, points, schema, target, weights, init, chunk=0):
+    ``schema`` holds the data's derivative rows and ``rows`` the cost's rows,
+    as indices into it (default: all; the network runs on schema[rows]).
+    ``target`` holds the rows of the target data object, whose derivative rows
+    are ``target_schema`` (default ``schema``), and ``target_rows`` names the
+    target row of each cost row (default: the same index).  ``weights`` is one
+    weight per cost row, shape (R,), or one per cost row and sample, shape
+    (R, points) (the [R][P][1] form, weight_samples = P).  ``linear`` flags
+    each layer (default: linear input and output, sigmoid hidden layers)."""
+
+    def __init__(self, name, neurons, points, schema, target, weights, init, chunk=0, linear=None, rows=None,
+                 target_schema=None, target_rows=None):
         self.name, self.neurons = name, list(neurons)
-        self.linear = linear_flags(neurons)
+        self.linear = linear_flags(neurons) if linear is None else [int(v) for v in linear]
         self.points = np.asarray(points, np.float32)
-        self.schema = schema
-        self.inputs = input_stack(self.points, schema)
-        self.target = np.asarray(target, np.float32)            # (rows, points)
-        self.row_weights = np.asarray(weights, np.float32)      # (rows,)
+        self.schema = np.asarray(schema, np.int32)
+        self.inputs = input_stack(self.points, self.schema)
+        self.cost_rows = np.arange(len(self.schema), dtype=np.int32) if rows is None else np.asarray(rows, np.int32)
+        self.target = np.asarray(target, np.float32)            # (target rows, points)
+        self.target_schema = self.schema if target_schema is None else np.asarray(target_schema, np.int32)
+        self.target_rows = self.cost_rows.copy() if target_rows is None else np.asarray(target_rows, np.int32)
+        self.row_weights = np.asarray(weights, np.float32)      # (R,) or (R, points)
         self.init = init
         self.chunk = chunk
 
     @property
     def rows(self):
-        return len(self.schema)
+        """Rows of the cost (the network's derivative rows)."""
+        return len(self.cost_rows)
+
+    @property
+    def cost_schema(self):
+        return self.schema[self.cost_rows]
+
+    @property
+    def weight_samples(self):
+        return 1 if self.row_weights.ndim == 1 else self.row_weights.shape[1]
+
+    def weight_block(self):
+        """The weights as the wire sends them: [R][weight_samples][outputs=1]."""
+        return self.row_weights.reshape(self.rows, self.weight_samples, 1)
 
     @property
     def size(self):
@@ -151,20 +165,25 @@ class MatchingWorkload:
         params = sum(b * (a + 1) for a, b in zip(self.neurons, self.neurons[1:]))
         return 4 * rp * (5 * hidden + 3 * self.neurons[-1]) + 28 * params
 
+    def points_slice(self, idx, name=None):
+        """The same workload (network, rows, row weights) on the points ``idx``,
+        unchunked; per-sample weights follow their points."""
+        idx = np.asarray(idx)
+        weights = self.row_weights if self.weight_samples == 1 else self.row_weights[:, idx]
+        return MatchingWorkload(name or f'{self.name}[{len(idx)} points]', self.neurons, self.points[idx],
+                                self.schema, self.target[:, idx], weights, self.init, linear=self.linear,
+                                rows=self.cost_rows, target_schema=self.target_schema, target_rows=self.target_rows)
+
     def subset(self, count):
-        """The same workload on `count` evenly spaced points (same network,
-        weights, row weights and targets), unchunked."""
-        idx = np.linspace(0, self.size - 1, count).astype(int)
-        return MatchingWorkload(f'{self.name}[{count} points]', self.neurons, self.points[idx], self.schema,
-                                self.target[:, idx], self.row_weights, self.init)
+        """The same workload on `count` evenly spaced points, unchunked."""
+        return self.points_slice(np.linspace(0, self.size - 1, count).astype(int))
 
     def upload(self, session, chunk=None):
         """Creates data, target, network and cost objects; returns their ids."""
         d = session.data(self.inputs, self.schema)
-        t = session.data(self.target[:, None, :], self.schema)
+        t = session.data(self.target[:, None, :], self.target_schema)
         n = session.network(self.neurons, self.linear, self.init)
-        rows = list(range(self.rows))
-        c = session.matching_cost(n, d, t, rows, rows, self.row_weights[:, None, None], 1,
+        c = session.matching_cost(n, d, t, self.cost_rows, self.target_rows, self.weight_block(), self.weight_samples,
                                   self.chunk if chunk is None else chunk)
         return dict(data=d, target=t, net=n, cost=c)
 
@@ -199,35 +218,6 @@ def fourier_large(grid=512, order=6, neurons=(2, 256, 256, 256, 256, 1), modes=1
     target = fourier_target(pts, schema, freq, coef, phase)
     return MatchingWorkload('fourier_large_order6', neurons, pts, schema, target, 1.0 / target.var(axis=1),
                             xavier_weights(neurons), chunk=min(chunk, len(pts)))
-
-
-def reference_benchmark(order):
-    """The published benchmark workload: 27x27 grid in [-1,1]^2, 10x10 Fourier
-    coefficient grid (seed 2026), rows weighted by 1/var, reference initialiser
-    with seed 3407 (scripts/benchmark_fourier_performance.py:20-57)."""
-    neurons = [2, 128, 128, 128, 128, 1]
-    schema = closed_schema(2, [(i, order - i) for i in range(order + 1)])
-    x, y = np.meshgrid(np.linspace(-1, 1, 27), np.linspace(-1, 1, 27), indexing='ij')
-    pts = np.column_stack((x.ravel(), y.ravel())).astype(np.float32)
-    xd, yd = pts.astype(float).T
-    coef = np.random.default_rng(2026).uniform(-1, 1, (4, 10, 10))
-    target = np.zeros((len(schema), len(pts)))
-    for row, (_, dx, dy) in enumerate(schema):
-        for n in range(1, 11):
-            for k in range(1, 11):
-                a, b, c, d = coef[:, n - 1, k - 1] * n ** int(dx) * k ** int(dy) / (n * k)
-                sx, cx = np.sin(n * xd + dx * np.pi / 2), np.cos(n * xd + dx * np.pi / 2)
-                sy, cy = np.sin(k * yd + dy * np.pi / 2), np.cos(k * yd + dy * np.pi / 2)
-                target[row] += a * sx * sy + b * sx * cy + c * cx * sy + d * cx * cy
-    weights = (1 / target.std(axis=1) ** 2).astype(np.float32)
-    return MatchingWorkload(f'reference_fourier_order{order}', neurons, pts, schema, target.astype(np.float32),
-                            weights, reference_init(neurons, 3407))
-
-
-# Published losses at initial weights for reference_benchmark(order), RTX 3090 CUDA
-# build (docs/benchmarks/fourier-rtx3090.json:159,189,219,249,279,309,339).
-PUBLISHED_LOSSES = [1519.6657229734592, 2989.1356939971447, 5187.967334091663, 8111.595301151276,
-                    11767.45415353775, 16145.947476387024, 21259.16511631012]
 
 
 # ----------------------------------------------------------------------------- Poisson

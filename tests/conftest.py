@@ -5,7 +5,7 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
-for p in (ROOT, ROOT / 'oracle'):
+for p in (ROOT, ROOT / 'oracle', ROOT / 'tests' / 'golden'):
     if str(p) not in sys.path:
         sys.path.insert(0, str(p))
 

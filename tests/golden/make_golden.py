@@ -26,8 +26,10 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parents[1]
 sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(HERE))
 
 from cpde_amd import wire, workloads as W  # noqa: E402
+from published_workload import PUBLISHED_LOSSES, reference_benchmark  # noqa: E402
 
 SERVER = ROOT / 'oracle' / '_ref' / 'cpde_cpu_server'
 SINGLE_LEAF = wire.graph_bytes([(1, 0, 0)], [0.0], 0)
@@ -148,14 +150,14 @@ def case_large_reduced(s):
 def case_published(s):
     losses = []
     for order in range(7):
-        wl = W.reference_benchmark(order)
+        wl = reference_benchmark(order)
         ids = wl.upload(s, 0)
         value, _ = s.graph_eval(ids['net'], [ids['cost']], SINGLE_LEAF, gradient=False)
         losses.append(value)
         for kind, key in ((2, 'cost'), (1, 'net'), (0, 'data'), (0, 'target')):
             s.close_object(kind, ids[key])
     return dict(published_losses=np.asarray(losses, np.float64),
-                published_reference=np.asarray(W.PUBLISHED_LOSSES, np.float64))
+                published_reference=np.asarray(PUBLISHED_LOSSES, np.float64))
 
 
 def case_poisson(s):
@@ -451,6 +453,165 @@ def case_poisson_full(s):
     return rec
 
 
+def closure_indices(schema, requested):
+    """Indices into ``schema`` of the closure of the requested count tuples."""
+    keys = [tuple(r[1:]) for r in schema]
+    return np.array([keys.index(tuple(r[1:])) for r in W.closed_schema(schema.shape[1] - 1, requested)], np.int32)
+
+
+def form_workload(order, points, seed, neurons, requested=None, reverse_target=False, per_sample=False, chunk=0):
+    """A matching workload on random points of [0,1]^2: data with the full
+    schema of ``order``; the cost over the closure of ``requested`` (default:
+    every row); targets in a data object whose rows are reversed when
+    ``reverse_target``; one weight per row (1/var) or, with ``per_sample``,
+    per row and sample, U(0.2, 1.5) with a fifth of them zero."""
+    schema = W.full_schema(2, order)
+    rng = np.random.default_rng(seed)
+    pts = rng.uniform(0, 1, (points, 2))
+    freq, coef, phase = W.fourier_modes(2, 3, 3, seed)
+    target = W.fourier_target(pts, schema, freq, coef, phase)
+    rows = np.arange(len(schema), dtype=np.int32) if requested is None else closure_indices(schema, requested)
+    perm = np.arange(len(schema))[::-1] if reverse_target else np.arange(len(schema))
+    target_rows = np.array([int(np.flatnonzero(perm == r)[0]) for r in rows], np.int32)
+    if per_sample:
+        weights = rng.uniform(0.2, 1.5, (len(rows), points))
+        weights[rng.random(weights.shape) < 0.2] = 0
+    else:
+        weights = 1.0 / target[rows].var(axis=1)
+    return W.MatchingWorkload('form', neurons, pts, schema, target[perm], weights, W.xavier_weights(neurons, seed),
+                              chunk=chunk, rows=rows, target_schema=schema[perm], target_rows=target_rows)
+
+
+FORMS = {
+    # name: form_workload arguments
+    'persample': dict(order=6, points=30, seed=71, neurons=(2, 8, 8, 1), per_sample=True, chunk=7),
+    'subset': dict(order=2, points=40, seed=72, neurons=(2, 10, 9, 1), requested=[(2, 0)], reverse_target=True),
+    'subset_persample': dict(order=4, points=33, seed=73, neurons=(2, 9, 8, 1), requested=[(1, 2)],
+                             reverse_target=True, per_sample=True, chunk=9),
+}
+
+
+def workload_record(wl, prefix):
+    rec = {f'{prefix}_{k}': v for k, v in dict(
+        neurons=np.asarray(wl.neurons, np.int32), linear=np.asarray(wl.linear, np.int32), schema=wl.schema,
+        points=wl.points, target=wl.target, target_schema=wl.target_schema, rows=wl.cost_rows,
+        target_rows=wl.target_rows, weights=wl.row_weights, chunk=np.int32(wl.chunk)).items()}
+    for t, w in enumerate(wl.init):
+        rec[f'{prefix}_init{t}'] = np.asarray(w, np.float32)
+    return rec
+
+
+def epoch_record(s, wl, prefix, outputs=False):
+    """op 14 (value and gradient), optionally op 4 outputs, and the weights
+    after one RPROP epoch from a fresh state."""
+    rec = workload_record(wl, prefix)
+    ids = wl.upload(s)
+    value, grads = s.graph_eval(ids['net'], [ids['cost']], SINGLE_LEAF, gradient=True)
+    rec[f'{prefix}_loss'] = np.float64(value)
+    for t, g in enumerate(grads):
+        rec[f'{prefix}_grad{t}'] = g
+    if outputs:
+        out = s.eval(ids['net'], ids['data'], wl.chunk)
+        rec[f'{prefix}_outputs'] = s.download(out).reshape(len(wl.schema), wl.size, wl.neurons[-1])
+        s.close_object(0, out)
+    s.train(ids['net'], [ids['cost']], 1, method=0, fresh=1, log=1)
+    _, layers = wire.decode_state(s.snapshot(ids['net']))
+    for t, layer in enumerate(layers):
+        rec[f'{prefix}_after{t}'] = layer['buffers'][0]
+    for kind, key in ((2, 'cost'), (1, 'net'), (0, 'data'), (0, 'target')):
+        s.close_object(kind, ids[key])
+    return rec
+
+
+def case_matching_forms(s):
+    """Matching-cost requests the client sends (cpde/api.py:350-362) in forms the
+    other cases leave out, each as op 14 (value + gradient) and one RPROP
+    epoch:
+      * ``persample``: one weight per row and sample (weight_samples = P, the
+        [R][P][1] layout, cuda/cost_kernels.cuh:17-19), a fifth of them zero,
+        order 6 on 30 points in chunks of 7, so the sample index is offset + p;
+      * ``subset``: data with the full order-2 schema, a cost over the closure
+        of {xx} = rows (1, x, xx), not a prefix, and targets in a data object
+        whose rows run in reverse order, so target_rows remaps
+        (cuda/cost_kernels.cuh:20);
+      * ``subset_persample``: both at order 4, the closure of {x y^2}, chunks
+        of 9."""
+    rec = {}
+    for name, kwargs in FORMS.items():
+        rec.update(epoch_record(s, form_workload(**kwargs), name))
+    return rec
+
+
+LINEAR_HIDDEN = {
+    # name: (neurons, linear flags, order, points, chunk)
+    'inner': ((2, 8, 6, 8, 1), (1, 0, 1, 0, 1), 4, 25, 10),
+    'first': ((2, 10, 8, 1), (1, 1, 0, 1), 6, 20, 0),
+}
+
+
+def case_linear_hidden(s):
+    """Networks with linear hidden layers, which the client accepts
+    (cpde/api.py:270-272) and whose composition the reference skips
+    (cuda/cpde_engine.cuh:894-909,973-987): 2->8->6(linear)->8->1 at order 4
+    in chunks of 10, and 2->10(linear)->8->1 at order 6.  op 14 value and
+    gradient, outputs (op 4 + op 5) and one RPROP epoch."""
+    rec = {}
+    for name, (neurons, linear, order, points, chunk) in LINEAR_HIDDEN.items():
+        schema = W.full_schema(2, order)
+        rng = np.random.default_rng(81 + order)
+        pts = rng.uniform(0, 1, (points, 2))
+        freq, coef, phase = W.fourier_modes(2, 3, 3, 81 + order)
+        target = W.fourier_target(pts, schema, freq, coef, phase)
+        wl = W.MatchingWorkload(name, neurons, pts, schema, target, 1.0 / target.var(axis=1),
+                                W.xavier_weights(neurons, 81 + order), chunk=chunk, linear=linear)
+        rec.update(epoch_record(s, wl, name, outputs=True))
+    return rec
+
+
+def empty_integral_graphs():
+    """Graphs over leaf 0 (a sampled integral) and leaf 1 (an empty one):
+    ``constant``: leaf0 + 3 exp(leaf1), multipliers known; ``dependent``:
+    leaf0 * (leaf1 + 2), leaf 0's multiplier depends on leaf 1's value."""
+    constant = wire.graph_bytes([(1, 0, 0), (1, 1, 0), (9, 1, 0), (0, 0, 0), (5, 2, 3), (3, 0, 4)],
+                                [0.0, 0.0, 0.0, 3.0, 0.0, 0.0], 5)
+    dependent = wire.graph_bytes([(1, 0, 0), (1, 1, 0), (0, 0, 0), (3, 1, 2), (5, 0, 3)],
+                                 [0.0, 0.0, 2.0, 0.0, 0.0], 4)
+    return dict(constant=constant, dependent=dependent)
+
+
+def empty_integral_costs(s, vw, n, d):
+    """Leaf 0: u**2 over the variation workload's points in chunks of 5; leaf 1:
+    an empty integral (op 12 with samples = 0 and no input data,
+    cuda/cpde_server.cu:491-497), whose pass does nothing (:226), so its value
+    stays 0."""
+    leaf0 = s.integral_cost(n, d, *vw.FREE, np.zeros((0, len(vw.points))), vw.weights, chunk=5)
+    leaf1 = s.integral_cost(n, 0, [(0, 0, 0)], [1.0], np.zeros((0, 0)), np.zeros(0))
+    return [leaf0, leaf1]
+
+
+def case_empty_integral(s):
+    """An empty integral as a graph leaf: op 14 value and gradient of both
+    graphs of ``empty_integral_graphs`` and the state after two RPROP epochs
+    of the value-dependent one."""
+    vw = W.VariationWorkload()
+    rec = dict(neurons=np.asarray(vw.neurons, np.int32), points=vw.points, quadrature=vw.weights)
+    for t, w in enumerate(vw.init):
+        rec[f'init{t}'] = np.asarray(w, np.float32)
+    d = s.data(W.input_stack(vw.points, vw.schema), vw.schema)
+    n = s.network(vw.neurons, W.linear_flags(vw.neurons), vw.init)
+    leaves = empty_integral_costs(s, vw, n, d)
+    for name, graph in empty_integral_graphs().items():
+        value, grads = s.graph_eval(n, leaves, graph, gradient=True)
+        rec[f'{name}_value'] = np.float64(value)
+        for t, g in enumerate(grads):
+            rec[f'{name}_grad{t}'] = g
+    res = s.train(n, leaves, 2, method=0, fresh=1, log=1, graph=empty_integral_graphs()['dependent'])
+    rec['reports'] = np.asarray([(e['completed'], e['updates'], e['after'], *e['values'], e['total'])
+                                 for e in res['events'] if e['kind'] == 6], np.float64)
+    rec['state'] = np.frombuffer(s.snapshot(n), np.uint8)
+    return rec
+
+
 CASES = {
     'tiny_order6': case_tiny_order6,
     'tiny_3var_order4': case_tiny_3var_order4,
@@ -466,6 +627,9 @@ CASES = {
     'protocol': case_protocol,
     'variations': case_variations,
     'poisson_full': case_poisson_full,
+    'matching_forms': case_matching_forms,
+    'linear_hidden': case_linear_hidden,
+    'empty_integral': case_empty_integral,
 }
 
 

@@ -6,7 +6,9 @@ import pytest
 
 import oracle
 from cpde_amd import workloads as W
-from helpers import check_gradient, load_golden as load, rel_l2
+from helpers import check_gradient, golden_form, load_golden as load, oracle_epoch, rel_l2
+from published_workload import PUBLISHED_LOSSES, reference_benchmark
+
 
 def transitions(g):
     return len(g['neurons']) - 1
@@ -75,9 +77,27 @@ def test_published_losses():
     the reference CPU server, and the oracle, against the published CUDA losses
     (docs/benchmarks/fourier-rtx3090.json)."""
     g = load('published')
-    assert np.allclose(g['published_losses'], W.PUBLISHED_LOSSES, rtol=2e-8)
+    assert np.allclose(g['published_losses'], PUBLISHED_LOSSES, rtol=2e-8)
     for order in (0, 3):
-        wl = W.reference_benchmark(order)
+        wl = reference_benchmark(order)
         loss, _, _ = oracle.matching_epoch(wl.neurons, wl.linear, wl.init, wl.schema, wl.inputs.transpose(0, 2, 1),
                                            wl.target[:, :, None], wl.row_weights[:, None, None], outputs=False)
-        assert abs(loss / W.PUBLISHED_LOSSES[order] - 1) < 1e-6, order
+        assert abs(loss / PUBLISHED_LOSSES[order] - 1) < 1e-6, order
+
+
+@pytest.mark.parametrize('record,prefix', [('matching_forms', 'persample'), ('matching_forms', 'subset'),
+                                           ('matching_forms', 'subset_persample'), ('linear_hidden', 'inner'),
+                                           ('linear_hidden', 'first')])
+def test_cost_forms_against_reference_server(record, prefix):
+    """Per-sample matching weights, a non-prefix row subset with remapped
+    target rows, and linear hidden layers: the oracle's epoch against the
+    reference server's op-14 value and gradient (and op-4 outputs)."""
+    g = load(record)
+    wl = golden_form(g, prefix)
+    loss, grads, _ = oracle_epoch(wl)
+    assert abs(loss / g[f'{prefix}_loss'] - 1) < 1e-5
+    for t, grad in enumerate(grads):
+        assert rel_l2(grad, g[f'{prefix}_grad{t}']) < 1e-5, t
+    if f'{prefix}_outputs' in g:
+        out = oracle.forward(wl.neurons, wl.linear, wl.init, wl.schema, wl.inputs.transpose(0, 2, 1))
+        assert rel_l2(out, g[f'{prefix}_outputs']) < 1e-5

@@ -18,8 +18,8 @@ BAD_REQUESTS = [
     (4, struct.pack('<QQi', 5, 6, 0)),                # unknown handles
     (11, struct.pack('<iQ', 7, 1)),                   # invalid object kind
     (1, b'x'),                                        # trailing fields
-    (3, wire.Writer().array([2, 1], 'i4').array([0, 1], 'i4').bytes()),  # input layer not linear
-    (3, wire.Writer().array([2], 'i4').array([1], 'i4').bytes()),        # too few layers
+    (3, wire.encode(('i32[]', [2, 1]), ('i32[]', [0, 1]))),  # input layer not linear
+    (3, wire.encode(('i32[]', [2]), ('i32[]', [1]))),        # too few layers
 ]
 
 
