@@ -440,13 +440,14 @@ class MatchingRun:
         self.net = Net(device, wl.neurons, wl.linear, wl.init)
         self.samples = wl.size
         self.width = min(chunk or wl.chunk or wl.size, wl.size)
-        self.plan = Plan(self.net, wl.schema, self.width, True)
-        # wire layouts: data [rows][samples][channels]
+        self.plan = Plan(self.net, wl.cost_schema, self.width, True)
+        # wire layouts: data [rows][samples][channels], weights [R][weight_samples][outputs]
         self.data = Buffer.of(device, np.ascontiguousarray(wl.inputs.transpose(0, 2, 1), np.float32))
         self.target = Buffer.of(device, np.ascontiguousarray(wl.target[:, :, None], np.float32))
-        self.target_rows = Buffer.of(device, np.arange(wl.rows, dtype=np.int32))
-        self.weights = Buffer.of(device, np.ascontiguousarray(wl.row_weights, np.float32))
-        self.rows = np.arange(wl.rows, dtype=np.int32)
+        self.target_rows = Buffer.of(device, np.ascontiguousarray(wl.target_rows, np.int32))
+        self.weights = Buffer.of(device, np.ascontiguousarray(wl.weight_block(), np.float32))
+        self.weight_samples = wl.weight_samples
+        self.rows = np.ascontiguousarray(wl.cost_rows, np.int32)
         self._loaded = None
         device.costs_begin(1)
 
@@ -463,20 +464,18 @@ class MatchingRun:
                 self.plan.activate(self.data, self.samples, self.rows, offset, valid)
                 self._loaded = (offset, valid)
             last = offset + self.width >= self.samples
+            cost = (self.target, self.samples, self.target_rows, self.weights, self.weight_samples, offset, valid, 0,
+                    collect)
             if update and last and self.one_pass and not self.static_scratch:
-                self.plan.epoch_matching_rprop(self.target, self.samples, self.target_rows, self.weights, 1, offset,
-                                               valid, 0, collect, not first)
+                self.plan.epoch_matching_rprop(*cost, not first)
                 return
             if self.static_scratch:
-                self.plan.epoch_matching_static(self.target, self.samples, self.target_rows, self.weights, 1, offset,
-                                                valid, 0, collect, not first)
+                self.plan.epoch_matching_static(*cost, not first)
             elif self.one_pass:
-                self.plan.epoch_matching(self.target, self.samples, self.target_rows, self.weights, 1, offset, valid, 0,
-                                         collect, not first)
+                self.plan.epoch_matching(*cost, not first)
             else:
                 self.plan.forward()
-                self.plan.matching(self.target, self.samples, self.target_rows, self.weights, 1, offset, valid, 0,
-                                   collect, True)
+                self.plan.matching(*cost, True)
                 self.plan.backward(not first)
             first = False
         if update:

@@ -64,6 +64,23 @@ def golden_workload(g):
                               g['row_weights'], [g[f'init{t}'] for t in range(T)], chunk=int(g['chunk']))
 
 
+def golden_form(g, prefix):
+    """MatchingWorkload of a record written by make_golden.workload_record."""
+    T = len(g[f'{prefix}_neurons']) - 1
+    return W.MatchingWorkload(prefix, list(g[f'{prefix}_neurons']), g[f'{prefix}_points'], g[f'{prefix}_schema'],
+                              g[f'{prefix}_target'], g[f'{prefix}_weights'], [g[f'{prefix}_init{t}'] for t in range(T)],
+                              chunk=int(g[f'{prefix}_chunk']), linear=g[f'{prefix}_linear'], rows=g[f'{prefix}_rows'],
+                              target_schema=g[f'{prefix}_target_schema'], target_rows=g[f'{prefix}_target_rows'])
+
+
+def oracle_epoch(wl, outputs=False):
+    """The oracle's epoch of a MatchingWorkload: loss, gradients, outputs."""
+    import oracle
+    return oracle.matching_epoch(wl.neurons, wl.linear, wl.init, wl.cost_schema, wl.inputs.transpose(0, 2, 1),
+                                 wl.target[:, :, None], wl.weight_block(), chunk=wl.chunk, rows=wl.cost_rows,
+                                 target_rows=wl.target_rows, weight_samples=wl.weight_samples, outputs=outputs)
+
+
 def check_gradient(g, t, grad, tol):
     """Relative L2 of a transition's gradient against the record (full vector,
     or its probe projections and norm)."""

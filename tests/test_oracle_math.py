@@ -146,6 +146,35 @@ def test_matching_cost_direct():
     assert (bs, bc) == (offset + 1, -1)
 
 
+def test_matching_cost_per_sample_weights_direct():
+    """The [R][P][outputs] weight layout (weight_samples = P): the weight of
+    (row d, chunk lane p, output o) is weights[d][offset + p][o] -- the sample
+    index, not the lane -- and a zero weight drops the term and its gradient.
+    Two outputs so that a swapped (sample, output) index also fails."""
+    rng = np.random.default_rng(6)
+    R, width, valid, samples, offset, outputs = 3, 5, 4, 11, 6, 2
+    y = rng.standard_normal((R, width, outputs)).astype(np.float32)
+    target = rng.standard_normal((R + 2, samples, outputs)).astype(np.float32)
+    trows = np.array([4, 0, 2], np.int32)
+    w = rng.uniform(0.5, 2.0, (R, samples, outputs)).astype(np.float32)
+    w[1, offset + 2, 0] = 0
+    w[:, offset + 1, :] = 0
+    loss, g, bs, bc = oracle.matching(y, target, trows, w, samples, width, valid, offset, samples)
+    ws = w[:, offset:offset + valid, :].astype(np.float64)
+    r = y[:, :valid, :].astype(np.float64) - target[trows, offset:offset + valid, :]
+    assert np.isclose(loss, np.sum(ws * r ** 2), rtol=1e-6)
+    assert np.allclose(g[:, :valid, :], 2 * ws * r, rtol=1e-6)
+    assert g[1, 2, 0] == 0 and np.all(g[:, 1, :] == 0) and np.all(g[:, valid:, :] == 0)
+    # a lane-indexed weight (wp = p instead of offset + p) gives another loss
+    lane = w[:, :valid, :].astype(np.float64)
+    assert not np.isclose(loss, np.sum(lane * r ** 2), rtol=1e-3)
+    assert bs == 0x7fffffff
+    # the first bad component of the first bad sample: (row 2, output 1) at lane 3
+    y[2, 3, 1] = np.inf
+    _, _, bs, bc = oracle.matching(y, target, trows, w, samples, width, valid, offset, samples)
+    assert (bs, bc) == (offset + 3, -1)
+
+
 def test_rprop_known_answers():
     # bound rejection: w=19, step=100, previous -1, current gradient of (w-100)^2
     W_, S, ga, gi = oracle.rprop([19.0], [100.0], [2 * (19 - 100)], [-1.0])
