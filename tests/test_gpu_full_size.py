@@ -1,5 +1,12 @@
-"""Full-size checks of the two largest workloads, through properties that need
-no full-size CPU reference:
+"""Full-size checks of the two largest workloads:
+
+  * against the reference CPU server at full size (tests/golden/
+    make_full_size.py): the epoch's loss (relative 1e-4), every weight
+    gradient (relative L2 1e-3, on probe projections and the norm for the
+    large blocks) and the derivative outputs at 64 sampled points (relative L2
+    per row 1e-3);
+
+and through properties that need no full-size CPU reference:
 
   * 2->256x4->1 sigmoid, order 6 (28 rows), 262,144 points in 65,536-point
     chunks, and 3->128x5->1 sigmoid, order 4 (35 rows), 32,768 points;
@@ -15,9 +22,34 @@ import pytest
 
 import oracle
 from cpde_amd import hip, workloads as W
-from helpers import rel_l2
+from helpers import check_gradient, load_golden, rel_l2
 
 pytestmark = pytest.mark.gpu
+
+FULL = {'3d_order4': ('fourier3d_full', W.fourier_3d), 'large_order6': ('large_full', W.fourier_large)}
+
+
+@pytest.mark.parametrize('name', list(FULL))
+def test_full_size_epoch_against_reference_server(device, name):
+    record, make = FULL[name]
+    g = load_golden(record)
+    wl = make()
+    print(f'[case] {wl.name} neurons={wl.neurons} R={wl.rows} P={wl.size} chunk={wl.chunk}', flush=True)
+    run = hip.MatchingRun(device, wl)
+    run.step()
+    device.synchronize()
+    loss = run.loss()
+    rel = abs(loss / g['loss'] - 1)
+    print(f'[result] loss {loss!r} reference {float(g["loss"])!r} rel {rel:.2e}', flush=True)
+    assert rel < 1e-4
+    for t, grad in enumerate(run.gradients()):
+        err = check_gradient(g, t, grad, 1e-3)
+        print(f'[result] transition {t} gradient rel-L2 {err:.2e}', flush=True)
+    run.close()
+    got = sampled_outputs(device, wl, g['sampled'])
+    worst = max(rel_l2(got[r], g['outputs'][r]) for r in range(wl.rows))
+    print(f'[result] worst sampled output row rel-L2 {worst:.2e}', flush=True)
+    assert worst < 1e-3
 
 
 def sampled_outputs(device, wl, idx):
