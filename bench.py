@@ -53,13 +53,20 @@ MFMA_KINDS = {'gemm_forward', 'gemm_transposed', 'gemm_wgrad', 'fused_forward', 
 CPU_SAMPLE_MACS = 3.0e9
 
 # HBM bytes per launch from rocprofv3 counter passes over this benchmark
-# (profiles/network_kernels_<workload>_traffic.md): mean FETCH_SIZE and
+# (profiles/network_kernels_<workload>_traffic.md and _counters.md): mean FETCH_SIZE and
 # WRITE_SIZE in KiB per dispatch, scaled by what the same counters read for a
 # plain 256 MiB copy (``--copy-calibration``): 268,435,456 B / 131,084.475 KiB
 # read, 268,435,456 B / 262,144 KiB written.
 COPY_SCALE = (268435456 / (131084.475 * 1024), 268435456 / (262144 * 1024))
 TRAFFIC_KIB = {
-    'fourier_fit_order6': {'network_epoch': (20859.94, 134919.15), 'gemm_wgrad': (31754.55, 4077.5)},
+    'fourier_fit_order2': {'network_epoch': (5101.3, 30162.8), 'gemm_wgrad': (6878.0, 3898.0),
+                           'split_reduce': (3952.1, 2713.1)},
+    'fourier_fit_order6': {'network_epoch': (20859.94, 134919.15), 'gemm_wgrad': (31754.55, 4077.5),
+                           'split_reduce': (4544.0, 2713.12)},
+    'poisson_disk_order2': {'network_epoch': (6934.3, 54427.2), 'gemm_wgrad': (7005.0, 2946.7),
+                            'split_reduce': (1940.5, 261.7)},
+    'fourier_3d_order4': {'network_forward': (51367.6, 5739531.1), 'network_backward': (1753565.2, 3341379.0),
+                          'gemm_wgrad': (2329450.2, 4388.1), 'split_reduce': (22647.6, 1113.0)},
     'fourier_large_order6': {'network_backward': (4986651.81, 8870448.64), 'network_forward': (423199.55, 14688002.1),
                              'gemm_wgrad': (6994723.69, 4064.13)},
 }
@@ -173,18 +180,45 @@ def upload_all(session, wl):
     return ids['net'], [ids['cost']], None
 
 
+def port_epochs(sample, epochs):
+    """Seconds for `epochs` matching epochs of the C restatement (oracle/), one
+    thread: forward + cost + weight gradient, then one RPROP pass over the
+    parameters, as in the timed step."""
+    sys.path.insert(0, str(ROOT / 'oracle'))
+    import oracle
+    x = sample.inputs.transpose(0, 2, 1)
+    t0 = time.perf_counter()
+    for _ in range(epochs):
+        oracle.matching_epoch(sample.neurons, sample.linear, sample.init, sample.cost_schema, x,
+                              sample.target[:, :, None], sample.weight_block(), chunk=sample.chunk,
+                              rows=sample.cost_rows, target_rows=sample.target_rows,
+                              weight_samples=sample.weight_samples, outputs=False)
+        for w in sample.init:
+            w = np.array(w, np.float32)
+            z = np.zeros_like(w)
+            oracle.rprop(w, np.full_like(w, 0.002), z, z)
+    return time.perf_counter() - t0
+
+
 def cpu_baseline(wl):
     """The CPU side of the same epoch on one thread.  Preferred: the
     reference's own CPU server built from its sources (oracle/_ref), driven over
     the wire protocol with training epochs (op 8/15: forward + cost + weight
-    gradient + statistics + RPROP).  Otherwise the C restatement of the same
-    matching epoch."""
+    gradient + statistics + RPROP).  The C restatement of the same matching
+    epoch is timed on the same sample beside it (``port``), or alone when the
+    reference build is absent."""
     sys.path.insert(0, str(ROOT / 'oracle'))
     import oracle
     sample, epochs = cpu_sample(wl)
     ref = oracle.reference_server()
     what = (f'{epochs} training epoch(s) of {sample.name} ({point_rows(sample)} point-rows'
             f'{")" if sample is wl else f", a {sample.size}-point even subsample of the {wl.size}-point workload)"}')
+    port = None
+    if not isinstance(wl, workloads.PoissonWorkload):
+        seconds = port_epochs(sample, epochs)
+        port = {'value': round(point_rows(sample) * epochs / seconds, 1), 'unit': 'points·derivs/s', 'cores': 1,
+                'kind': 'port', 'seconds': round(seconds, 3),
+                'sample': f'{what} of the C restatement: fwd+cost+wgrad+RPROP, single thread'}
     if ref is not None:
         from cpde_amd import wire
         with wire.Session(ref) as s:
@@ -192,26 +226,15 @@ def cpu_baseline(wl):
             t0 = time.perf_counter()
             s.train(net, costs, epochs, method=0, fresh=1, log=0, graph=graph)
             seconds = time.perf_counter() - t0
-        return {'value': round(point_rows(sample) * epochs / seconds, 1), 'unit': 'points·derivs/s', 'cores': 1,
-                'kind': 'reference', 'seconds': round(seconds, 3),
-                'sample': f'{what} on the reference CPU server (serial BLAS): fwd+cost+wgrad+stats+RPROP, '
-                          'single thread'}
-    if isinstance(wl, workloads.PoissonWorkload):
-        return None
-    x = sample.inputs.transpose(0, 2, 1)
-    t0 = time.perf_counter()
-    for _ in range(epochs):
-        oracle.matching_epoch(sample.neurons, sample.linear, sample.init, sample.schema, x,
-                              sample.target[:, :, None], sample.row_weights[:, None, None], chunk=sample.chunk,
-                              outputs=False)
-        for w in sample.init:  # one RPROP pass over the parameters, as in the timed step
-            w = np.array(w, np.float32)
-            z = np.zeros_like(w)
-            oracle.rprop(w, np.full_like(w, 0.002), z, z)
-    seconds = time.perf_counter() - t0
-    return {'value': round(point_rows(sample) * epochs / seconds, 1), 'unit': 'points·derivs/s', 'cores': 1,
-            'kind': 'port', 'seconds': round(seconds, 3),
-            'sample': f'{what} of the C restatement: fwd+cost+wgrad+RPROP, single thread'}
+        out = {'value': round(point_rows(sample) * epochs / seconds, 1), 'unit': 'points·derivs/s', 'cores': 1,
+               'kind': 'reference', 'seconds': round(seconds, 3),
+               'sample': f'{what} on the reference CPU server (serial BLAS): fwd+cost+wgrad+stats+RPROP, '
+                         'single thread'}
+        if port is not None:
+            port['ratio_to_reference'] = round(port['value'] / out['value'], 3)
+            out['port'] = port
+        return out
+    return port
 
 
 def copy_calibration(mib=256, repeats=5):
