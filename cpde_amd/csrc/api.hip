@@ -1780,12 +1780,13 @@ int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, c
         require(costs <= dev->cost_capacity && layers == net->layers - 1 && layers <= dev->grad_capacity,
                 "scalar slots out of range");
         flush_reduce(*dev);
-        // one copy over costs, gradient totals and (with a graph) the summary slot
+        // one copy over costs, gradient totals and (with a graph) the summary
+        // slot, made by the update launch's first workgroup (no copy launch of
+        // its own); the host waits for that launch
         const size_t bytes = with_graph ? dev->scalar_bytes
                                         : size_t(reinterpret_cast<char*>(dev->grad_totals + layers) -
                                                  static_cast<char*>(dev->scalar_block));
-        HIP_CHECK(hipMemcpyAsync(dev->host_block, dev->scalar_block, bytes, hipMemcpyDeviceToHost, dev->stream));
-        HIP_CHECK(hipEventRecord(dev->copied, dev->stream));
+        const ScalarPublish copy{dev->scalar_block, dev->host_block, bytes};
         unsigned long long fresh = 0;
         for (int i = 0; i < costs && i < int(dev->slot_fresh.size()); ++i)
             if (dev->slot_fresh[i]) fresh |= 1ull << i;
@@ -1793,11 +1794,12 @@ int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, c
                                 with_graph ? dev->graph_summary : nullptr};
         const bool wt_current = net->wt_current;
         if (method == 0) {
-            launch_rprop(*dev, *net, &guard);
+            launch_rprop(*dev, *net, &guard, &copy);
             rprop_done(*net);  // in expectation; cpde_update_resolve switches back if the rule rejects the epoch
         } else {
-            launch_adam(*dev, *net, step, lr, &guard);
+            launch_adam(*dev, *net, step, lr, &guard, &copy);
         }
+        HIP_CHECK(hipEventRecord(dev->copied, dev->stream));
         dev->issued = Device::IssuedUpdate{true, net, costs, layers, with_graph != 0, method == 0, wt_current, fresh};
     });
 }

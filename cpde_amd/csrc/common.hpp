@@ -444,9 +444,16 @@ void launch_reduce_rprop(Device& d, const ReduceArgs& a, Net& net, int first);
 // RPROP over every transition, then the switch of the active gradient
 // buffers; with `guard`, the update applies only where the rule accepts the
 // epoch, and the switch is left to the caller.
-void launch_rprop(Device& d, Net& net, const UpdateGuard* guard = nullptr);
+// A copy of the scalar block to its host mirror made by an update launch.
+struct ScalarPublish {
+    const void* src;
+    void* dst;
+    size_t bytes;  // a multiple of 4
+};
+void launch_rprop(Device& d, Net& net, const UpdateGuard* guard = nullptr, const ScalarPublish* publish = nullptr);
 // Adam step `step`; with `guard`, only where the rule accepts the epoch.
-void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* guard = nullptr);
+void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* guard = nullptr,
+                 const ScalarPublish* publish = nullptr);
 void launch_set_steps(Device& d, Net& net, float value);
 void launch_restore_steps(Device& d, Net& net, float floor_value);
 GraphLaunch graph_launch(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,

@@ -547,7 +547,21 @@ struct OptimizerArgs {
     UpdateGuard guard;
     int guarded;
     int* verdict;
+    // publish_dst non-null: the first workgroup copies publish_words 32-bit
+    // words of the scalar block to its pinned host mirror (the download the
+    // guarded update goes out behind), whether or not the update applies
+    const unsigned* publish_src;
+    unsigned* publish_dst;
+    int publish_words;
 };
+
+// The scalar block to the host, by the first workgroup of an update launch,
+// released to the system before the launch ends.
+__device__ __forceinline__ void publish_scalars(const OptimizerArgs& a) {
+    if (!a.publish_dst || blockIdx.x != 0) return;
+    for (int i = threadIdx.x; i < a.publish_words; i += blockDim.x) a.publish_dst[i] = a.publish_src[i];
+    __threadfence_system();
+}
 
 // The guarded update's rule, the same on every lane of the grid; the first
 // lane records it for the reductions that wait on it (ReduceArgs::gate).
@@ -1531,6 +1545,7 @@ __device__ __forceinline__ bool entry_of(const OptimizerArgs& a, int& t, int& j)
 
 // One lane per entry: the gradient already reduced into the active buffer.
 __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs a) {
+    publish_scalars(a);
     if (!update_applies(a)) return;
     int t, j;
     if (entry_of(a, t, j)) rprop_update(a, t, j, a.Ga[t][j]);
@@ -1540,6 +1555,7 @@ __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs 
 __global__ __launch_bounds__(kOptimizerThreads) void adam_kernel(OptimizerArgs a, float lr, float beta1, float beta2,
                                                                   float beta1t, float beta2t) {
 #pragma clang fp contract(off)
+    publish_scalars(a);
     if (!update_applies(a)) return;
     int t, j;
     if (entry_of(a, t, j)) {
@@ -1595,13 +1611,25 @@ static void for_transition_groups(Net& net, F launch) {
     }
 }
 
-void launch_rprop(Device& d, Net& net, const UpdateGuard* guard) {
+// The first group's launch publishes `publish` (device scalar block, host
+// mirror, bytes) when given.
+static void set_publish(OptimizerArgs& a, const ScalarPublish* publish, bool& first) {
+    if (!publish || !first) return;
+    first = false;
+    a.publish_src = static_cast<const unsigned*>(publish->src);
+    a.publish_dst = static_cast<unsigned*>(publish->dst);
+    a.publish_words = int(publish->bytes / sizeof(unsigned));
+}
+
+void launch_rprop(Device& d, Net& net, const UpdateGuard* guard, const ScalarPublish* publish) {
+    bool first = true;
     for_transition_groups(net, [&](OptimizerArgs a, int blocks) {
         if (guard) {
             a.guard = *guard;
             a.guarded = 1;
             a.verdict = d.update_verdict;
         }
+        set_publish(a, publish, first);
         TraceScope trace(d, kTraceOptimizer, 28.0 * a.begin[a.transitions]);  // 4 reads, 3 writes per entry
         hipLaunchKernelGGL(rprop_kernel, blocks, kOptimizerThreads, 0, d.stream, a);
         HIP_CHECK(hipGetLastError());
@@ -1611,15 +1639,17 @@ void launch_rprop(Device& d, Net& net, const UpdateGuard* guard) {
     net.wt_current = true;
 }
 
-void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* guard) {
+void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* guard, const ScalarPublish* publish) {
     const float b1 = 0.9f, b2 = 0.999f;
     const float b1t = std::pow(b1, float(step)), b2t = std::pow(b2, float(step));
+    bool first = true;
     for_transition_groups(net, [&](OptimizerArgs a, int blocks) {
         if (guard) {
             a.guard = *guard;
             a.guarded = 1;
             a.verdict = d.update_verdict;
         }
+        set_publish(a, publish, first);
         hipLaunchKernelGGL(adam_kernel, blocks, kOptimizerThreads, 0, d.stream, a, lr, b1, b2, b1t, b2t);
         HIP_CHECK(hipGetLastError());
     });
