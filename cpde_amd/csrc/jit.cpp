@@ -689,6 +689,10 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
     // holds the last hidden layer's values until the output backward
     const std::string scratch = "(kNNC * " + std::to_string(NO) + " > 4 * kNPB ? kNNC * " + std::to_string(NO) +
                                 " : 4 * kNPB)";
+    // The grids have one block per kNPB points of the chunk's width, so at one
+    // point per block every block has its point: npts is the constant 1 there,
+    // which leaves the phases' loops and the products' column checks to the
+    // compiler.
     ep << tile_declarations()
        << "    __shared__ __attribute__((aligned(16))) float O[2 * kNNC * " << NO << "];\n"
        << "#ifdef CPDE_ALIAS_TILES\n"
@@ -696,7 +700,7 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
        << "#else\n"
        << "    float* const S = T;\n"
        << "#endif\n"
-       << "    const int p0 = net_block(a) * kNPB, npts = min(kNPB, points - p0);\n"
+       << "    const int p0 = net_block(a) * kNPB, npts = kNPB == 1 ? 1 : min(kNPB, points - p0);\n"
        << prefetch << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
        << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
        << "    __syncthreads();\n";
@@ -723,7 +727,7 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     // network-fused forward and backward, one call per layer with its widths;
     // the one-pass epoch runs both with the matching cost between them
     std::ostringstream fwd, bwd;
-    fwd << "    const int p0 = net_block(a) * kNPB, npts = min(kNPB, points - p0);\n";
+    fwd << "    const int p0 = net_block(a) * kNPB, npts = kNPB == 1 ? 1 : min(kNPB, points - p0);\n";
     for (int t = 1; t + 2 < L; ++t)
         fwd << "    net_transpose<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ");\n";
     fwd << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
@@ -749,7 +753,7 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
       << tiles << fwd.str() << "}\n";
     o << "extern \"C\" __global__ __launch_bounds__(" << nt << ", " << tuning.backward_blocks
       << ") void network_backward_k(NetArgs a, int points) {\n"
-      << tiles << "    const int p0 = net_block(a) * kNPB, npts = min(kNPB, points - p0);\n" << bwd.str() << "}\n";
+      << tiles << "    const int p0 = net_block(a) * kNPB, npts = kNPB == 1 ? 1 : min(kNPB, points - p0);\n" << bwd.str() << "}\n";
     {
         const int NO = neurons[L - 1];
         const std::string prefetch =
