@@ -258,20 +258,22 @@ int cpde_rprop(cpde_net* net);
 int cpde_scalars_download_rprop(cpde_device* dev, int costs, cpde_cost_stats* cost_out, int layers,
                                 cpde_gradient_stats* gradient_out, cpde_graph_summary* summary_out, cpde_net* net,
                                 int* updated);
-/* The first half of that call: the copy of `costs` cost totals, the gradient
- * totals of every transition (layers = the network's transitions) and, with
- * with_graph, the device's graph summary, to the device's host block; then the
- * update behind the copy -- method 0 RPROP, 1 Adam step `step` with rate lr
- * (ADAM_k, cuda/derivative_kernels_v4.cu:780-799) -- which applies only if
- * every cost is finite with no bad sample, the graph has no bad node and every
- * gradient is finite: the checks after which the server updates.  RPROP's
- * active gradient buffers switch now, in expectation, so that calls made
- * before the resolution (the next epoch's first passes) write the next
+/* The first half of that call: the update -- method 0 RPROP, 1 Adam step
+ * `step` with rate lr (ADAM_k, cuda/derivative_kernels_v4.cu:780-799) --
+ * which applies only if every cost is finite with no bad sample, the graph has
+ * no bad node and every gradient is finite: the checks after which the server
+ * updates.  Its launch also copies `costs` cost totals, the gradient totals of
+ * every transition (layers = the network's transitions) and, with with_graph,
+ * the device's graph summary to the device's host block, and leaves its
+ * verdict on the device, where reductions launched before the resolution read
+ * it and store into this network's gradient buffers only if it applied.
+ * RPROP's active gradient buffers switch now, in expectation, so that calls
+ * made before the resolution (the next epoch's first passes) write the next
  * gradient where it belongs.  costs <= 64; one issued update per device at a
  * time. */
 int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net, int method, int step,
                       float lr);
-/* The second half: wait for the copy alone, hand out the scalars (as
+/* The second half: wait for that launch, hand out the scalars (as
  * cpde_scalars_download_graph does) and say whether the update applied; where
  * it did not, RPROP's buffers switch back. */
 int cpde_update_resolve(cpde_device* dev, cpde_cost_stats* cost_out, cpde_gradient_stats* gradient_out,
@@ -280,8 +282,9 @@ int cpde_update_resolve(cpde_device* dev, cpde_cost_stats* cost_out, cpde_gradie
  * held one-pass epoch and the waiting weight-gradient and reduction launches
  * without launching them, and stop deferring (cpde_gradients_defer):
  * for passes issued ahead of a check that then rejected the epoch before them.
- * Such passes write scratch only (stacks, records, partials), so nothing of
- * the network's state changes. */
+ * Such passes write scratch (stacks, records, partials), and the reductions
+ * they had to launch stored nothing into a network whose issued update did not
+ * apply, so nothing of the network's state changes. */
 int cpde_gradients_discard(cpde_device* dev);
 /* Adam step `step` (>= 1) with learning rate lr (ADAM_k, :780-799). */
 int cpde_adam(cpde_net* net, int step, float lr);
