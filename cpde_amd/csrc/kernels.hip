@@ -587,15 +587,21 @@ __device__ __forceinline__ void copy_transposed(const OptimizerArgs& a, int t, i
 // round every product and sum separately, as the reference's CPU build does:
 // no multiply-add contraction (hipcc contracts by default, and
 // __fmul_rn/__fadd_rn do not prevent it).
-__device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int j, float g) {
+// The entry's optimizer state, loaded apart from the update so that a caller
+// can send the loads out before its gradient is complete.
+struct RpropState {
+    float w, step, gi;
+};
+__device__ __forceinline__ RpropState rprop_state(const OptimizerArgs& a, int t, int j) {
+    return RpropState{a.W[t][j], a.S[t][j], a.Gi[t][j]};
+}
+__device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int j, float g, const RpropState& e) {
 #pragma clang fp contract(off)
-    float* W = a.W[t] + j;
-    float* step = a.S[t] + j;
-    const float gi = a.Gi[t][j];
+    const float gi = e.gi;
     const float prod = g * gi;
-    float s = *step;
+    float s = e.step;
     if (prod > 0) s *= 1.2f;
-    const float w = *W;
+    const float w = e.w;
     const float nW = w - copysignf(s, g);
     float kept = w, kept_g = g;
     if (prod < 0) {
@@ -610,9 +616,12 @@ __device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int 
         }
     }
     a.Ga[t][j] = kept_g;
-    *W = kept;
-    *step = s;
+    a.W[t][j] = kept;
+    a.S[t][j] = s;
     copy_transposed(a, t, j, kept);
+}
+__device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int j, float g) {
+    rprop_update(a, t, j, g, rprop_state(a, t, j));
 }
 
 // grad_t[m + M*n] (+)= sum over splits of the partials of entry (m, n), n = N
@@ -623,31 +632,36 @@ __device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int 
 // l + 64u (+ 256i) into running sum u (four, combined in a fixed order), then a
 // fixed shuffle tree.  Either way the summation order is fixed whatever the
 // scheduling.
-__device__ void finish_cost_records(const CostStats* __restrict__ records, int count, CostStats* __restrict__ total,
-                                    int overwrite);
-__device__ void run_graph(const GraphLaunch& g);
+__device__ void finish_costs(const ReduceArgs& a);
+__device__ void run_graph_block(const GraphLaunch& g, bool fresh = false);
 
 // UPDATE: the lane that finishes an entry's gradient applies RPROP to it
 // (reduce_rprop_kernel), which is the reduction followed by rprop_kernel in one
-// launch, bit for bit.
+// launch, bit for bit; it loads the entry's optimizer state (and, accumulating,
+// its gradient) before the partials, so that the two loads' latencies overlap.
+// Block 0 finishes the costs and evaluates the graph when the launch carries
+// them: the longest chain of the launch is dispatched first.
 template <bool UPDATE>
 __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const OptimizerArgs& o) {
     __shared__ float part[4][64];
-    if ((a.costs || a.with_graph) && int(blockIdx.x) == a.block_begin[a.transitions]) {
-        for (int c = 0; c < a.costs; ++c) {
-            if (c) __syncthreads();  // the block reduction's shared slots are reused
-            finish_cost_records(a.cost_partials[c], a.cost_count[c], a.cost_total[c], a.cost_overwrite[c]);
-        }
-        // the lane that wrote the finished costs evaluates the graph on them
-        if (a.with_graph && threadIdx.x == 0) run_graph(a.graph);
+    const int cost_block = a.costs || a.with_graph ? 1 : 0;
+    if (cost_block && blockIdx.x == 0) {
+        finish_costs(a);
+        if (a.with_graph) run_graph_block(a.graph, true);
         return;
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int block = int(blockIdx.x) - cost_block;
     int t = 0;
-    while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
-    const int local = int(blockIdx.x) - a.block_begin[t];
+    while (t + 1 < a.transitions && block >= a.block_begin[t + 1]) ++t;
+    const int local = block - a.block_begin[t];
     const int M = a.M[t], N1 = a.N[t] + 1, S = a.splits[t];
     const int count = M * N1;
+    // where entry j of transition t lives in the gradient and optimizer buffers
+    auto index_of = [&](int j) {
+        const int mrow = j / N1, n = j - mrow * N1;
+        return mrow + M * n;
+    };
     // Sixteen running sums per lane, each fed by an unconditional load (an
     // index past the last split reads the last split and adds nothing), so a
     // round's sixteen loads are in flight together; the sums then meet in a
@@ -664,6 +678,14 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
     if (!a.split_minor[t]) {
         const size_t stride = size_t(count);
         const int j = local * 64 + lane;
+        const bool finisher = wave == 0 && j < count;
+        const int idx = finisher ? index_of(j) : 0;
+        RpropState e{};
+        float before = 0.0f;
+        if (finisher) {
+            if constexpr (UPDATE) e = rprop_state(o, t, idx);
+            if (a.accumulate) before = a.grad[t][idx];
+        }
         // every wave; the sum of entry j is valid on wave 0's lane
         auto sum_major = [&](const float* base, int S) {
             float s = 0.0f;
@@ -689,17 +711,22 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
         };
         const float sum = sum_major(a.partial[t], S);
         const float sum2 = two ? sum_major(a.partial2[t], a.splits2[t]) : 0.0f;
-        if (wave == 0 && j < count) {
-            const int mrow = j / N1, n = j - mrow * N1;
-            const int idx = mrow + M * n;
-            float v = a.accumulate ? a.grad[t][idx] + sum : sum;
+        if (finisher) {
+            float v = a.accumulate ? before + sum : sum;
             if (two) v = v + sum2;
-            if constexpr (UPDATE) rprop_update(o, t, idx, v);
+            if constexpr (UPDATE) rprop_update(o, t, idx, v, e);
             else if (!a.gate || *a.gate) a.grad[t][idx] = v;
         }
     } else {
         const int j = local * 4 + wave;
         if (j >= count) return;
+        const int idx = index_of(j);
+        RpropState e{};
+        float before = 0.0f;
+        if (lane == 0) {
+            if constexpr (UPDATE) e = rprop_state(o, t, idx);
+            if (a.accumulate) before = a.grad[t][idx];
+        }
         // the sum of entry j, valid on lane 0
         auto sum_minor = [&](const float* base, int S) {
             const float* P = base + size_t(j) * S;
@@ -720,11 +747,9 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
         const float s = sum_minor(a.partial[t], S);
         const float s2 = two ? sum_minor(a.partial2[t], a.splits2[t]) : 0.0f;
         if (lane == 0) {
-            const int mrow = j / N1, n = j - mrow * N1;
-            const int idx = mrow + M * n;
-            float v = a.accumulate ? a.grad[t][idx] + s : s;
+            float v = a.accumulate ? before + s : s;
             if (two) v = v + s2;
-            if constexpr (UPDATE) rprop_update(o, t, idx, v);
+            if constexpr (UPDATE) rprop_update(o, t, idx, v, e);
             else if (!a.gate || *a.gate) a.grad[t][idx] = v;
         }
     }
@@ -747,8 +772,9 @@ __global__ __launch_bounds__(256) void reduce_rprop_kernel(ReduceArgs a, Optimiz
 // workgroup then sums its four waves' tiles in LDS in the fixed order
 // (w0 + w2) + (w1 + w3) and writes its split's partial, as the LDS-staged
 // tiles do.  The bias (n-tile 0 only) is the sum of G over value-row columns.
-constexpr int kWdStride = 65;                  // LDS row stride of a 64x64 tile
-constexpr int kWdLds = 2 * 64 * kWdStride;     // two tiles; also the thin roles' 256 x 17 scratch
+constexpr int kWdSlot = 64 * 64;                // one 64x64 tile in LDS, float4 per (x, z, lane)
+constexpr int kWdLds = 2 * kWdSlot + 256;       // two tiles; also the thin roles' 256 x 17 scratch
+constexpr int kWdBiasAhead = 4;                 // bias column groups loaded before the tile's epilogue
 #ifndef CPDE_WD_DEPTH
 #define CPDE_WD_DEPTH 2
 #endif
@@ -888,50 +914,67 @@ __device__ __forceinline__ void wgrad_direct_tile(const WgradArgs& a, int t, int
         for (int y = 0; y < 4; ++y) acc[x][y] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     if (VEC && m0 + 64 <= M && n0 + 64 <= N) wd_accumulate<VEC, false>(acc, G, Y, M, N, kbegin, kend, gm, yn, wave, q);
     else wd_accumulate<VEC, true>(acc, G, Y, M, N, kbegin, kend, gm, yn, wave, q);
-    // (w0 + w2) + (w1 + w3): waves 2 and 3 store, waves 0 and 1 add
-    auto store = [&](float* T) {
+    // bias (n-tile 0): the sum of G over the split's value-row columns; lane
+    // group (wave, q) takes value columns first + R (4 wave + q + 16 i) for its
+    // 4 rows, the sixteen groups then meet in a fixed order.  The first
+    // kWdBiasAhead columns of each group are loaded now (an index past the
+    // split reads its last column and is not added), so that their latency
+    // passes under the tile's epilogue, whose barriers wait on LDS only.
+    const bool with_bias = n0 == 0;
+    const int bias_c0 = (kbegin + R - 1) / R * R + R * (4 * wave + q);
+    float4 bias_ahead[kWdBiasAhead];
+    if (with_bias)
+#pragma unroll
+        for (int u = 0; u < kWdBiasAhead; ++u) {
+            const int c = min(bias_c0 + 16 * R * u, kend - 1);
+            bias_ahead[u] = wd_load<VEC, true>(G, unsigned(c) * unsigned(M) + unsigned(gm), gm, M);
+        }
+    // (w0 + w2) + (w1 + w3): waves 2 and 3 put their tiles in the two LDS
+    // slots, waves 0 and 1 add them and put w0 + w2 and w1 + w3 back, each
+    // lane's accumulator quad (x, z) as one float4 at ((4x + z) 64 + lane) 4;
+    // then every lane adds the two sums of 16 entries, a wave writing one
+    // 64-entry row of the partial per instruction
+    auto slot = [&](int k, int x, int z) {
+        return reinterpret_cast<floatx4*>(lds + k * kWdSlot + ((4 * x + z) * 64 + lane) * 4);
+    };
+    if (wave >= 2)
 #pragma unroll
         for (int x = 0; x < 4; ++x)
 #pragma unroll
-            for (int z = 0; z < 4; ++z)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) T[(4 * (4 * q + v) + x) * kWdStride + 4 * j + z] = acc[x][z][v];
-    };
-    auto add = [&](const float* T) {
-#pragma unroll
-        for (int x = 0; x < 4; ++x)
-#pragma unroll
-            for (int z = 0; z < 4; ++z)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc[x][z][v] += T[(4 * (4 * q + v) + x) * kWdStride + 4 * j + z];
-    };
-    // waves 2 and 3 put their tiles in the two LDS slots, waves 0 and 1 add
-    // them and put w0 + w2 and w1 + w3 back; every lane then adds the two
-    // sums of 16 entries, a wave writing one 64-entry row per instruction
-    if (wave >= 2) store(lds + (wave - 2) * 64 * kWdStride);
+            for (int z = 0; z < 4; ++z) *slot(wave - 2, x, z) = acc[x][z];
     __syncthreads();
-    if (wave < 2) {
-        add(lds + wave * 64 * kWdStride);
-        store(lds + wave * 64 * kWdStride);
-    }
+    if (wave < 2)
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int z = 0; z < 4; ++z) {
+                floatx4* p = slot(wave, x, z);
+                *p = acc[x][z] + *p;
+            }
     __syncthreads();
     float* P = a.partial[t] + size_t(split) * M * (N + 1);
     if (n0 + lane < N) {
+        // entry (row ml, column lane) of the tile: accumulator quad
+        // (x, z) = (ml % 4, lane % 4) of lane 16 (ml / 16) + lane / 4, component (ml / 4) % 4
+        const int zl = lane & 3, jl = lane >> 2;
 #pragma unroll 4
         for (int i = 0; i < 16; ++i) {
             const int ml = wave + 4 * i;
-            if (m0 + ml < M)
-                P[size_t(m0 + ml) * (N + 1) + n0 + lane] =
-                    lds[ml * kWdStride + lane] + lds[(64 + ml) * kWdStride + lane];
+            const int at = ((4 * (ml & 3) + zl) * 64 + 16 * (ml >> 4) + jl) * 4 + ((ml >> 2) & 3);
+            if (m0 + ml < M) P[size_t(m0 + ml) * (N + 1) + n0 + lane] = lds[at] + lds[kWdSlot + at];
         }
     }
-    // bias (n-tile 0): the sum of G over the split's value-row columns; lane
-    // group (wave, q) takes value columns first + R (4 wave + q + 16 i) for its
-    // 4 rows, the sixteen groups then meet in a fixed order
-    if (n0 == 0) {
+    if (with_bias) {
         float4 bias = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        const int first = (kbegin + R - 1) / R * R;
-        for (int c = first + R * (4 * wave + q); c < kend; c += 16 * R) {
+#pragma unroll
+        for (int u = 0; u < kWdBiasAhead; ++u)
+            if (bias_c0 + 16 * R * u < kend) {
+                bias.x += bias_ahead[u].x;
+                bias.y += bias_ahead[u].y;
+                bias.z += bias_ahead[u].z;
+                bias.w += bias_ahead[u].w;
+            }
+        for (int c = bias_c0 + 16 * R * kWdBiasAhead; c < kend; c += 16 * R) {
             const float4 g = wd_load<VEC, true>(G, unsigned(c) * unsigned(M) + unsigned(gm), gm, M);
             bias.x += g.x;
             bias.y += g.y;
@@ -946,8 +989,7 @@ __device__ __forceinline__ void wgrad_direct_tile(const WgradArgs& a, int t, int
         bias.y += __shfl_xor(bias.y, 32);
         bias.z += __shfl_xor(bias.z, 32);
         bias.w += __shfl_xor(bias.w, 32);
-        float* bias_lds = lds + 64 * kWdStride;  // the second tile slot
-        __syncthreads();                          // every lane has read the slots
+        float* bias_lds = lds + 2 * kWdSlot;  // past the two tile slots
         if (q == 0) {
             bias_lds[wave * 64 + 4 * j + 0] = bias.x;
             bias_lds[wave * 64 + 4 * j + 1] = bias.y;
@@ -1136,13 +1178,97 @@ __device__ CostStats block_reduce_cost(CostStats v) {
 }
 
 // One block of kCostThreads lanes: lane l combines records l, l + 256, ... in
-// order, then the fixed block reduction; the result overwrites or joins *total.
+// order (loaded four at a time, so that their latencies overlap: an index past
+// the end reads the last record again and is not combined), then the fixed
+// block reduction; the result overwrites or joins *total.
 __device__ void finish_cost_records(const CostStats* __restrict__ records, int count, CostStats* __restrict__ total,
                                     int overwrite) {
+    constexpr int U = 4;
     CostStats v = empty_cost();
-    for (int i = threadIdx.x; i < count; i += blockDim.x) v = combine(v, records[i]);
+    const int step = int(blockDim.x);
+    for (int i = threadIdx.x; i < count; i += U * step) {
+        CostStats r[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) r[u] = records[min(i + u * step, count - 1)];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (i + u * step < count) v = combine(v, r[u]);
+    }
     v = block_reduce_cost(v);
     if (threadIdx.x == 0) *total = overwrite ? v : combine(*total, v);
+}
+
+// The cost finishes a reduction launch carries, on its cost block (256
+// lanes): each cost's records combined exactly as finish_cost_records combines
+// them (lane l: records l, l + 256, ... in order; then the fixed block
+// reduction), so the same bits, but with every cost's records loaded in one
+// go (four per lane and cost, an index past the end reading the last record
+// again, not combined) and the trees side by side.  The finished totals stay
+// in LDS for the graph (reduce_finished: the totals, their slots, how many).
+__shared__ CostStats reduce_finished[kReduceCosts];
+__shared__ const CostStats* reduce_finished_slot[kReduceCosts];
+__shared__ int reduce_finished_count;
+
+__device__ void finish_costs(const ReduceArgs& a) {
+    constexpr int U = 4;
+    __shared__ CostStats waves[kReduceCosts][kCostThreads / 64];
+    const int step = int(blockDim.x), lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    CostStats v[kReduceCosts], prior[kReduceCosts];
+    int rounds = 0;
+#pragma unroll
+    for (int c = 0; c < kReduceCosts; ++c) {
+        v[c] = empty_cost();
+        if (c < a.costs) {
+            rounds = max(rounds, (a.cost_count[c] + U * step - 1) / (U * step));
+            // a total joined rather than overwritten: loaded with the records
+            if (threadIdx.x == 0 && !a.cost_overwrite[c]) prior[c] = *a.cost_total[c];
+        }
+    }
+    for (int k = 0; k < rounds; ++k) {
+        CostStats r[kReduceCosts][U];
+#pragma unroll
+        for (int c = 0; c < kReduceCosts; ++c)
+            if (c < a.costs && a.cost_count[c] > 0) {
+                const int count = a.cost_count[c];
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    r[c][u] = a.cost_partials[c][min(int(threadIdx.x) + (k * U + u) * step, count - 1)];
+            }
+#pragma unroll
+        for (int c = 0; c < kReduceCosts; ++c)
+            if (c < a.costs) {
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (int(threadIdx.x) + (k * U + u) * step < a.cost_count[c]) v[c] = combine(v[c], r[c][u]);
+            }
+    }
+#pragma unroll
+    for (int c = 0; c < kReduceCosts; ++c)
+        if (c < a.costs) {
+            CostStats x = v[c];
+            for (int off = 32; off > 0; off >>= 1) {
+                CostStats o;
+                o.value = __shfl_down(x.value, off, 64);
+                o.bad_sample = __shfl_down(x.bad_sample, off, 64);
+                o.bad_component = __shfl_down(x.bad_component, off, 64);
+                x = combine(x, o);
+            }
+            if (lane == 0) waves[c][wave] = x;
+        }
+    __syncthreads();
+    if (threadIdx.x == 0)
+#pragma unroll
+        for (int c = 0; c < kReduceCosts; ++c)
+            if (c < a.costs) {
+                CostStats r = empty_cost();
+                for (int w = 0; w < step / 64; ++w) r = combine(r, waves[c][w]);
+                const CostStats total = a.cost_overwrite[c] ? r : combine(prior[c], r);
+                *a.cost_total[c] = total;
+                reduce_finished[c] = total;
+                reduce_finished_slot[c] = a.cost_total[c];
+            }
+    if (threadIdx.x == 0) reduce_finished_count = a.costs;
+    __syncthreads();
 }
 
 __global__ __launch_bounds__(kCostThreads) void cost_finish_kernel(const CostStats* __restrict__ blocks, int count,
@@ -1416,20 +1542,31 @@ struct GradGroupArgs {
 
 constexpr int kGradThreads = 1024;
 
+// Entries are loaded eight at a time per lane (an index past the end reads the
+// last entry again and is not counted), so that a transition of up to 8,192
+// entries waits on one round of loads.
 __global__ __launch_bounds__(kGradThreads) void grad_stats_kernel(GradGroupArgs a, GradStats* __restrict__ totals) {
-    const int t = blockIdx.x;
+    constexpr int U = 8;
+    const int t = blockIdx.x, count = a.count[t];
     const float* __restrict__ g = a.g[t];
     GradStats acc{0.0, 0.0, 0ull, INT_MAX, 0};
-#pragma unroll 4
-    for (int i = threadIdx.x; i < a.count[t]; i += kGradThreads) {
-        const double v = g[i];
-        if (!isfinite(v)) {
-            ++acc.nonfinite;
-            if (i < acc.first) acc.first = i;
-        } else {
-            acc.squared_norm += v * v;
-            const double mag = fabs(v);
-            if (mag > acc.max_abs) acc.max_abs = mag;
+    for (int i0 = threadIdx.x; i0 < count; i0 += U * kGradThreads) {
+        float x[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) x[u] = g[min(i0 + u * kGradThreads, count - 1)];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = i0 + u * kGradThreads;
+            if (i >= count) break;
+            const double v = x[u];
+            if (!isfinite(v)) {
+                ++acc.nonfinite;
+                if (i < acc.first) acc.first = i;
+            } else {
+                acc.squared_norm += v * v;
+                const double mag = fabs(v);
+                if (mag > acc.max_abs) acc.max_abs = mag;
+            }
         }
     }
     acc = block_reduce_grad(acc);
@@ -1544,29 +1681,43 @@ __device__ __forceinline__ bool entry_of(const OptimizerArgs& a, int& t, int& j)
 }
 
 // One lane per entry: the gradient already reduced into the active buffer.
+// The entry (state and gradient) is loaded first, so that its latency overlaps
+// the publish copy's and the rule's.
 __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs a) {
+    int t, j;
+    const bool mine = entry_of(a, t, j);
+    RpropState e{};
+    float g = 0.0f;
+    if (mine) {
+        e = rprop_state(a, t, j);
+        g = a.Ga[t][j];
+    }
     publish_scalars(a);
     if (!update_applies(a)) return;
-    int t, j;
-    if (entry_of(a, t, j)) rprop_update(a, t, j, a.Ga[t][j]);
+    if (mine) rprop_update(a, t, j, g, e);
 }
 
 // ADAM_k (cuda/derivative_kernels_v4.cu:780-799); M in S, V in the inactive buffer.
 __global__ __launch_bounds__(kOptimizerThreads) void adam_kernel(OptimizerArgs a, float lr, float beta1, float beta2,
                                                                   float beta1t, float beta2t) {
 #pragma clang fp contract(off)
+    int t, j;
+    const bool mine = entry_of(a, t, j);
+    float g = 0.0f, m = 0.0f, v = 0.0f, w = 0.0f;
+    if (mine) {  // loaded first, as in rprop_kernel
+        g = a.Ga[t][j];
+        m = a.S[t][j];
+        v = a.Gi[t][j];
+        w = a.W[t][j];
+    }
     publish_scalars(a);
     if (!update_applies(a)) return;
-    int t, j;
-    if (entry_of(a, t, j)) {
-        const float g = a.Ga[t][j];
-        float m = a.S[t][j], v = a.Gi[t][j];
+    if (mine) {
         m = beta1 * m + (1 - beta1) * g;
         v = beta2 * v + (1 - beta2) * g * g;
         a.S[t][j] = m;
         a.Gi[t][j] = v;
         const float mh = m / (1 - beta1t), vh = v / (1 - beta2t);
-        const float w = a.W[t][j];
         const float nW = float(double(w) - double(lr * mh) / (double(sqrtf(vh)) + 1e-8));
         const float kept = fabsf(nW) <= 20.0f ? nW : w;
         a.W[t][j] = kept;
@@ -1756,10 +1907,89 @@ __device__ void run_graph(const GraphLaunch& g) {
         if (!isfinite(multipliers[i])) summary->bad_node = root;
 }
 
-__global__ void graph_kernel(GraphLaunch g) {
-    if (blockIdx.x || threadIdx.x) return;
-    run_graph(g);
+// Graphs of at most this many nodes and leaves are evaluated on a copy in LDS.
+constexpr int kGraphLdsNodes = 256, kGraphLdsLeaves = 64;
+
+// run_graph with every lane of the block helping: the lanes copy the nodes and
+// leaf values into LDS, lane 0 runs the same two sweeps on the copy (each step
+// of the serial chain then waits on LDS, not on a round trip to global memory),
+// and the lanes write the values, adjoints, activity, multipliers and summary
+// out.  The same operations in the same order as run_graph, so the same bits.
+// Larger graphs run on global memory.  Every lane of the block calls it.
+__device__ void run_graph_block(const GraphLaunch& g, bool fresh) {
+    const int count = g.count, leaves = g.leaves, root = g.root;
+    if (count > kGraphLdsNodes || leaves > kGraphLdsLeaves) {
+        if (threadIdx.x == 0) run_graph(g);
+        return;
+    }
+    __shared__ int4 node[kGraphLdsNodes];  // op, a, b, active
+    __shared__ double parameter[kGraphLdsNodes], value[kGraphLdsNodes], adjoint[kGraphLdsNodes];
+    __shared__ double multiplier[kGraphLdsLeaves];
+    __shared__ int bad_node;
+    for (int i = threadIdx.x; i < count; i += blockDim.x) {
+        const cpde_scalar_node n = g.nodes[i];
+        node[i] = make_int4(n.op, n.a, n.b, n.op == kLeaf);
+        parameter[i] = n.parameter;
+        double leaf = 0.0;
+        if (n.op == kLeaf) {
+            // a total the launch has just finished (finish_costs) is taken from LDS
+            const CostStats* slot = g.integrals + n.a;
+            const int finished = fresh ? reduce_finished_count : 0;
+            int c = 0;
+            while (c < finished && reduce_finished_slot[c] != slot) ++c;
+            leaf = c < finished ? reduce_finished[c].value : slot->value;
+        }
+        value[i] = leaf;
+        adjoint[i] = 0;
+    }
+    for (int i = threadIdx.x; i < leaves; i += blockDim.x) multiplier[i] = 0;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int bad = -1;
+        for (int i = 0; i < count; ++i) {
+            const int4 n = node[i];
+            if (n.x != kLeaf) {
+                value[i] = scalar_value(n.x, n.y < 0 ? 0 : value[n.y], n.z < 0 ? 0 : value[n.z], parameter[i]);
+                if (n.x > 2) node[i].w = node[n.y].w || ((n.x <= kDiv || n.x == kAttach) && node[n.z].w);
+            }
+            if (!isfinite(value[i]) && bad < 0) bad = i;
+        }
+        if (g.gradient && bad < 0) {
+            adjoint[root] = 1;
+            for (int i = count - 1; i >= 0; --i) {
+                const int4 n = node[i];
+                const double seed = adjoint[i];
+                if (seed == 0 || !n.w) continue;
+                if (n.x == kLeaf) multiplier[n.y] += seed;
+                else if (n.x > 2) {
+                    double da, db;
+                    scalar_partials(n.x, value[n.y], n.z < 0 ? 0 : value[n.z], value[i], parameter[i], da, db);
+                    if (node[n.y].w) adjoint[n.y] += seed * da;
+                    if ((n.x <= kDiv || n.x == kAttach) && node[n.z].w) adjoint[n.z] += seed * db;
+                }
+                if (!isfinite(seed) && bad < 0) bad = i;
+            }
+            for (int i = 0; i < leaves; ++i)
+                if (!isfinite(multiplier[i])) bad = root;
+        }
+        bad_node = bad;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < count; i += blockDim.x) {
+        g.values[i] = value[i];
+        g.adjoints[i] = adjoint[i];
+        g.active[i] = node[i].w;
+    }
+    for (int i = threadIdx.x; i < leaves; i += blockDim.x) g.multipliers[i] = multiplier[i];
+    if (threadIdx.x == 0) {
+        g.summary->value = value[root];
+        g.summary->bad_node = bad_node;
+    }
 }
+
+constexpr int kGraphThreads = 64;
+
+__global__ __launch_bounds__(kGraphThreads) void graph_kernel(GraphLaunch g) { run_graph_block(g); }
 
 GraphLaunch graph_launch(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,
                          double* adjoints, double* multipliers, int* active, cpde_graph_summary* summary,
@@ -1769,7 +1999,7 @@ GraphLaunch graph_launch(Device& d, const cpde_scalar_node* nodes, int count, in
 }
 
 void launch_graph(Device& d, const GraphLaunch& g) {
-    hipLaunchKernelGGL(graph_kernel, 1, 1, 0, d.stream, g);
+    hipLaunchKernelGGL(graph_kernel, 1, kGraphThreads, 0, d.stream, g);
     HIP_CHECK(hipGetLastError());
 }
 
