@@ -1769,10 +1769,23 @@ int cpde_scalars_download_graph(cpde_device* dev, int costs, cpde_cost_stats* co
     });
 }
 
-int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net, int method, int step,
-                      float lr) {
+// cpde_update_issue; with `inspect`, cpde_inspect_gradients first -- or, where
+// the statistics need not be whole (`full` false) and update_tests(net) holds,
+// the update launch's own finiteness test in their place.
+static int issue_update(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net, int method, int step,
+                        float lr, bool inspect, bool full) {
     return guarded([&] {
         require(dev && net, "null argument");
+        bool test = false;
+        if (inspect) {
+            if (full || !update_tests(*net)) {
+                if (int code = cpde_inspect_gradients(net)) throw_code(code);
+            } else {
+                test = true;
+                flush_reduce(*dev);
+                dev->reserve_grads(net->layers - 1);
+            }
+        }
         require(method == 0 || (method == 1 && step >= 1), "method 0 (RPROP) or 1 (Adam, step >= 1)");
         require(net->dev == dev, "network of another device");
         require(!dev->issued.open, "an issued update is not resolved yet");
@@ -1790,18 +1803,29 @@ int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, c
         unsigned long long fresh = 0;
         for (int i = 0; i < costs && i < int(dev->slot_fresh.size()); ++i)
             if (dev->slot_fresh[i]) fresh |= 1ull << i;
-        const UpdateGuard guard{dev->cost_totals, costs, fresh, dev->grad_totals, layers,
+        // with its own test the launch reads no gradient totals
+        const UpdateGuard guard{dev->cost_totals, costs, fresh, test ? nullptr : dev->grad_totals, test ? 0 : layers,
                                 with_graph ? dev->graph_summary : nullptr};
         const bool wt_current = net->wt_current;
         if (method == 0) {
-            launch_rprop(*dev, *net, &guard, &copy);
+            launch_rprop(*dev, *net, &guard, &copy, test);
             rprop_done(*net);  // in expectation; cpde_update_resolve switches back if the rule rejects the epoch
         } else {
-            launch_adam(*dev, *net, step, lr, &guard, &copy);
+            launch_adam(*dev, *net, step, lr, &guard, &copy, test);
         }
         HIP_CHECK(hipEventRecord(dev->copied, dev->stream));
         dev->issued = Device::IssuedUpdate{true, net, costs, layers, with_graph != 0, method == 0, wt_current, fresh};
     });
+}
+
+int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net, int method, int step,
+                      float lr) {
+    return issue_update(dev, costs, layers, with_graph, net, method, step, lr, false, false);
+}
+
+int cpde_inspect_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net, int method,
+                              int step, float lr, int full_stats) {
+    return issue_update(dev, costs, layers, with_graph, net, method, step, lr, true, full_stats != 0);
 }
 
 int cpde_update_resolve(cpde_device* dev, cpde_cost_stats* cost_out, cpde_gradient_stats* gradient_out,

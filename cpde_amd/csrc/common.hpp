@@ -450,10 +450,17 @@ struct ScalarPublish {
     void* dst;
     size_t bytes;  // a multiple of 4
 };
-void launch_rprop(Device& d, Net& net, const UpdateGuard* guard = nullptr, const ScalarPublish* publish = nullptr);
+// test: the launch tests the gradients for finiteness itself and writes the
+// gradient totals in their short form (only where update_tests(net) holds).
+void launch_rprop(Device& d, Net& net, const UpdateGuard* guard = nullptr, const ScalarPublish* publish = nullptr,
+                  bool test = false);
 // Adam step `step`; with `guard`, only where the rule accepts the epoch.
 void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* guard = nullptr,
-                 const ScalarPublish* publish = nullptr);
+                 const ScalarPublish* publish = nullptr, bool test = false);
+// Whether an update launch can test the network's gradients itself: one
+// transition group whose entries fit the launch's chunk table (10,240 and
+// fewer, about).
+bool update_tests(const Net& net);
 void launch_set_steps(Device& d, Net& net, float value);
 void launch_restore_steps(Device& d, Net& net, float floor_value);
 GraphLaunch graph_launch(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,

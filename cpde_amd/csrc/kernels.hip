@@ -532,6 +532,13 @@ __global__ __launch_bounds__(256, 2) void wgrad_grouped_kernel(WgradArgs a) {
 
 // Optimizers: one launch covers every transition.  Each transition's buffers
 // are separate allocations; the launch carries their pointers by value.
+constexpr int kOptimizerThreads = 256;
+
+// Chunks of an update launch's own finiteness test (OptimizerArgs::test),
+// kOptimizerThreads entries each: every lane loads its entry of every one, so
+// their number is kept small (10,240 entries and fewer, about).
+constexpr int kTestChunks = 40;
+
 struct OptimizerArgs {
     float* W[kMaxTransitions];
     float* S[kMaxTransitions];   // RPROP step / Adam first moment
@@ -553,26 +560,102 @@ struct OptimizerArgs {
     const unsigned* publish_src;
     unsigned* publish_dst;
     int publish_words;
+    // test: the launch tests the active gradients for finiteness itself where
+    // the rule would read the gradient totals (the transitions' entries make at
+    // most kTestChunks chunks), and its first workgroup writes stats[t] = {0,
+    // 0, whether transition t has a non-finite entry, none}, into the totals
+    // and straight into the host mirror, before it releases the publish copy
+    int test;
+    GradStats* stats;
 };
 
 // The scalar block to the host, by the first workgroup of an update launch,
 // released to the system before the launch ends.
+// A launch with its own finiteness test copies all but the gradient totals,
+// unreleased: test_gradients writes those and releases the copy.
 __device__ __forceinline__ void publish_scalars(const OptimizerArgs& a) {
     if (!a.publish_dst || blockIdx.x != 0) return;
-    for (int i = threadIdx.x; i < a.publish_words; i += blockDim.x) a.publish_dst[i] = a.publish_src[i];
-    __threadfence_system();
+    int skip_begin = 0, skip_end = 0;
+    if (a.test) {
+        skip_begin = int(reinterpret_cast<const unsigned*>(a.stats) - a.publish_src);
+        skip_end = skip_begin + a.transitions * int(sizeof(GradStats) / sizeof(unsigned));
+    }
+    for (int i = threadIdx.x; i < a.publish_words; i += blockDim.x)
+        if (i < skip_begin || i >= skip_end) a.publish_dst[i] = a.publish_src[i];
+    if (!a.test) __threadfence_system();
+}
+
+// The launch's own finiteness test (OptimizerArgs::test): lane c lays chunk c
+// of the transitions' entries out in LDS (where it starts, how many entries,
+// which transition), then every lane loads its entry of every chunk at once
+// (one round of loads for the whole network; a slot past the last chunk loads
+// that chunk again, with no branch to hold the loads back), the workgroup ORs
+// the transitions with a non-finite entry into one mask, and the first
+// workgroup writes the totals.  Whether every entry is finite, on every lane.
+__device__ bool test_gradients(const OptimizerArgs& a) {
+    // chunk c: {address low and high words, its last entry's lane, transition}
+    __shared__ int4 chunk[kTestChunks];
+    __shared__ unsigned bad_mask;
+    const int lane = threadIdx.x;
+    int chunks = 0;
+    for (int t = 0; t < a.transitions; ++t) {
+        const int count = a.begin[t + 1] - a.begin[t];
+        const int n = (count + kOptimizerThreads - 1) / kOptimizerThreads;
+        if (lane >= chunks && lane < chunks + n && lane < kTestChunks) {
+            const int start = (lane - chunks) * kOptimizerThreads;
+            const unsigned long long p = reinterpret_cast<unsigned long long>(a.Ga[t] + start);
+            chunk[lane] = make_int4(int(unsigned(p)), int(unsigned(p >> 32)),
+                                    min(kOptimizerThreads, count - start) - 1, t);
+        }
+        chunks += n;
+    }
+    chunks = min(chunks, kTestChunks);
+    if (lane == 0) bad_mask = 0;
+    __syncthreads();
+    // global (not flat) loads: a flat load would count against the LDS reads'
+    // wait too
+    typedef const __attribute__((address_space(1))) float* global_floats;
+    int4 e[kTestChunks];
+#pragma unroll
+    for (int c = 0; c < kTestChunks; ++c) e[c] = chunk[min(c, chunks - 1)];
+    float v[kTestChunks];
+#pragma unroll
+    for (int c = 0; c < kTestChunks; ++c) {
+        const unsigned long long p = unsigned(e[c].x) | (static_cast<unsigned long long>(unsigned(e[c].y)) << 32);
+        v[c] = reinterpret_cast<global_floats>(p)[min(lane, e[c].z)];
+    }
+    unsigned mask = 0;
+#pragma unroll
+    for (int c = 0; c < kTestChunks; ++c)
+        if (!isfinite(v[c])) mask |= 1u << e[c].w;
+    __syncthreads();  // bad_mask is cleared
+    if (mask) atomicOr(&bad_mask, mask);
+    __syncthreads();
+    const unsigned m = bad_mask;
+    if (blockIdx.x == 0 && a.publish_dst) {
+        if (threadIdx.x < a.transitions) {
+            const GradStats r{0.0, 0.0, (m >> threadIdx.x) & 1u, INT_MAX, 0};
+            a.stats[threadIdx.x] = r;
+            const int offset = int(reinterpret_cast<const unsigned*>(a.stats) - a.publish_src);
+            reinterpret_cast<GradStats*>(a.publish_dst + offset)[threadIdx.x] = r;
+        }
+        __threadfence_system();
+    } else if (blockIdx.x == 0 && threadIdx.x < a.transitions) {
+        a.stats[threadIdx.x] = GradStats{0.0, 0.0, (m >> threadIdx.x) & 1u, INT_MAX, 0};
+    }
+    return m == 0;
 }
 
 // The guarded update's rule, the same on every lane of the grid; the first
 // lane records it for the reductions that wait on it (ReduceArgs::gate).
-__device__ __forceinline__ bool update_applies(const OptimizerArgs& a) {
+// `finite`: the launch's own test of the gradients (OptimizerArgs::test_*).
+__device__ __forceinline__ bool update_applies(const OptimizerArgs& a, bool finite = true) {
     if (!a.guarded) return true;
-    const bool ok = update_accepted(a.guard);
+    const bool ok = finite && update_accepted(a.guard);
     if (a.verdict && blockIdx.x == 0 && threadIdx.x == 0) *a.verdict = ok ? 1 : 0;
     return ok;
 }
 
-constexpr int kOptimizerThreads = 256;
 
 // Entry j = o + NO*i of a weight block into its row-major copy (bias column i = NI excluded).
 __device__ __forceinline__ void copy_transposed(const OptimizerArgs& a, int t, int j, float w) {
@@ -1693,7 +1776,8 @@ __global__ __launch_bounds__(kOptimizerThreads) void rprop_kernel(OptimizerArgs 
         g = a.Ga[t][j];
     }
     publish_scalars(a);
-    if (!update_applies(a)) return;
+    const bool finite = !a.test || test_gradients(a);
+    if (!update_applies(a, finite)) return;
     if (mine) rprop_update(a, t, j, g, e);
 }
 
@@ -1711,7 +1795,8 @@ __global__ __launch_bounds__(kOptimizerThreads) void adam_kernel(OptimizerArgs a
         w = a.W[t][j];
     }
     publish_scalars(a);
-    if (!update_applies(a)) return;
+    const bool finite = !a.test || test_gradients(a);
+    if (!update_applies(a, finite)) return;
     if (mine) {
         m = beta1 * m + (1 - beta1) * g;
         v = beta2 * v + (1 - beta2) * g * g;
@@ -1772,7 +1857,24 @@ static void set_publish(OptimizerArgs& a, const ScalarPublish* publish, bool& fi
     a.publish_words = int(publish->bytes / sizeof(unsigned));
 }
 
-void launch_rprop(Device& d, Net& net, const UpdateGuard* guard, const ScalarPublish* publish) {
+bool update_tests(const Net& net) {
+    const int T = net.layers - 1;
+    if (T > kMaxTransitions) return false;
+    int chunks = 0;
+    for (int t = 0; t < T; ++t) chunks += (net.param_count(t) + kOptimizerThreads - 1) / kOptimizerThreads;
+    return chunks <= kTestChunks;
+}
+
+// The launch's own finiteness test over the group's active gradients, the
+// totals written to the device's gradient slots (update_tests(net) holds:
+// one transition group).
+static void set_test(Device& d, OptimizerArgs& a, bool test) {
+    if (!test) return;
+    a.test = 1;
+    a.stats = d.grad_totals;
+}
+
+void launch_rprop(Device& d, Net& net, const UpdateGuard* guard, const ScalarPublish* publish, bool test) {
     bool first = true;
     for_transition_groups(net, [&](OptimizerArgs a, int blocks) {
         if (guard) {
@@ -1781,6 +1883,7 @@ void launch_rprop(Device& d, Net& net, const UpdateGuard* guard, const ScalarPub
             a.verdict = d.update_verdict;
         }
         set_publish(a, publish, first);
+        set_test(d, a, test);
         TraceScope trace(d, kTraceOptimizer, 28.0 * a.begin[a.transitions]);  // 4 reads, 3 writes per entry
         hipLaunchKernelGGL(rprop_kernel, blocks, kOptimizerThreads, 0, d.stream, a);
         HIP_CHECK(hipGetLastError());
@@ -1790,7 +1893,8 @@ void launch_rprop(Device& d, Net& net, const UpdateGuard* guard, const ScalarPub
     net.wt_current = true;
 }
 
-void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* guard, const ScalarPublish* publish) {
+void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* guard, const ScalarPublish* publish,
+                 bool test) {
     const float b1 = 0.9f, b2 = 0.999f;
     const float b1t = std::pow(b1, float(step)), b2t = std::pow(b2, float(step));
     bool first = true;
@@ -1801,6 +1905,7 @@ void launch_adam(Device& d, Net& net, int step, float lr, const UpdateGuard* gua
             a.verdict = d.update_verdict;
         }
         set_publish(a, publish, first);
+        set_test(d, a, test);
         hipLaunchKernelGGL(adam_kernel, blocks, kOptimizerThreads, 0, d.stream, a, lr, b1, b2, b1t, b2t);
         HIP_CHECK(hipGetLastError());
     });

@@ -760,7 +760,7 @@ private:
     // launches, then the graph, those launches and the gradient statistics.
     bool halves_apply(const std::vector<uint64_t>& ids, const GraphRecord* graph);
     void first_half(NetRecord& n, const std::vector<uint64_t>& ids, GraphRecord* graph, bool collect);
-    void second_half(NetRecord& n);
+    void second_half(NetRecord& n, int costs, int layers, bool graph, int method, bool full_stats);
     void download(int costs, int layers, std::vector<cpde_cost_stats>& cs, std::vector<cpde_gradient_stats>& gs,
                   GraphRecord* graph = nullptr);
     void validate_costs(const std::vector<cpde_cost_stats>& cs, std::vector<double>& values, bool before_update);
@@ -1018,10 +1018,15 @@ void Server::first_half(NetRecord& n, const std::vector<uint64_t>& ids, GraphRec
         pass(n, cost(ids[i]), int(i), first, Pass{true, collect, nullptr, 0, INT_MAX, false});
 }
 
-// The second half: the waiting gradient launches, the statistics.
-void Server::second_half(NetRecord& n) {
+// The second half: the waiting gradient launches, then the statistics and
+// the update issued in one call (the update applies only if the epoch passes
+// the checks, which cpde_update_resolve reports).  full_stats: the whole
+// gradient statistics are reported this epoch; otherwise the library may hand
+// out short ones, and a rejected epoch's are taken whole afterwards.
+void Server::second_half(NetRecord& n, int costs, int layers, bool graph, int method, bool full_stats) {
     call(cpde_gradients_defer(dev_, 0));
-    call(cpde_inspect_gradients(n.net));
+    call(cpde_inspect_update_issue(dev_, costs, layers, graph ? 1 : 0, n.net, method,
+                                   method == 1 ? int(n.adam_step + 1) : 0, n.learning_rate, full_stats ? 1 : 0));
 }
 
 // Server::validate_costs (cuda/cpde_server.cu:341-352).
@@ -1387,6 +1392,10 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
         }
     } ahead_guard{dev_, ahead, halves};
     auto collect_at = [&](uint64_t done) { return (log && (done + 1) % log == 0) || done + 1 == epochs; };
+    // the epochs after which the gradient statistics are reported (event 5)
+    auto reports_diagnostics = [&](uint64_t done) {
+        return diagnostics && ((done + 1) % diagnostics == 0 || done + 1 == epochs);
+    };
     while (completed < epochs && (ahead || !stop.load())) {
         const bool collect = collect_at(completed);
         // RPROP goes out behind the download and applies only if the checks
@@ -1396,10 +1405,9 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
         if (halves) {
             if (!ahead) first_half(n, ids, graph.get(), collect);
             ahead = false;
-            second_half(n);
             require(method == 0 || n.adam_step < uint64_t(INT_MAX), "Adam counter exceeds supported range");
-            call(cpde_update_issue(dev_, int(ids.size()), layers, graph ? 1 : 0, n.net, method,
-                                   method == 1 ? int(n.adam_step + 1) : 0, n.learning_rate));
+            const bool full_stats = reports_diagnostics(completed);
+            second_half(n, int(ids.size()), layers, graph != nullptr, method, full_stats);
             const uint64_t next = completed + 1;
             const bool acts = next == epochs || (eval && next % eval == 0) || (save && next % save == 0) ||
                               (restore_every && (n.updates + 1) % restore_every == 0) || stop.load();
@@ -1420,6 +1428,12 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
             call(cpde_update_resolve(dev_, cs.data(), gs.data(), graph ? &graph->host : nullptr, &updated));
             cs.resize(ids.size());
             gs.resize(layers);
+            bool short_bad = false;
+            for (const auto& g : gs) short_bad = short_bad || (!full_stats && g.nonfinite_count != 0);
+            if (short_bad) {  // the report of a rejected epoch: its untouched gradients' whole statistics
+                call(cpde_inspect_gradients(n.net));
+                call(cpde_scalars_download(dev_, 0, nullptr, layers, gs.data()));
+            }
         } else {
             gradient_epoch(replays, n, completed > 0, collect, [&] {
                 if (graph) graph_pass(n, ids, *graph, true);
@@ -1438,7 +1452,7 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
         }
         bool bad_gradient = false;
         for (const auto& g : gs) bad_gradient = bad_gradient || g.nonfinite_count != 0;
-        if (bad_gradient || (diagnostics && ((completed + 1) % diagnostics == 0 || completed + 1 == epochs))) {
+        if (bad_gradient || reports_diagnostics(completed)) {
             Frame r;
             r.put<uint64_t>(completed + 1).put<uint64_t>(n.updates).put<int32_t>(layers);
             for (const auto& g : gs)

@@ -79,6 +79,7 @@ SIGNATURES = {
     'cpde_rprop': (i32, [vp]),
     'cpde_scalars_download_rprop': (i32, [vp, i32, vp, i32, vp, vp, vp, vp]),
     'cpde_update_issue': (i32, [vp, i32, i32, i32, vp, i32, i32, f32]),
+    'cpde_inspect_update_issue': (i32, [vp, i32, i32, i32, vp, i32, i32, f32, i32]),
     'cpde_update_resolve': (i32, [vp, vp, vp, vp, vp]),
     'cpde_gradients_discard': (i32, [vp]),
     'cpde_adam': (i32, [vp, i32, f32]),
@@ -304,6 +305,27 @@ class Net:
         updated = i32()
         check(load().cpde_scalars_download_rprop(self.device.handle, costs, ctypes.cast(c, vp), layers,
                                                  ctypes.cast(g, vp), None, self.handle, ctypes.byref(updated)))
+        return list(c)[:costs], list(g), updated.value
+
+    def issue_update(self, costs=0, method=0, step=0, lr=0.0, inspect=None):
+        """cpde_update_issue (no graph); with `inspect` ('full' or 'short'),
+        cpde_inspect_update_issue: the gradient statistics taken first, or the
+        update launch's own finiteness test where the network allows."""
+        layers = len(self.neurons) - 1
+        if inspect is None:
+            check(load().cpde_update_issue(self.device.handle, costs, layers, 0, self.handle, method, step, lr))
+        else:
+            check(load().cpde_inspect_update_issue(self.device.handle, costs, layers, 0, self.handle, method, step, lr,
+                                                   int(inspect == 'full')))
+
+    def resolve_update(self, costs=0):
+        """cpde_update_resolve: cost and gradient totals, and whether the update applied."""
+        layers = len(self.neurons) - 1
+        c = (CostStats * max(costs, 1))()
+        g = (GradientStats * layers)()
+        updated = i32()
+        check(load().cpde_update_resolve(self.device.handle, ctypes.cast(c, vp), ctypes.cast(g, vp), None,
+                                         ctypes.byref(updated)))
         return list(c)[:costs], list(g), updated.value
 
     def adam(self, step, lr):

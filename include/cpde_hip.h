@@ -273,6 +273,18 @@ int cpde_scalars_download_rprop(cpde_device* dev, int costs, cpde_cost_stats* co
  * time. */
 int cpde_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net, int method, int step,
                       float lr);
+/* cpde_inspect_gradients(net), then cpde_update_issue, as one call (the
+ * reference takes the statistics and then updates, cuda/cpde_server.cu:394-410,
+ * with no call of its own for the pair).  With full_stats = 0, on a network of
+ * one transition group whose weights and biases fit the launch's chunk table
+ * (40 chunks of 256 per transition group, about 10,240 entries), the update
+ * launch tests the gradients for finiteness itself instead, and the gradient
+ * totals it hands out are short: nonfinite_count 1 where the transition has a
+ * non-finite entry (else 0), first_nonfinite none, squared norm and maximum 0.
+ * The verdict is the same; for whole statistics of a rejected epoch, call
+ * cpde_inspect_gradients afterwards (the gradients are untouched). */
+int cpde_inspect_update_issue(cpde_device* dev, int costs, int layers, int with_graph, cpde_net* net, int method,
+                              int step, float lr, int full_stats);
 /* The second half: wait for that launch, hand out the scalars (as
  * cpde_scalars_download_graph does) and say whether the update applied; where
  * it did not, RPROP's buffers switch back. */

@@ -128,6 +128,53 @@ def test_download_rprop_updates_only_on_clean_scalars(device, net):
             np.testing.assert_array_equal(net.state(t, 3 - act), rgi)
 
 
+@pytest.mark.parametrize('stats', ['full', 'short'])
+@pytest.mark.parametrize('method', [0, 1], ids=['rprop', 'adam'])
+@pytest.mark.parametrize('neurons', [NEURONS, [2, 128, 128, 128, 1]], ids=['tested', 'separate'])
+def test_inspecting_update_matches_inspect_then_update(device, neurons, method, stats):
+    """cpde_inspect_update_issue against cpde_inspect_gradients followed by
+    cpde_update_issue on the same crafted states, clean and with infinite
+    gradient entries: the same verdict and the same states, bit for bit.  The
+    gradient totals are the same too, except where the update launch tested the
+    gradients itself (3->40->33->7->2, 1,767 entries, short statistics asked
+    for): then each transition's non-finite count is 1 if it has any non-finite
+    entry, and the rest is left empty.  2->128->128->128->1 (33,537 entries in
+    133 chunks of 256) is beyond the launch's chunk table of 40 and runs both
+    launches."""
+    T = len(neurons) - 1
+    nets = [hip.Net(device, neurons, W.linear_flags(neurons), W.xavier_weights(neurons, 2)) for _ in range(2)]
+    for clean in (True, False):
+        for t in range(T):
+            st = crafted(neurons[t + 1] * (neurons[t] + 1), 500 + t)
+            if clean:
+                st[2][~np.isfinite(st[2])] = np.float32(1.5)
+            for n in nets:
+                load_state(n, t, *st)
+        nets[0].inspect_gradients()
+        nets[0].issue_update(0, method, 1, 0.01)
+        _, g0, u0 = nets[0].resolve_update(0)
+        nets[1].issue_update(0, method, 1, 0.01, inspect=stats)
+        _, g1, u1 = nets[1].resolve_update(0)
+        device.synchronize()
+        print(f'[case] neurons={neurons} method={method} stats={stats} clean={clean}: updated {u0} / {u1}, '
+              f'non-finite {[g.nonfinite_count for g in g0]} / {[g.nonfinite_count for g in g1]}', flush=True)
+        assert u0 == u1 == (1 if clean else 0)
+        short = stats == 'short' and neurons == NEURONS
+        for a, b in zip(g0, g1):
+            if short:
+                assert (b.nonfinite_count, b.first_nonfinite, b.squared_norm, b.max_abs) == \
+                    (int(a.nonfinite_count > 0), 2**31 - 1, 0.0, 0.0)
+            else:
+                assert (a.nonfinite_count, a.first_nonfinite, a.squared_norm, a.max_abs) == \
+                    (b.nonfinite_count, b.first_nonfinite, b.squared_norm, b.max_abs)
+        for t in range(T):
+            assert nets[0].active(t) == nets[1].active(t)
+            for k in range(4):
+                np.testing.assert_array_equal(nets[0].state(t, k), nets[1].state(t, k))
+    for n in nets:
+        n.destroy()
+
+
 @pytest.mark.parametrize('mode', ['set', 'restore'])
 def test_set_and_restore_steps_bit_exact(device, net, mode):
     T = len(NEURONS) - 1
