@@ -704,8 +704,12 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
        << prefetch << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
        << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
        << "    __syncthreads();\n";
+    // the last hidden layer's y (read from X by the output layer's partial) and
+    // the first one's dE/dz (read from X by the input transition's) stay in the
+    // workgroup: no later launch reads them
     for (int t = 1; t + 2 < L; ++t)
-        ep << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
+        ep << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << (t + 3 == L ? ", false" : "") << ">(a, " << t
+           << ", X, T, p0, npts);\n";
     const std::string last = std::to_string(neurons[L - 2]);
     ep << "    float ua[R];  // the last hidden layer's u rows, in flight during the output layer and the cost\n"
        << "    u_ahead<" << last << ", output_adjoint_split<" << last << ">()>(a, " << L - 2 << ", p0, npts, ua);\n"
@@ -714,7 +718,8 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
        << cost << "    net_output_backward<" << neurons[L - 2] << ", " << NO << ", true>(a, " << L - 2
        << ", X, p0, npts, ua, O + kNNC * " << NO << ");\n";
     for (int t = L - 3; t >= 1; --t)
-        ep << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << ">(a, " << t << ", X, T, p0, npts);\n";
+        ep << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << (t == 1 ? ", false" : "") << ">(a, "
+           << t << ", X, T, p0, npts);\n";
     ep << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
     return ep.str();
 }

@@ -192,7 +192,10 @@ int cpde_cost_matching(cpde_plan* plan, const float* target, int target_width, c
  * them as separate launches; on the network-fused kernels, when the chunk's
  * workgroups fit on the device together, this is one launch (a point's
  * matching terms depend on that point alone), the cost's finish and the
- * weight-gradient contraction.  The input chunk must be activated. */
+ * weight-gradient contraction.  The input chunk must be activated.  That one
+ * launch leaves two stacks unwritten, which no later launch reads: y of the
+ * last hidden layer and dE/dz of the first (cpde_plan_stack kinds 1 and 2);
+ * read them after the separate calls instead. */
 int cpde_epoch_matching(cpde_plan* plan, const float* target, int target_width, const int* target_rows,
                         const float* weights, int weight_samples, int offset, int valid, int cost_index, int collect,
                         int accumulate);
@@ -331,7 +334,8 @@ int cpde_cost_expression(cpde_plan* plan, cpde_program* program, const double* f
  * and adjoint depend on that sample alone; the program is compiled into the
  * network module on first use), the cost's finish and the weight-gradient
  * contraction.  The multiplier must be final when the call is made.  The input
- * chunk must be activated. */
+ * chunk must be activated.  The one launch leaves the same two stacks
+ * unwritten as cpde_epoch_matching's. */
 int cpde_epoch_expression(cpde_plan* plan, cpde_program* program, const double* fields,
                           const double* quadrature_weights, int samples, int offset, int valid,
                           const double* multiplier, void* scratch, int cost_index, int collect, int accumulate);
