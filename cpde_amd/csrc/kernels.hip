@@ -511,6 +511,18 @@ __device__ __forceinline__ void wgrad_thin(const WgradArgs& a, int t, int split,
 // XCD with its own L2.  This renumbering gives every XCD a contiguous range of
 // work items, so that the tiles of one split, which read the same rows of G
 // or Y, run under one L2.  It is a permutation of [0, n) for any n.
+// The group whose range [begin[t], begin[t + 1]) holds b (b in [0,
+// begin[count])).  Every boundary is loaded at once and compared, instead of a
+// search whose every step waits on the load before it: kernel arguments come
+// through the scalar cache, which is cold at each launch, so each such step
+// costs a memory round trip before the workgroup's first real load.
+__device__ __forceinline__ int group_of(const int (&begin)[kMaxTransitions + 1], int count, int b) {
+    int t = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxTransitions; ++k) t += (k < count && b >= begin[k]) ? 1 : 0;
+    return t;
+}
+
 __device__ __forceinline__ int xcd_grouped(int b, int n) {
     const int x = b & 7, q = b >> 3, per = (n + 7) >> 3, full = (n & 7) ? (n & 7) : 8;
     return x < full ? x * per + q : full * per + (x - full) * (per - 1) + q;
@@ -522,8 +534,7 @@ __global__ __launch_bounds__(256, 2) void wgrad_grouped_kernel(WgradArgs a) {
     __shared__ __attribute__((aligned(16))) float lds[kWgLds];
     static_assert(256 * 17 <= kWgLds, "thin-transition scratch exceeds the shared LDS");
     const int b = xcd_grouped(int(blockIdx.x), int(gridDim.x));
-    int t = 0;
-    while (t + 1 < a.transitions && b >= a.block_begin[t + 1]) ++t;
+    const int t = group_of(a.block_begin, a.transitions, b);
     const int local = b - a.block_begin[t];
     if (a.M[t] <= 16 || a.N[t] <= 16) wgrad_thin(a, t, local, lds);
     else if (a.tile[t] == 64) wgrad_tile<64>(a, t, local, lds);
@@ -735,8 +746,7 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int block = int(blockIdx.x) - cost_block;
-    int t = 0;
-    while (t + 1 < a.transitions && block >= a.block_begin[t + 1]) ++t;
+    const int t = group_of(a.block_begin, a.transitions, block);
     const int local = block - a.block_begin[t];
     const int M = a.M[t], N1 = a.N[t] + 1, S = a.splits[t];
     const int count = M * N1;
@@ -1095,8 +1105,7 @@ __global__ __launch_bounds__(256, CPDE_WD_MIN_BLOCKS) void wgrad_direct_kernel(W
     __shared__ __attribute__((aligned(16))) float lds[kWdLds];
     static_assert(256 * 17 <= kWdLds, "thin-transition scratch exceeds the shared LDS");
     const int b = xcd_grouped(int(blockIdx.x), int(gridDim.x));
-    int t = 0;
-    while (t + 1 < a.transitions && b >= a.block_begin[t + 1]) ++t;
+    const int t = group_of(a.block_begin, a.transitions, b);
     const int local = b - a.block_begin[t];
     if (a.M[t] <= 16 || a.N[t] <= 16) wgrad_thin(a, t, local, lds);
     else if (a.M[t] % 4 == 0 && a.N[t] % 4 == 0) wgrad_direct_tile<true>(a, t, local, lds);
@@ -1757,8 +1766,7 @@ void launch_fill(Device& d, float* p, size_t count, float value) {
 // Entry j of transition t for this lane: each block lies within one
 // transition, so t and its pointers are uniform (scalar loads).
 __device__ __forceinline__ bool entry_of(const OptimizerArgs& a, int& t, int& j) {
-    t = 0;
-    while (t + 1 < a.transitions && int(blockIdx.x) >= a.block_begin[t + 1]) ++t;
+    t = group_of(a.block_begin, a.transitions, int(blockIdx.x));
     j = (int(blockIdx.x) - a.block_begin[t]) * kOptimizerThreads + int(threadIdx.x);
     return j < a.begin[t + 1] - a.begin[t];
 }

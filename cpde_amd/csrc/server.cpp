@@ -1430,7 +1430,15 @@ void Server::train(Frame& b, std::atomic<bool>& stop, bool graph_mode) {
             gs.resize(layers);
             bool short_bad = false;
             for (const auto& g : gs) short_bad = short_bad || (!full_stats && g.nonfinite_count != 0);
-            if (short_bad) {  // the report of a rejected epoch: its untouched gradients' whole statistics
+            if (short_bad) {
+                // the report of a rejected epoch: its untouched gradients' whole
+                // statistics, after the next epoch's first half is dropped (the
+                // statistics launch would send its waiting launches out, no
+                // longer gated on the resolved update)
+                if (ahead) {
+                    call(cpde_gradients_discard(dev_));
+                    ahead = false;
+                }
                 call(cpde_inspect_gradients(n.net));
                 call(cpde_scalars_download(dev_, 0, nullptr, layers, gs.data()));
             }

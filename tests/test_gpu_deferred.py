@@ -111,13 +111,15 @@ def run_counted(env, body, counts):
     return result, json.loads(counts.read_text())
 
 
-def rejected_at_epoch_one(method):
+def rejected_at_epoch_one(method, diagnostics=1):
     """u = w x + b on one point, w = 0, b = 1, cost (k u)^2: epoch 0 is clean;
     its update moves w, so epoch 1 overflows and is rejected -- after epoch
     1's first passes went out behind epoch 0's update.  RPROP: x = 1e30, k = 1
     (epoch 0: dE/dw 2e30; epoch 1's objective overflows).  Adam: x = 1e22,
     k^2 = 5e-4 (epoch 0: dE/dw 1e19, whose square Adam's second moment still
-    holds; a first step of about lr makes epoch 1's dE/dw about -1e39)."""
+    holds; a first step of about lr makes epoch 1's dE/dw about -1e39).
+    diagnostics=0: the update launches test the gradients themselves, and the
+    rejected epoch's report takes its statistics afterwards."""
     x, k = (1e30, 1.0) if method == 0 else (1e22, np.sqrt(5e-4))
 
     def body(s):
@@ -126,7 +128,7 @@ def rejected_at_epoch_one(method):
         c = s.polynomial_cost(n, d, [0], 1, [[0, 0, -1]], np.full((1, 1), k, np.float32),
                               np.zeros((1, 1), np.float32), np.ones((1, 1), np.float32))
         with pytest.raises(wire.ServerError) as err:
-            s.train(n, [c], 4, method=method, fresh=1, lr=0.01, log=1, diagnostics=1)
+            s.train(n, [c], 4, method=method, fresh=1, lr=0.01, log=1, diagnostics=diagnostics)
         return str(err.value), canonical(err.value.events), s.snapshot(n)
     return body
 
@@ -134,7 +136,7 @@ def rejected_at_epoch_one(method):
 SQUARE = ([(1, 0, 0), (7, 0, -1)], [0.0, 2.0])  # u ** 2 (scalar ops Component 1, Power 7)
 
 
-def rejected_integrals(method, layout):
+def rejected_integrals(method, layout, diagnostics=1):
     """u = w x + b (w = 0, b = 1) under integral costs q u**2: epoch 0 is clean;
     its update moves w, so epoch 1's dE/dw = 2 u q x overflows in fp32 and is
     rejected, after epoch 2's first half went out behind epoch 1's update.
@@ -145,7 +147,8 @@ def rejected_integrals(method, layout):
         backward pass launches the first two's reduction.
     RPROP: x = 1e30, q = 1.  Adam: x = 1e22 and q = 5e-4 / samples, so that
     epoch 0's dE/dw is 1e19, whose square Adam's second moment still holds,
-    and a first step of about lr gives epoch 1 a dE/dw of about -1e39."""
+    and a first step of about lr gives epoch 1 a dE/dw of about -1e39.
+    diagnostics=0: as in rejected_at_epoch_one."""
     samples = 2 if layout == 'graph' else 3
     x, q = (1e30, 1.0) if method == 0 else (1e22, 5e-4 / samples)
 
@@ -161,7 +164,7 @@ def rejected_integrals(method, layout):
             costs = [s.integral_cost(n, d, *SQUARE, np.zeros((0, 3)), [q] * 3, chunk=1)]
             graph = None
         with pytest.raises(wire.ServerError) as err:
-            s.train(n, costs, 6, method=method, fresh=1, lr=0.01, log=1, diagnostics=1, graph=graph)
+            s.train(n, costs, 6, method=method, fresh=1, lr=0.01, log=1, diagnostics=diagnostics, graph=graph)
         return str(err.value), canonical(err.value.events), s.snapshot(n)
     return body
 
@@ -180,7 +183,10 @@ def two_costs_adam(s):
                                        ('rejected-graph', rejected_integrals(0, 'graph')),
                                        ('rejected-graph-adam', rejected_integrals(1, 'graph')),
                                        ('rejected-chunks', rejected_integrals(0, 'chunks')),
-                                       ('rejected-chunks-adam', rejected_integrals(1, 'chunks'))])
+                                       ('rejected-chunks-adam', rejected_integrals(1, 'chunks')),
+                                       ('rejected-short', rejected_at_epoch_one(0, 0)),
+                                       ('rejected-graph-short', rejected_integrals(0, 'graph', 0)),
+                                       ('rejected-chunks-adam-short', rejected_integrals(1, 'chunks', 0))])
 def test_epochs_in_halves_match_whole_epochs(tmp_path, name, body):
     """Training (RPROP and Adam) with each epoch's first passes sent before
     the previous epoch's scalars are back (its update guarded on the device)
