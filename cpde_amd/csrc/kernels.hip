@@ -727,21 +727,24 @@ __device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int 
 // fixed shuffle tree.  Either way the summation order is fixed whatever the
 // scheduling.
 __device__ void finish_costs(const ReduceArgs& a);
-__device__ void run_graph_block(const GraphLaunch& g, bool fresh = false);
+__device__ void graph_stage(const GraphLaunch& g);
+__device__ void graph_run(const GraphLaunch& g, bool fresh);
 
 // UPDATE: the lane that finishes an entry's gradient applies RPROP to it
 // (reduce_rprop_kernel), which is the reduction followed by rprop_kernel in one
 // launch, bit for bit; it loads the entry's optimizer state (and, accumulating,
 // its gradient) before the partials, so that the two loads' latencies overlap.
 // Block 0 finishes the costs and evaluates the graph when the launch carries
-// them: the longest chain of the launch is dispatched first.
+// them: the longest chain of the launch is dispatched first, and the graph's
+// nodes are loaded before the costs are finished.
 template <bool UPDATE>
 __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const OptimizerArgs& o) {
-    __shared__ float part[4][64];
+    __shared__ float part[2][4][64];
     const int cost_block = a.costs || a.with_graph ? 1 : 0;
     if (cost_block && blockIdx.x == 0) {
+        if (a.with_graph) graph_stage(a.graph);
         finish_costs(a);
-        if (a.with_graph) run_graph_block(a.graph, true);
+        if (a.with_graph) graph_run(a.graph, true);
         return;
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -767,7 +770,11 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
             for (int u = 0; u < U; u += 2 * w) acc[u] += acc[u + w];
         return acc[0];
     };
+    // A second pass's partials (splits2 > 0) are summed in the same rounds of
+    // loads as the first's, each into running sums of its own, so the two
+    // sums are what two rounds in turn give, bit for bit.
     const bool two = a.splits2[t] > 0;  // uniform over the block
+    const int S2 = two ? a.splits2[t] : 0, Smax = max(S, S2);
     if (!a.split_minor[t]) {
         const size_t stride = size_t(count);
         const int j = local * 64 + lane;
@@ -779,31 +786,35 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
             if constexpr (UPDATE) e = rprop_state(o, t, idx);
             if (a.accumulate) before = a.grad[t][idx];
         }
-        // every wave; the sum of entry j is valid on wave 0's lane
-        auto sum_major = [&](const float* base, int S) {
-            float s = 0.0f;
-            if (j < count) {
-                const float* P = base + j;
-                float acc[U];
+        // every wave; the sums of entry j are valid on wave 0's lane
+        float s1 = 0.0f, s2 = 0.0f;
+        if (j < count) {
+            const float* P1 = a.partial[t] + j;
+            const float* P2 = two ? a.partial2[t] + j : P1;
+            float acc1[U], acc2[U];
 #pragma unroll
-                for (int u = 0; u < U; ++u) acc[u] = 0.0f;
-                for (int q = wave; q < S; q += 4 * U) {  // wave w: splits w, w + 4, ...
-                    float v[U];
+            for (int u = 0; u < U; ++u) acc1[u] = acc2[u] = 0.0f;
+            for (int q = wave; q < Smax; q += 4 * U) {  // wave w: splits w, w + 4, ...
+                float v1[U], v2[U];
 #pragma unroll
-                    for (int u = 0; u < U; ++u) v[u] = P[size_t(min(q + 4 * u, S - 1)) * stride];
+                for (int u = 0; u < U; ++u) v1[u] = P1[size_t(min(q + 4 * u, S - 1)) * stride];
+                if (two)
 #pragma unroll
-                    for (int u = 0; u < U; ++u) acc[u] += q + 4 * u < S ? v[u] : 0.0f;
-                }
-                s = tree(acc);
+                    for (int u = 0; u < U; ++u) v2[u] = P2[size_t(min(q + 4 * u, S2 - 1)) * stride];
+#pragma unroll
+                for (int u = 0; u < U; ++u) acc1[u] += q + 4 * u < S ? v1[u] : 0.0f;
+                if (two)
+#pragma unroll
+                    for (int u = 0; u < U; ++u) acc2[u] += q + 4 * u < S2 ? v2[u] : 0.0f;
             }
-            part[wave][lane] = s;
-            __syncthreads();
-            const float sum = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
-            __syncthreads();  // part is reused
-            return sum;
-        };
-        const float sum = sum_major(a.partial[t], S);
-        const float sum2 = two ? sum_major(a.partial2[t], a.splits2[t]) : 0.0f;
+            s1 = tree(acc1);
+            if (two) s2 = tree(acc2);
+        }
+        part[0][wave][lane] = s1;
+        part[1][wave][lane] = s2;
+        __syncthreads();
+        const float sum = (part[0][0][lane] + part[0][1][lane]) + (part[0][2][lane] + part[0][3][lane]);
+        const float sum2 = (part[1][0][lane] + part[1][1][lane]) + (part[1][2][lane] + part[1][3][lane]);
         if (finisher) {
             float v = a.accumulate ? before + sum : sum;
             if (two) v = v + sum2;
@@ -820,25 +831,31 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
             if constexpr (UPDATE) e = rprop_state(o, t, idx);
             if (a.accumulate) before = a.grad[t][idx];
         }
-        // the sum of entry j, valid on lane 0
-        auto sum_minor = [&](const float* base, int S) {
-            const float* P = base + size_t(j) * S;
-            float acc[U];
+        // the sums of entry j, valid on lane 0
+        const float* P1 = a.partial[t] + size_t(j) * S;
+        const float* P2 = two ? a.partial2[t] + size_t(j) * S2 : P1;
+        float acc1[U], acc2[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) acc[u] = 0.0f;
-            for (int q = lane; q < S + 63; q += 64 * U) {  // lane l: splits l, l + 64, ...
-                float v[U];
+        for (int u = 0; u < U; ++u) acc1[u] = acc2[u] = 0.0f;
+        for (int q = lane; q < Smax + 63; q += 64 * U) {  // lane l: splits l, l + 64, ...
+            float v1[U], v2[U];
 #pragma unroll
-                for (int u = 0; u < U; ++u) v[u] = P[min(q + 64 * u, S - 1)];
+            for (int u = 0; u < U; ++u) v1[u] = P1[min(q + 64 * u, S - 1)];
+            if (two)
 #pragma unroll
-                for (int u = 0; u < U; ++u) acc[u] += q + 64 * u < S ? v[u] : 0.0f;
-            }
-            float s = tree(acc);
-            for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
-            return s;
-        };
-        const float s = sum_minor(a.partial[t], S);
-        const float s2 = two ? sum_minor(a.partial2[t], a.splits2[t]) : 0.0f;
+                for (int u = 0; u < U; ++u) v2[u] = P2[min(q + 64 * u, S2 - 1)];
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc1[u] += q + 64 * u < S ? v1[u] : 0.0f;
+            if (two)
+#pragma unroll
+                for (int u = 0; u < U; ++u) acc2[u] += q + 64 * u < S2 ? v2[u] : 0.0f;
+        }
+        float s = tree(acc1), s2 = 0.0f;
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+        if (two) {
+            s2 = tree(acc2);
+            for (int off = 32; off > 0; off >>= 1) s2 += __shfl_down(s2, off, 64);
+        }
         if (lane == 0) {
             float v = a.accumulate ? before + s : s;
             if (two) v = v + s2;
@@ -2029,34 +2046,59 @@ constexpr int kGraphLdsNodes = 256, kGraphLdsLeaves = 64;
 // and the lanes write the values, adjoints, activity, multipliers and summary
 // out.  The same operations in the same order as run_graph, so the same bits.
 // Larger graphs run on global memory.  Every lane of the block calls it.
-__device__ void run_graph_block(const GraphLaunch& g, bool fresh) {
+// The LDS copy of a graph (graph_stage, graph_run): nodes {op, a, b, active},
+// parameters, values, adjoints, leaf multipliers.
+__shared__ int4 graph_node[kGraphLdsNodes];
+__shared__ double graph_parameter[kGraphLdsNodes], graph_value[kGraphLdsNodes], graph_adjoint[kGraphLdsNodes];
+__shared__ double graph_multiplier[kGraphLdsLeaves];
+__shared__ int graph_bad_node;
+
+__device__ __forceinline__ bool graph_in_lds(const GraphLaunch& g) {
+    return g.count <= kGraphLdsNodes && g.leaves <= kGraphLdsLeaves;
+}
+
+// run_graph with every lane of the block helping, in two steps.  graph_stage:
+// the lanes copy the nodes and the leaf values into LDS (no barrier; a launch
+// that finishes costs first stages the graph before them, so the loads go out
+// together).  graph_run: the totals the launch has just finished (fresh,
+// finish_costs) replace their leaves' values, lane 0 runs the same two sweeps
+// as run_graph on the copy (each step of the serial chain then waits on LDS,
+// not on a round trip to global memory), and the lanes write the values,
+// adjoints, activity, multipliers and summary out.  The same operations in the
+// same order as run_graph, so the same bits.  Larger graphs run on global
+// memory.  Every lane of the block calls both.
+__device__ void graph_stage(const GraphLaunch& g) {
+    if (!graph_in_lds(g)) return;
+    for (int i = threadIdx.x; i < g.count; i += blockDim.x) {
+        const cpde_scalar_node n = g.nodes[i];
+        graph_node[i] = make_int4(n.op, n.a, n.b, n.op == kLeaf);
+        graph_parameter[i] = n.parameter;
+        graph_value[i] = n.op == kLeaf ? g.integrals[n.a].value : 0.0;
+        graph_adjoint[i] = 0;
+    }
+    for (int i = threadIdx.x; i < g.leaves; i += blockDim.x) graph_multiplier[i] = 0;
+}
+
+__device__ void graph_run(const GraphLaunch& g, bool fresh) {
     const int count = g.count, leaves = g.leaves, root = g.root;
-    if (count > kGraphLdsNodes || leaves > kGraphLdsLeaves) {
+    if (!graph_in_lds(g)) {
         if (threadIdx.x == 0) run_graph(g);
         return;
     }
-    __shared__ int4 node[kGraphLdsNodes];  // op, a, b, active
-    __shared__ double parameter[kGraphLdsNodes], value[kGraphLdsNodes], adjoint[kGraphLdsNodes];
-    __shared__ double multiplier[kGraphLdsLeaves];
-    __shared__ int bad_node;
-    for (int i = threadIdx.x; i < count; i += blockDim.x) {
-        const cpde_scalar_node n = g.nodes[i];
-        node[i] = make_int4(n.op, n.a, n.b, n.op == kLeaf);
-        parameter[i] = n.parameter;
-        double leaf = 0.0;
-        if (n.op == kLeaf) {
-            // a total the launch has just finished (finish_costs) is taken from LDS
-            const CostStats* slot = g.integrals + n.a;
-            const int finished = fresh ? reduce_finished_count : 0;
-            int c = 0;
-            while (c < finished && reduce_finished_slot[c] != slot) ++c;
-            leaf = c < finished ? reduce_finished[c].value : slot->value;
-        }
-        value[i] = leaf;
-        adjoint[i] = 0;
+    int4* const node = graph_node;
+    double *const parameter = graph_parameter, *const value = graph_value, *const adjoint = graph_adjoint;
+    double* const multiplier = graph_multiplier;
+    __syncthreads();  // the staged copy is complete
+    if (fresh) {
+        const int finished = reduce_finished_count;
+        for (int i = threadIdx.x; i < count; i += blockDim.x)
+            if (node[i].x == kLeaf) {
+                const CostStats* slot = g.integrals + node[i].y;
+                for (int c = 0; c < finished; ++c)
+                    if (reduce_finished_slot[c] == slot) value[i] = reduce_finished[c].value;
+            }
+        __syncthreads();
     }
-    for (int i = threadIdx.x; i < leaves; i += blockDim.x) multiplier[i] = 0;
-    __syncthreads();
     if (threadIdx.x == 0) {
         int bad = -1;
         for (int i = 0; i < count; ++i) {
@@ -2085,7 +2127,7 @@ __device__ void run_graph_block(const GraphLaunch& g, bool fresh) {
             for (int i = 0; i < leaves; ++i)
                 if (!isfinite(multiplier[i])) bad = root;
         }
-        bad_node = bad;
+        graph_bad_node = bad;
     }
     __syncthreads();
     for (int i = threadIdx.x; i < count; i += blockDim.x) {
@@ -2096,13 +2138,16 @@ __device__ void run_graph_block(const GraphLaunch& g, bool fresh) {
     for (int i = threadIdx.x; i < leaves; i += blockDim.x) g.multipliers[i] = multiplier[i];
     if (threadIdx.x == 0) {
         g.summary->value = value[root];
-        g.summary->bad_node = bad_node;
+        g.summary->bad_node = graph_bad_node;
     }
 }
 
 constexpr int kGraphThreads = 64;
 
-__global__ __launch_bounds__(kGraphThreads) void graph_kernel(GraphLaunch g) { run_graph_block(g); }
+__global__ __launch_bounds__(kGraphThreads) void graph_kernel(GraphLaunch g) {
+    graph_stage(g);
+    graph_run(g, false);
+}
 
 GraphLaunch graph_launch(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,
                          double* adjoints, double* multipliers, int* active, cpde_graph_summary* summary,
