@@ -317,6 +317,15 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
             t.col_tile = 16;
         }
     }
+    // A value-only plan over at most one point per CU (a boundary leaf, which
+    // the server's graph epochs pair with the interior's launch): eight points
+    // per workgroup instead of one per CU -- eight columns still take one
+    // 16-column tile, so a workgroup costs what one point's did, and the pair
+    // launch carries an eighth of the waves.  Four waves, so that it still pairs.
+    // Poisson graph epoch 0.0595 -> 0.0581 ms (one, two, four, eight and
+    // sixteen points: 0.0595, 0.0593, 0.0587, 0.0581, 0.0587).
+    const bool value_leaf = rows == 1 && width > 0 && width <= compute_units;
+    if (value_leaf) npb = 8;
     t.points_per_block = std::max(1, env_int("CPDE_FUSED_POINTS", t.points_per_block));
     t.net_points_per_block = std::max(1, env_int("CPDE_NET_POINTS", npb));
     // A chunk of several-point workgroups that leaves CUs without a second
@@ -326,7 +335,8 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
     // workgroups), ms per epoch at orders 0..3: 0.0416 -> 0.0409, 0.0454 ->
     // 0.0445, 0.0500 -> 0.0487, 0.0576 -> 0.0563.  With more workgroups than
     // CUs it was slower (order 4, 365 workgroups: 0.0700 -> 0.0742).
-    if (width > 0 && rows <= 16 && npb > 1 && (width + npb - 1) / npb <= compute_units) t.net_threads = 512;
+    if (width > 0 && rows <= 16 && npb > 1 && !value_leaf && (width + npb - 1) / npb <= compute_units)
+        t.net_threads = 512;
     t.net_threads = env_int("CPDE_NET_THREADS", t.net_threads) == 512 ? 512 : 256;
     // The waves of a workgroup share a layer's products by output tile.  Where
     // 32x32 tiles of the narrowest hidden layer are fewer than the waves (a

@@ -190,7 +190,7 @@ def test_weight_gradient_tile_forms(device, monkeypatch, order, neurons, points)
     (6, [2, 64, 48, 32, 1], 61, '1'),     # one-pass epoch, scaled rows on three hidden layers
     (2, [2, 64, 64, 64, 1], 300, '1'),    # several points per workgroup
     (3, [2, 80, 96, 1], 97, '0'),         # separate forward and backward launches
-    (0, [2, 64, 64, 64, 1], 256, '1'),    # the Poisson boundary leaf's shape: one row, one point per workgroup
+    (0, [2, 64, 64, 64, 1], 256, '1'),    # the Poisson boundary leaf's shape: one row, eight points per workgroup
 ])
 def test_weight_gradient_inside_the_backward(device, monkeypatch, order, neurons, points, one_pass):
     """Hidden transitions' weight-gradient partials written by the network
