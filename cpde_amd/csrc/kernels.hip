@@ -675,12 +675,6 @@ __device__ __forceinline__ void copy_transposed(const OptimizerArgs& a, int t, i
 }
 
 
-// Resile_k (cuda/derivative_kernels_v4.cu:752-778) on entry j of transition t
-// with gradient g: sign tests on float products, the gradient kept (or zeroed
-// on a rollback or a rejected step) in the active buffer.  The optimizers
-// round every product and sum separately, as the reference's CPU build does:
-// no multiply-add contraction (hipcc contracts by default, and
-// __fmul_rn/__fadd_rn do not prevent it).
 // The entry's optimizer state, loaded apart from the update so that a caller
 // can send the loads out before its gradient is complete.
 struct RpropState {
@@ -689,6 +683,13 @@ struct RpropState {
 __device__ __forceinline__ RpropState rprop_state(const OptimizerArgs& a, int t, int j) {
     return RpropState{a.W[t][j], a.S[t][j], a.Gi[t][j]};
 }
+
+// Resile_k (cuda/derivative_kernels_v4.cu:752-778) on entry j of transition t
+// with gradient g and state e: sign tests on float products, the gradient kept
+// (or zeroed on a rollback or a rejected step) in the active buffer.  The
+// optimizers round every product and sum separately, as the reference's CPU
+// build does: no multiply-add contraction (hipcc contracts by default, and
+// __fmul_rn/__fadd_rn do not prevent it).
 __device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int j, float g, const RpropState& e) {
 #pragma clang fp contract(off)
     const float gi = e.gi;
@@ -714,18 +715,15 @@ __device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int 
     a.S[t][j] = s;
     copy_transposed(a, t, j, kept);
 }
-__device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int j, float g) {
-    rprop_update(a, t, j, g, rprop_state(a, t, j));
-}
 
 // grad_t[m + M*n] (+)= sum over splits of the partials of entry (m, n), n = N
 // being the bias.  Split-major partials ([split][entry]): block = 64 consecutive
-// entries x 4 waves, wave w sums splits w, w+4, ... (eight running sums,
-// combined in a fixed order), then the four wave sums in wave order.
+// entries x 4 waves, wave w sums splits w + 4u (+ 64i) into running sum u
+// (sixteen, combined in a fixed tree), then the four wave sums in wave order.
 // Split-minor partials ([entry][split]): one wave per entry, lane l sums splits
-// l + 64u (+ 256i) into running sum u (four, combined in a fixed order), then a
-// fixed shuffle tree.  Either way the summation order is fixed whatever the
-// scheduling.
+// l + 64u (+ 1024i) into running sum u (sixteen, combined in a fixed tree),
+// then a fixed shuffle tree.  Either way the summation order is fixed whatever
+// the scheduling.
 __device__ void finish_costs(const ReduceArgs& a);
 __device__ void graph_stage(const GraphLaunch& g);
 __device__ void graph_run(const GraphLaunch& g, bool fresh);
