@@ -367,6 +367,12 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
     t.backward_blocks = std::max(1, env_int("CPDE_NET_BWD_OCC", t.backward_blocks));
     t.col_tile = env_int("CPDE_NET_COLTILE", t.col_tile);
     t.alias = env_int("CPDE_NET_ALIAS", t.alias);
+    // Paired neuron blocks in the 16-column products (weight operands as
+    // float2, one LDS operand read per two products), on wherever a layer's
+    // width is a multiple of 32 per wave.  Measured, ms per epoch against the
+    // single blocks: 2->128^4->1 order 6 at 729 points 0.0952 / 0.0963, order 5
+    // 0.0879 / 0.0876, 3->128^5->1 order 4 at 32768 points 5.20 / 5.37.
+    t.b_pairs = env_int("CPDE_NET_BPAIR", t.b_pairs);
     t.scaled = env_int("CPDE_SCALED", t.scaled) ? 1 : 0;
     // Hidden weight-gradient partials from the network backward itself, on
     // request (CPDE_INKERNEL_WGRAD=1; hidden widths that are multiples of 16).

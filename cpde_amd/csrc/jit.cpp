@@ -659,6 +659,7 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
     o << "#define CPDE_MAX_SPLIT_ADJOINT " << tuning.max_split_adjoint << "\n";
     if (tuning.scaled) o << "#define CPDE_SCALED 1\n";
     if (tuning.inkernel_wgrad) o << "#define CPDE_INKERNEL_WGRAD 1\n";
+    if (tuning.b_pairs) o << "#define CPDE_B_PAIRS 1\n";
     // row splits of the compositions used by the network-fused kernels (scaled
     // forward compositions split over mirror lanes instead)
     std::vector<int> splits;

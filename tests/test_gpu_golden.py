@@ -58,7 +58,7 @@ def test_epoch_against_reference_server(device, path, name):
     run.close()
 
 
-@pytest.mark.parametrize('col_tile', [16, 32, 'paired'])
+@pytest.mark.parametrize('col_tile', [16, 'single16', 32, 'paired'])
 @pytest.mark.parametrize('name', ['fourier_order6', 'fourier3d_reduced', 'large_reduced'])
 def test_network_products_column_tiles(device, monkeypatch, name, col_tile):
     """The network-fused products on 16-column (v_mfma_f32_16x16x4f32) and
@@ -66,9 +66,15 @@ def test_network_products_column_tiles(device, monkeypatch, name, col_tile):
     other is the default (28 rows: 32 columns either way; 35 rows: 48 or 64),
     and the long-grid form ('paired': two points per workgroup on 16-column
     tiles, the product tile written over its operand tile) forced on these
-    short grids, against the reference server's epoch at the order-6 bars."""
+    short grids, against the reference server's epoch at the order-6 bars.
+    16-column products take 32-neuron blocks per wave (float2 weight pairs)
+    where a width allows; 'single16' forces one 16-neuron block at a time."""
     monkeypatch.setenv('CPDE_FUSED', '2')
-    if col_tile == 'paired':
+    if col_tile == 'single16':
+        monkeypatch.setenv('CPDE_NET_COLTILE', '16')
+        monkeypatch.setenv('CPDE_NET_BPAIR', '0')
+        monkeypatch.setenv('CPDE_NET_ALIAS', '0')
+    elif col_tile == 'paired':
         for k, v in (('CPDE_NET_COLTILE', '16'), ('CPDE_NET_POINTS', '2'), ('CPDE_NET_ALIAS', '1')):
             monkeypatch.setenv(k, v)
     else:
