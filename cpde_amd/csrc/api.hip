@@ -1998,6 +1998,14 @@ int cpde_cost_expression(cpde_plan* plan, cpde_program* program, const double* f
     });
 }
 
+// Whether a program's source defines the per-sample functions that the one-pass
+// expression epoch compiles into the network module (the input gather and the
+// point function).
+static bool defines_point_function(const cpde_program& program) {
+    return program.source.find("cpde_expression_point") != std::string::npos &&
+           program.source.find("cpde_expression_inputs") != std::string::npos;
+}
+
 int cpde_epoch_expression(cpde_plan* plan, cpde_program* program, const double* fields,
                           const double* quadrature_weights, int samples, int offset, int valid, const double* multiplier,
                           void* scratch, int cost_index, int collect, int accumulate) {
@@ -2009,7 +2017,7 @@ int cpde_epoch_expression(cpde_plan* plan, cpde_program* program, const double* 
         require(plan->backward, "plan has no adjoint storage");
         require(valid >= 0 && valid <= plan->width && offset >= 0, "invalid chunk range");
         const bool one_pass =
-            one_pass_fits(*plan) && program->source.find("cpde_expression_point") != std::string::npos;
+            one_pass_fits(*plan) && defines_point_function(*program);
         if (!one_pass) {
             if (int code = cpde_forward(plan)) throw_code(code);
             if (int code = cpde_cost_expression(plan, program, fields, quadrature_weights, samples, offset, valid,
@@ -2029,7 +2037,7 @@ int cpde_epoch_expression_fused(cpde_plan* plan, cpde_program* program, int* fus
     return guarded([&] {
         require(plan && program && fused, "null argument");
         *fused = plan->backward && one_pass_fits(*plan) &&
-                 program->source.find("cpde_expression_point") != std::string::npos;
+                 defines_point_function(*program);
     });
 }
 

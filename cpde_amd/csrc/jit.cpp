@@ -787,20 +787,28 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     return o.str();
 }
 
+// The expression cost's stage of a one-pass epoch, and the fetch of its
+// inputs when the epoch starts.
+static std::string expression_cost(int L, int NO) {
+    return "    net_expression<" + std::to_string(NO) + ">(a, e, " + std::to_string(L - 1) +
+           ", S, p0, npts, O, O + kNNC * " + std::to_string(NO) + ", ahead);\n";
+}
+static std::string expression_ahead_line() {
+    return "    const ExpressionAhead ahead = expression_ahead(e, p0, npts);\n";
+}
+
 // The one-pass epoch of an expression cost: the expression program (which
-// defines cpde_expression_point) compiled together with the network kernels of
-// a schema and architecture.
+// defines cpde_expression_inputs and cpde_expression_point) compiled together
+// with the network kernels of a schema and architecture.
 std::string expression_epoch_source(const Tables& t, const std::vector<int>& neurons, const FusedTuning& tuning,
                                     const std::string& program) {
     std::ostringstream o;
     const int L = int(neurons.size()), NO = neurons[L - 1];
     o << "// generated: one-pass epoch of an expression cost\n" << program << "\n#define CPDE_EXPRESSION_EPOCH 1\n";
     emit_prologue(o, t, neurons, tuning);
-    const std::string cost = "    net_expression<" + std::to_string(NO) + ">(a, e, " + std::to_string(L - 1) +
-                             ", S, p0, npts, O, O + kNNC * " + std::to_string(NO) + ");\n";
     o << "extern \"C\" __global__ __launch_bounds__(" << tuning.net_threads << ", " << tuning.backward_blocks
-      << ") void network_epoch_expression_k(NetArgs a, ExpressionArgs e, int points) {\n" << epoch_body(neurons, "", cost)
-      << "}\n";
+      << ") void network_epoch_expression_k(NetArgs a, ExpressionArgs e, int points) {\n"
+      << epoch_body(neurons, expression_ahead_line(), expression_cost(L, NO)) << "}\n";
     return o.str();
 }
 
@@ -818,8 +826,7 @@ std::string expression_pair_source(const Tables& t0, const FusedTuning& u0, cons
     std::ostringstream o;
     const int L = int(neurons.size()), NO = neurons[L - 1];
     o << "// generated: two one-pass epochs of expression costs in one launch\n";
-    const std::string cost = "    net_expression<" + std::to_string(NO) + ">(a, e, " + std::to_string(L - 1) +
-                             ", S, p0, npts, O, O + kNNC * " + std::to_string(NO) + ");\n";
+    const std::string cost = expression_cost(L, NO);
     for (int leaf = 0; leaf < 2; ++leaf) {
         std::ostringstream part;
         // the program's stand-alone cost kernel has C linkage, which the
@@ -828,7 +835,7 @@ std::string expression_pair_source(const Tables& t0, const FusedTuning& u0, cons
              << (leaf ? program1 : program0) << "\n#undef expression\n#define CPDE_EXPRESSION_EPOCH 1\n";
         emit_prologue(part, leaf ? t1 : t0, neurons, leaf ? u1 : u0);
         part << "__device__ __forceinline__ void epoch(const NetArgs& a, const ExpressionArgs& e, int points) {\n"
-             << epoch_body(neurons, "", cost) << "}\n";
+             << epoch_body(neurons, expression_ahead_line(), cost) << "}\n";
         const std::string text = part.str();
         o << "namespace cpde_leaf" << leaf << " {\n" << text << "}  // namespace cpde_leaf" << leaf << "\n";
         std::istringstream lines(text);

@@ -288,20 +288,42 @@ std::string number(double x) {
 }
 
 // The program of an expression cost (cuda/cost_kernels.cuh expression costs,
-// cpde/_expressions.py IR): a per-sample device function
-// cpde_expression_point(yp, gp, ...) -- value, non-finite flag and, with
-// `gradient`, d(loss)/d(output component) scaled by the multiplier into gp --
-// and the kernel `expression` that applies it to every sample of a chunk.  The
-// library's one-pass epoch compiles the same function into the network module
-// and applies it to the output values a workgroup holds in LDS.
+// cpde/_expressions.py IR): the gather of a sample's inputs from global memory
+// (cpde_expression_inputs: its quadrature weight and the field values the
+// program reads), a per-sample device function cpde_expression_point(yp, gp,
+// inputs, ...) -- value, non-finite flag and, with `gradient`,
+// d(loss)/d(output component) scaled by the multiplier into gp -- and the
+// kernel `expression` that applies both to every sample of a chunk.  The
+// library's one-pass epoch compiles the same functions into the network module,
+// gathers a workgroup's inputs when it starts and applies the point function to
+// the output values the workgroup holds in LDS.
 std::string expression_source(const std::vector<ExpressionNode>& nodes) {
     std::ostringstream s;
-    s << "__device__ __forceinline__ void cpde_expression_point(const float* __restrict__ yp, float* __restrict__ gp,\n"
-         "    const double* __restrict__ fields, const double* __restrict__ weights, int comps, int samples, int offset,\n"
-         "    int p, int valid, double scale, int collect, int gradient, double* loss_out, int* bad_out) {\n"
+    std::vector<int> field_ids;  // the fields the program reads, in order of first use
+    std::map<int, int> field_slot;
+    for (const ExpressionNode& n : nodes)
+        if (n.op == kField && !field_slot.count(n.a)) {
+            field_slot[n.a] = int(field_ids.size());
+            field_ids.push_back(n.a);
+        }
+    s << "struct CpdeExpressionInputs {\n  double weight;\n  double field[" << std::max<size_t>(1, field_ids.size())
+      << "];\n};\n"
+         "// Sample p's inputs; one past `valid` reads the last valid sample's (not used).\n"
+         "__device__ __forceinline__ CpdeExpressionInputs cpde_expression_inputs(const double* __restrict__ fields,\n"
+         "    const double* __restrict__ weights, int samples, int offset, int p, int valid) {\n"
+         "  CpdeExpressionInputs in{};\n"
+         "  if (valid > 0) {\n"
+         "    const int q = p < valid ? p : valid - 1;\n"
+         "    in.weight = weights[offset + q];\n";
+    for (size_t k = 0; k < field_ids.size(); ++k)
+        s << "    in.field[" << k << "] = fields[" << field_ids[k] << " * (size_t)samples + offset + q];\n";
+    s << "  }\n  return in;\n}\n"
+         "__device__ __forceinline__ void cpde_expression_point(const float* __restrict__ yp, float* __restrict__ gp,\n"
+         "    const CpdeExpressionInputs& in, int comps, int p, int valid, double scale, int collect, int gradient,\n"
+         "    double* loss_out, int* bad_out) {\n"
          "  *loss_out = 0; *bad_out = -2;\n"
          "  if (gradient) for (int c = 0; c < comps; ++c) gp[c] = 0.0f;\n"
-         "  if (p >= valid || weights[offset + p] == 0) return;\n"
+         "  if (p >= valid || in.weight == 0) return;\n"
          "  if (gradient && scale == 0 && !collect) return;\n"
          "  int bad = -2;\n"
          "  double lossv = 0;\n"
@@ -314,7 +336,7 @@ std::string expression_source(const std::vector<ExpressionNode>& nodes) {
         switch (n.op) {
         case kConstant: e = number(n.parameter); break;
         case kComponent: e = "(double)yp[" + std::to_string(n.a) + "]"; break;
-        case kField: e = "fields[" + std::to_string(n.a) + " * (size_t)samples + offset + p]"; break;
+        case kField: e = "in.field[" + std::to_string(field_slot[n.a]) + "]"; break;
         case kAdd: e = a + " + " + b; break;
         case kSub: e = a + " - " + b; break;
         case kMul: e = a + " * " + b; break;
@@ -340,7 +362,7 @@ std::string expression_source(const std::vector<ExpressionNode>& nodes) {
         active.push_back(act);
     }
     const size_t last = nodes.size() - 1;
-    s << "    if (collect) lossv = weights[offset + p] * v" << last << ";\n"
+    s << "    if (collect) lossv = in.weight * v" << last << ";\n"
       << "    if (!isfinite(lossv)) bad = -1;\n"
       << "    *loss_out = lossv; *bad_out = bad;\n"
       << "    if (!gradient || scale == 0 || bad != -2) return;\n";
@@ -381,7 +403,7 @@ std::string expression_source(const std::vector<ExpressionNode>& nodes) {
     for (const auto& kv : comps) {
         s << "    { double t = 0";
         for (size_t i : kv.second) s << " + d" << i;
-        s << "; const float out = (float)(t * weights[offset + p] * scale); gp[" << kv.first
+        s << "; const float out = (float)(t * in.weight * scale); gp[" << kv.first
           << "] = out; if (!isfinite(out)) *bad_out = " << kv.first << "; }\n";
     }
     s << "  }\n}\n"
@@ -392,8 +414,9 @@ std::string expression_source(const std::vector<ExpressionNode>& nodes) {
          "  const int comps = rows * outputs;\n"
          "  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < width; p += blockDim.x * gridDim.x) {\n"
          "    const double scale = multiplier ? *multiplier : 1.0;\n"
-         "    cpde_expression_point(y + (size_t)p * comps, gradient ? g + (size_t)p * comps : nullptr, fields, weights,\n"
-         "                          comps, samples, offset, p, valid, scale, collect, gradient, &loss[p], &bad[p]);\n"
+         "    const CpdeExpressionInputs in = cpde_expression_inputs(fields, weights, samples, offset, p, valid);\n"
+         "    cpde_expression_point(y + (size_t)p * comps, gradient ? g + (size_t)p * comps : nullptr, in, comps, p,\n"
+         "                          valid, scale, collect, gradient, &loss[p], &bad[p]);\n"
          "  }\n}\n";
     return s.str();
 }
