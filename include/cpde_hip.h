@@ -315,8 +315,11 @@ int cpde_reset_optimizer(cpde_net* net);
 /* ---- scalar-expression costs: generated source compiled with hipRTC for gfx950
  *      (cuda/expression_program.hpp:96-131 used NVRTC) and the scalar cost graph.
  * The source defines the kernel `expression` (arguments as cpde_cost_expression
- * passes them) and may define the per-sample function cpde_expression_point
- * that cpde_epoch_expression compiles into the network kernels. */
+ * passes them) and may define the per-sample functions cpde_expression_inputs
+ * (a sample's quadrature weight and field values, gathered from global memory)
+ * and cpde_expression_point (value, flag and adjoint from those inputs and the
+ * sample's outputs), which cpde_epoch_expression compiles into the network
+ * kernels. */
 int cpde_program_compile(cpde_device* dev, const char* source, cpde_program** out, char* log, size_t log_capacity);
 int cpde_program_destroy(cpde_program* program);
 /* Per-sample expression over the plan's output stack, then its deterministic
@@ -330,7 +333,7 @@ int cpde_cost_expression(cpde_plan* plan, cpde_program* program, const double* f
  * (cuda/cpde_server.cu:223-257): cpde_forward, cpde_cost_expression(gradient=1)
  * and cpde_backward(accumulate) with the same arguments.  On the network-fused
  * kernels, when the chunk's workgroups fit on the device together and the
- * program defines cpde_expression_point, this is one launch (a sample's value
+ * program defines both per-sample functions, this is one launch (a sample's value
  * and adjoint depend on that sample alone; the program is compiled into the
  * network module on first use), the cost's finish and the weight-gradient
  * contraction.  The multiplier must be final when the call is made.  The input
