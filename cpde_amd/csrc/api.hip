@@ -374,6 +374,9 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
     // 0.0879 / 0.0876, 3->128^5->1 order 4 at 32768 points 5.20 / 5.37.
     t.b_pairs = env_int("CPDE_NET_BPAIR", t.b_pairs);
     t.scaled = env_int("CPDE_SCALED", t.scaled) ? 1 : 0;
+    // Diagnostics: clock stamps of the one-pass epoch's phases, written over
+    // the output stack (cpde_amd/stamps.py reads them back).
+    t.stamps = env_int("CPDE_PHASE_STAMPS", 0) ? 1 : 0;
     // Hidden weight-gradient partials from the network backward itself, on
     // request (CPDE_INKERNEL_WGRAD=1; hidden widths that are multiples of 16).
     // Measured on the Poisson graph epoch, whose 256-point one-row boundary

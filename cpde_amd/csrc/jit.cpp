@@ -660,6 +660,7 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
     if (tuning.scaled) o << "#define CPDE_SCALED 1\n";
     if (tuning.inkernel_wgrad) o << "#define CPDE_INKERNEL_WGRAD 1\n";
     if (tuning.b_pairs) o << "#define CPDE_B_PAIRS 1\n";
+    if (tuning.stamps) o << "#define CPDE_STAMPS 1\n";
     // row splits of the compositions used by the network-fused kernels (scaled
     // forward compositions split over mirror lanes instead)
     std::vector<int> splits;
@@ -682,7 +683,8 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
 // output values and the output adjoint of its columns kept in LDS (O), the
 // cost stage `cost` between them (it fills O's second half), then the
 // backward.  The row-major weight copies are written before the launch.
-static std::string epoch_body(const std::vector<int>& neurons, const std::string& prefetch, const std::string& cost) {
+static std::string epoch_body(const std::vector<int>& neurons, const std::string& prefetch, const std::string& cost,
+                              bool stamps) {
     const int L = int(neurons.size()), NO = neurons[L - 1];
     std::ostringstream ep;
     // S: the cost stage's scratch (matching terms, or a double and an int per
@@ -722,7 +724,27 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
         ep << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << (t == 1 ? ", false" : "") << ">(a, "
            << t << ", X, T, p0, npts);\n";
     ep << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
-    return ep.str();
+    // Diagnostics (FusedTuning::stamps): a clock stamp after every phase --
+    // each call above and each barrier between them -- written over the
+    // block's output stack when the epoch ends.
+    if (!stamps) return ep.str();
+    std::istringstream lines(ep.str());
+    std::ostringstream st;
+    std::string line;
+    int k = 0;
+    bool begun = false;
+    while (std::getline(lines, line)) {
+        st << line << "\n";
+        if (!begun && line.find("const int p0") != std::string::npos) {
+            st << "    STAMP_BEGIN\n";
+            begun = true;
+        } else if (begun && (line.rfind("    net_", 0) == 0 || line.rfind("    __syncthreads();", 0) == 0)) {
+            st << "    STAMP(" << k++ << ")\n";
+        }
+    }
+    st << "    STAMP_END(" << k << ", a.Z[" << L - 1 << "] + size_t(p0) * R * " << NO << ", R * " << NO
+       << " * npts)\n";
+    return st.str();
 }
 
 // Full source of the fused module for a schema and architecture.
@@ -767,8 +789,8 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
         const std::string cost = "    net_match<" + std::to_string(NO) + ">(a, m, " + std::to_string(L - 1) +
                                  ", S, p0, npts, O, O + kNNC * " + std::to_string(NO) + ", pre);\n";
         o << "extern \"C\" __global__ __launch_bounds__(" << nt << ", " << tuning.backward_blocks
-          << ") void network_epoch_k(NetArgs a, MatchArgs m, int points) {\n" << epoch_body(neurons, prefetch, cost)
-          << "}\n";
+          << ") void network_epoch_k(NetArgs a, MatchArgs m, int points) {\n"
+          << epoch_body(neurons, prefetch, cost, tuning.stamps != 0) << "}\n";
     }
     o << "\nextern \"C\" __global__ __launch_bounds__(256) void input_layer_k(const float* W, const float* X, float* Z,"
          " float* Y, int points) { input_layer<"
@@ -808,7 +830,7 @@ std::string expression_epoch_source(const Tables& t, const std::vector<int>& neu
     emit_prologue(o, t, neurons, tuning);
     o << "extern \"C\" __global__ __launch_bounds__(" << tuning.net_threads << ", " << tuning.backward_blocks
       << ") void network_epoch_expression_k(NetArgs a, ExpressionArgs e, int points) {\n"
-      << epoch_body(neurons, expression_ahead_line(), expression_cost(L, NO)) << "}\n";
+      << epoch_body(neurons, expression_ahead_line(), expression_cost(L, NO), tuning.stamps != 0) << "}\n";
     return o.str();
 }
 
@@ -835,7 +857,7 @@ std::string expression_pair_source(const Tables& t0, const FusedTuning& u0, cons
              << (leaf ? program1 : program0) << "\n#undef expression\n#define CPDE_EXPRESSION_EPOCH 1\n";
         emit_prologue(part, leaf ? t1 : t0, neurons, leaf ? u1 : u0);
         part << "__device__ __forceinline__ void epoch(const NetArgs& a, const ExpressionArgs& e, int points) {\n"
-             << epoch_body(neurons, expression_ahead_line(), cost) << "}\n";
+             << epoch_body(neurons, expression_ahead_line(), cost, (leaf ? u1 : u0).stamps != 0) << "}\n";
         const std::string text = part.str();
         o << "namespace cpde_leaf" << leaf << " {\n" << text << "}  // namespace cpde_leaf" << leaf << "\n";
         std::istringstream lines(text);
