@@ -575,15 +575,19 @@ struct OptimizerArgs {
     // the rule would read the gradient totals (the transitions' entries make at
     // most kTestChunks chunks), and its first workgroup writes stats[t] = {0,
     // 0, whether transition t has a non-finite entry, none}, into the totals
-    // and straight into the host mirror, before it releases the publish copy
+    // and straight into the host mirror
     int test;
     GradStats* stats;
 };
 
-// The scalar block to the host, by the first workgroup of an update launch,
-// released to the system before the launch ends.
-// A launch with its own finiteness test copies all but the gradient totals,
-// unreleased: test_gradients writes those and releases the copy.
+// The scalar block to the host, by the first workgroup of an update launch.
+// A launch with its own finiteness test copies all but the gradient totals:
+// test_gradients writes those.  No fence: the host block is coherent pinned
+// memory, which the stores reach over the bus without passing a GPU cache,
+// and the host reads it only after the launch's completion event (hipEvent-
+// Synchronize), which orders the launch's writes before it.  (A system-scope
+// fence here writes back the L2 first: 10.1 -> 9.2 us for the Poisson graph
+// epoch's update launch without it.)
 __device__ __forceinline__ void publish_scalars(const OptimizerArgs& a) {
     if (!a.publish_dst || blockIdx.x != 0) return;
     int skip_begin = 0, skip_end = 0;
@@ -593,7 +597,6 @@ __device__ __forceinline__ void publish_scalars(const OptimizerArgs& a) {
     }
     for (int i = threadIdx.x; i < a.publish_words; i += blockDim.x)
         if (i < skip_begin || i >= skip_end) a.publish_dst[i] = a.publish_src[i];
-    if (!a.test) __threadfence_system();
 }
 
 // The launch's own finiteness test (OptimizerArgs::test): lane c lays chunk c
@@ -650,7 +653,6 @@ __device__ bool test_gradients(const OptimizerArgs& a) {
             const int offset = int(reinterpret_cast<const unsigned*>(a.stats) - a.publish_src);
             reinterpret_cast<GradStats*>(a.publish_dst + offset)[threadIdx.x] = r;
         }
-        __threadfence_system();
     } else if (blockIdx.x == 0 && threadIdx.x < a.transitions) {
         a.stats[threadIdx.x] = GradStats{0.0, 0.0, (m >> threadIdx.x) & 1u, INT_MAX, 0};
     }
