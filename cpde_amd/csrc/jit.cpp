@@ -704,7 +704,8 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
        << "    float* const S = T;\n"
        << "#endif\n"
        << "    const int p0 = net_block(a) * kNPB, npts = kNPB == 1 ? 1 : min(kNPB, points - p0);\n"
-       << prefetch << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
+       << prefetch << "    const float xin = input_ahead<" << neurons[0] << ">(a, p0, npts);  // for the input gradient\n"
+       << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
        << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
        << "    __syncthreads();\n";
     // the last hidden layer's y (read from X by the output layer's partial) and
@@ -723,7 +724,7 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
     for (int t = L - 3; t >= 1; --t)
         ep << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << (t == 1 ? ", false" : "") << ">(a, "
            << t << ", X, T, p0, npts);\n";
-    ep << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n";
+    ep << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ", true>(a, X, p0, npts, xin);\n";
     // Diagnostics (FusedTuning::stamps): a clock stamp after every phase --
     // each call above and each barrier between them -- written over the
     // block's output stack when the epoch ends.

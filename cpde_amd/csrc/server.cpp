@@ -342,9 +342,13 @@ std::string expression_source(const std::vector<ExpressionNode>& nodes) {
         case kMul: e = a + " * " + b; break;
         case kDiv: e = "(" + b + " == 0 ? __builtin_nan(\"\") : " + a + " / " + b + ")"; break;
         case kPower:
-            e = "((" + a + " < 0 && floor(" + number(n.parameter) + ") != " + number(n.parameter) + ") || (" + a +
-                " == 0 && " + number(n.parameter) + " < 0) ? __builtin_nan(\"\") : pow(" + a + ", " + number(n.parameter) +
-                "))";
+            // a^1 and a^2 as a and a*a: pow's value there, with no call
+            if (n.parameter == 1.0) e = a;
+            else if (n.parameter == 2.0) e = a + " * " + a;
+            else
+                e = "((" + a + " < 0 && floor(" + number(n.parameter) + ") != " + number(n.parameter) + ") || (" + a +
+                    " == 0 && " + number(n.parameter) + " < 0) ? __builtin_nan(\"\") : pow(" + a + ", " +
+                    number(n.parameter) + "))";
             break;
         case kNeg: e = "-" + a; break;
         case kExp: e = "exp(" + a + ")"; break;
@@ -380,8 +384,9 @@ std::string expression_source(const std::vector<ExpressionNode>& nodes) {
         case kPower:
             da = n.parameter == 0 ? "0"
                                   : (n.parameter == 1 ? "1"
-                                                      : number(n.parameter) + " * pow(" + a + ", " +
-                                                            number(n.parameter - 1) + ")");
+                                                      : (n.parameter == 2 ? "2.0 * " + a
+                                                                          : number(n.parameter) + " * pow(" + a + ", " +
+                                                                                number(n.parameter - 1) + ")"));
             break;
         case kNeg: da = "-1"; break;
         case kExp: da = v; break;
