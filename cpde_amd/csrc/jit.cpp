@@ -715,7 +715,8 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
         ep << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << (t + 3 == L ? ", false" : "") << ">(a, " << t
            << ", X, T, p0, npts);\n";
     const std::string last = std::to_string(neurons[L - 2]);
-    ep << "    float ua[R];  // the last hidden layer's u rows, in flight during the output layer and the cost\n"
+    ep << "    UAhead<" << last << ", output_adjoint_split<" << last
+       << ">()> ua;  // the last hidden layer's u rows, in flight during the output layer and the cost\n"
        << "    u_ahead<" << last << ", output_adjoint_split<" << last << ">()>(a, " << L - 2 << ", p0, npts, ua);\n"
        << "    net_output<" << neurons[L - 2] << ", " << NO << ">(a, " << L - 2 << ", X, p0, npts, O);\n"
        << "    __syncthreads();  // the output values of the block's columns are in O\n"
@@ -767,7 +768,8 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     fwd << "    net_output<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2 << ", X, p0, npts);\n";
     {
         const std::string last = std::to_string(neurons[L - 2]);
-        bwd << "    float ua[R];\n    u_ahead<" << last << ", output_adjoint_split<" << last << ">()>(a, " << L - 2
+        bwd << "    UAhead<" << last << ", output_adjoint_split<" << last << ">()> ua;\n    u_ahead<" << last
+            << ", output_adjoint_split<" << last << ">()>(a, " << L - 2
             << ", p0, npts, ua);\n"
             << "    net_output_backward<" << neurons[L - 2] << ", " << neurons[L - 1] << ">(a, " << L - 2
             << ", X, p0, npts, ua);\n";
