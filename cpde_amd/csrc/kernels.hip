@@ -595,7 +595,7 @@ __device__ __forceinline__ void publish_scalars(const OptimizerArgs& a) {
         skip_begin = int(reinterpret_cast<const unsigned*>(a.stats) - a.publish_src);
         skip_end = skip_begin + a.transitions * int(sizeof(GradStats) / sizeof(unsigned));
     }
-    for (int i = threadIdx.x; i < a.publish_words; i += blockDim.x)
+    for (int i = threadIdx.x; i < a.publish_words; i += kOptimizerThreads)
         if (i < skip_begin || i >= skip_end) a.publish_dst[i] = a.publish_src[i];
 }
 
@@ -727,7 +727,9 @@ __device__ __forceinline__ void rprop_update(const OptimizerArgs& a, int t, int 
 // then a fixed shuffle tree.  Either way the summation order is fixed whatever
 // the scheduling.
 __device__ void finish_costs(const ReduceArgs& a);
+template <int THREADS>
 __device__ void graph_stage(const GraphLaunch& g);
+template <int THREADS>
 __device__ void graph_run(const GraphLaunch& g, bool fresh);
 
 // UPDATE: the lane that finishes an entry's gradient applies RPROP to it
@@ -742,9 +744,9 @@ __device__ __forceinline__ void reduce_grouped(const ReduceArgs& a, const Optimi
     __shared__ float part[2][4][64];
     const int cost_block = a.costs || a.with_graph ? 1 : 0;
     if (cost_block && blockIdx.x == 0) {
-        if (a.with_graph) graph_stage(a.graph);
+        if (a.with_graph) graph_stage<256>(a.graph);
         finish_costs(a);
-        if (a.with_graph) graph_run(a.graph, true);
+        if (a.with_graph) graph_run<256>(a.graph, true);
         return;
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1282,7 +1284,7 @@ __device__ CostStats block_reduce_cost(CostStats v) {
     __syncthreads();
     CostStats r = empty_cost();
     if (threadIdx.x == 0)
-        for (int w = 0; w < int(blockDim.x >> 6); ++w) r = combine(r, waves[w]);
+        for (int w = 0; w < kCostThreads / 64; ++w) r = combine(r, waves[w]);
     return r;
 }
 
@@ -1294,7 +1296,7 @@ __device__ void finish_cost_records(const CostStats* __restrict__ records, int c
                                     int overwrite) {
     constexpr int U = 4;
     CostStats v = empty_cost();
-    const int step = int(blockDim.x);
+    constexpr int step = kCostThreads;
     for (int i = threadIdx.x; i < count; i += U * step) {
         CostStats r[U];
 #pragma unroll
@@ -1321,7 +1323,8 @@ __shared__ int reduce_finished_count;
 __device__ void finish_costs(const ReduceArgs& a) {
     constexpr int U = 4;
     __shared__ CostStats waves[kReduceCosts][kCostThreads / 64];
-    const int step = int(blockDim.x), lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int step = kCostThreads;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     CostStats v[kReduceCosts], prior[kReduceCosts];
     int rounds = 0;
 #pragma unroll
@@ -1620,8 +1623,10 @@ __device__ __forceinline__ GradStats combine_grad(GradStats a, const GradStats& 
     return a;
 }
 
+constexpr int kGradThreads = 1024;
+
 __device__ GradStats block_reduce_grad(GradStats v) {
-    __shared__ GradStats waves[16];
+    __shared__ GradStats waves[kGradThreads / 64];
     for (int off = 32; off > 0; off >>= 1) {
         GradStats o;
         o.squared_norm = __shfl_down(v.squared_norm, off, 64);
@@ -1635,7 +1640,7 @@ __device__ GradStats block_reduce_grad(GradStats v) {
     __syncthreads();
     GradStats r{0.0, 0.0, 0ull, INT_MAX, 0};
     if (threadIdx.x == 0)
-        for (int w = 0; w < int(blockDim.x >> 6); ++w) r = combine_grad(r, waves[w]);
+        for (int w = 0; w < kGradThreads / 64; ++w) r = combine_grad(r, waves[w]);
     return r;
 }
 
@@ -1649,7 +1654,6 @@ struct GradGroupArgs {
     int transitions;
 };
 
-constexpr int kGradThreads = 1024;
 
 // Entries are loaded eight at a time per lane (an index past the end reads the
 // last entry again and is not counted), so that a transition of up to 8,192
@@ -2066,19 +2070,21 @@ __device__ __forceinline__ bool graph_in_lds(const GraphLaunch& g) {
 // not on a round trip to global memory), and the lanes write the values,
 // adjoints, activity, multipliers and summary out.  The same operations in the
 // same order as run_graph, so the same bits.  Larger graphs run on global
-// memory.  Every lane of the block calls both.
+// memory.  Every lane of the block (THREADS lanes) calls both.
+template <int THREADS>
 __device__ void graph_stage(const GraphLaunch& g) {
     if (!graph_in_lds(g)) return;
-    for (int i = threadIdx.x; i < g.count; i += blockDim.x) {
+    for (int i = threadIdx.x; i < g.count; i += THREADS) {
         const cpde_scalar_node n = g.nodes[i];
         graph_node[i] = make_int4(n.op, n.a, n.b, n.op == kLeaf);
         graph_parameter[i] = n.parameter;
         graph_value[i] = n.op == kLeaf ? g.integrals[n.a].value : 0.0;
         graph_adjoint[i] = 0;
     }
-    for (int i = threadIdx.x; i < g.leaves; i += blockDim.x) graph_multiplier[i] = 0;
+    for (int i = threadIdx.x; i < g.leaves; i += THREADS) graph_multiplier[i] = 0;
 }
 
+template <int THREADS>
 __device__ void graph_run(const GraphLaunch& g, bool fresh) {
     const int count = g.count, leaves = g.leaves, root = g.root;
     if (!graph_in_lds(g)) {
@@ -2091,7 +2097,7 @@ __device__ void graph_run(const GraphLaunch& g, bool fresh) {
     __syncthreads();  // the staged copy is complete
     if (fresh) {
         const int finished = reduce_finished_count;
-        for (int i = threadIdx.x; i < count; i += blockDim.x)
+        for (int i = threadIdx.x; i < count; i += THREADS)
             if (node[i].x == kLeaf) {
                 const CostStats* slot = g.integrals + node[i].y;
                 for (int c = 0; c < finished; ++c)
@@ -2130,12 +2136,12 @@ __device__ void graph_run(const GraphLaunch& g, bool fresh) {
         graph_bad_node = bad;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < count; i += blockDim.x) {
+    for (int i = threadIdx.x; i < count; i += THREADS) {
         g.values[i] = value[i];
         g.adjoints[i] = adjoint[i];
         g.active[i] = node[i].w;
     }
-    for (int i = threadIdx.x; i < leaves; i += blockDim.x) g.multipliers[i] = multiplier[i];
+    for (int i = threadIdx.x; i < leaves; i += THREADS) g.multipliers[i] = multiplier[i];
     if (threadIdx.x == 0) {
         g.summary->value = value[root];
         g.summary->bad_node = graph_bad_node;
@@ -2145,8 +2151,8 @@ __device__ void graph_run(const GraphLaunch& g, bool fresh) {
 constexpr int kGraphThreads = 64;
 
 __global__ __launch_bounds__(kGraphThreads) void graph_kernel(GraphLaunch g) {
-    graph_stage(g);
-    graph_run(g, false);
+    graph_stage<kGraphThreads>(g);
+    graph_run<kGraphThreads>(g, false);
 }
 
 GraphLaunch graph_launch(Device& d, const cpde_scalar_node* nodes, int count, int root, int leaves, double* values,
