@@ -62,6 +62,7 @@ def main(argv=None):
     ap.add_argument('--workload', default='fourier_fit_order6', choices=[f'fourier_fit_order{k}' for k in range(5, 7)])
     ap.add_argument('--warmup', type=int, default=300)
     ap.add_argument('--epochs', type=int, default=20)
+    ap.add_argument('--save', default=None, help='also write the raw stamps (.npy: epoch x slot x point)')
     args = ap.parse_args(argv)
     if os.environ.get('CPDE_PHASE_STAMPS') != '1':
         sys.exit('set CPDE_PHASE_STAMPS=1: the stamps are generated into the kernels only then')
@@ -69,10 +70,15 @@ def main(argv=None):
     names = phase_names(wl.neurons)
     n = len(names)
     u = collect(wl, args.warmup, args.epochs).astype(np.int64)
+    if args.save:
+        np.save(args.save, u)
     t = u[:, :n, :]
     w0, w1 = u[:, n, :], u[:, n + 1, :]
     if not (np.diff(t, axis=1) >= 0).all() or not (w1 > w0).all():
         sys.exit('the output stack does not hold phase stamps (was the module generated with CPDE_PHASE_STAMPS=1?)')
+    waves = 4
+    hw = u[:, n + 2:n + 2 + waves, :]  # hardware id register of each wave
+    simd = (hw >> 4) & 3
     d = np.diff(np.concatenate([np.zeros_like(t[:, :1, :]), t], axis=1), axis=1)
     blocks = t.shape[2]
     tiers = [(f'blocks {a}-{min(b, blocks) - 1}', slice(a, min(b, blocks))) for a, b in ((0, 256), (256, 512), (512, 768))
@@ -91,6 +97,10 @@ def main(argv=None):
     for name, s in tiers:
         print(f'{name}: lifetime median {np.median(life[:, s]):.1f} µs; cycles per µs '
               f'{np.median(t[:, n - 1, s]) / np.median(life[:, s]):.0f}')
+    print('SIMD of waves 0-3 (share of workgroups per SIMD):')
+    for w in range(waves):
+        share = [float((simd[:, w, :] == k).mean()) for k in range(4)]
+        print(f'  wave {w}: ' + ', '.join(f'SIMD {k} {share[k]:.2f}' for k in range(4)))
 
 
 if __name__ == '__main__':
