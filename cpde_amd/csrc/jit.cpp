@@ -684,7 +684,7 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
 // cost stage `cost` between them (it fills O's second half), then the
 // backward.  The row-major weight copies are written before the launch.
 static std::string epoch_body(const std::vector<int>& neurons, const std::string& prefetch, const std::string& cost,
-                              bool stamps) {
+                              bool stamps, const std::string& after_input = "") {
     const int L = int(neurons.size()), NO = neurons[L - 1];
     std::ostringstream ep;
     // S: the cost stage's scratch (matching terms, or a double and an int per
@@ -707,7 +707,8 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
        << prefetch << "    const float xin = input_ahead<" << neurons[0] << ">(a, p0, npts);  // for the input gradient\n"
        << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
        << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
-       << "    __syncthreads();\n";
+       << "    __syncthreads();\n"
+       << after_input;
     // the last hidden layer's y (read from X by the output layer's partial) and
     // the first one's dE/dz (read from X by the input transition's) stay in the
     // workgroup: no later launch reads them
@@ -788,12 +789,14 @@ std::string fused_source(const Tables& t, const std::vector<int>& neurons, const
     {
         const int NO = neurons[L - 1];
         const std::string prefetch =
-            "    const MatchTerm pre = match_prefetch<" + std::to_string(NO) + ">(m, p0, npts);\n";
+            "    const MatchAhead pa = match_ahead<" + std::to_string(NO) + ">(m, p0, npts);\n";
+        const std::string after_input =
+            "    const MatchTerm pre = match_fetch<" + std::to_string(NO) + ">(m, p0, npts, pa);\n";
         const std::string cost = "    net_match<" + std::to_string(NO) + ">(a, m, " + std::to_string(L - 1) +
                                  ", S, p0, npts, O, O + kNNC * " + std::to_string(NO) + ", pre);\n";
         o << "extern \"C\" __global__ __launch_bounds__(" << nt << ", " << tuning.backward_blocks
           << ") void network_epoch_k(NetArgs a, MatchArgs m, int points) {\n"
-          << epoch_body(neurons, prefetch, cost, tuning.stamps != 0) << "}\n";
+          << epoch_body(neurons, prefetch, cost, tuning.stamps != 0, after_input) << "}\n";
     }
     o << "\nextern \"C\" __global__ __launch_bounds__(256) void input_layer_k(const float* W, const float* X, float* Z,"
          " float* Y, int points) { input_layer<"
