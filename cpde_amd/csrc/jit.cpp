@@ -719,10 +719,12 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
     ep << "    UAhead<" << last << ", output_adjoint_split<" << last
        << ">()> ua;  // the last hidden layer's u rows, in flight during the output layer and the cost\n"
        << "    u_ahead<" << last << ", output_adjoint_split<" << last << ">()>(a, " << L - 2 << ", p0, npts, ua);\n"
+       << "    WAhead<" << last << ", " << NO << "> wa;  // and the output weights of the lane's adjoint items\n"
+       << "    w_ahead<" << last << ", " << NO << ">(a, " << L - 2 << ", npts, wa);\n"
        << "    net_output<" << neurons[L - 2] << ", " << NO << ">(a, " << L - 2 << ", X, p0, npts, O);\n"
        << "    __syncthreads();  // the output values of the block's columns are in O\n"
        << cost << "    net_output_backward<" << neurons[L - 2] << ", " << NO << ", true>(a, " << L - 2
-       << ", X, p0, npts, ua, O + kNNC * " << NO << ");\n";
+       << ", X, p0, npts, ua, O + kNNC * " << NO << ", &wa);\n";
     for (int t = L - 3; t >= 1; --t)
         ep << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << (t == 1 ? ", false" : "") << ">(a, "
            << t << ", X, T, p0, npts);\n";
