@@ -377,6 +377,11 @@ static FusedTuning tuning(int rows, int width, int compute_units, const std::vec
     // Diagnostics: clock stamps of the one-pass epoch's phases, written over
     // the output stack (cpde_amd/stamps.py reads them back).
     t.stamps = env_int("CPDE_PHASE_STAMPS", 0) ? 1 : 0;
+    // One-pass epochs: wave priority by dispatch round (tier_priority in the
+    // generated source; 0 turns it off).  It acts only where a launch has more
+    // workgroups than CUs.
+    t.tier_prio = env_int("CPDE_NET_TIER_PRIO", 125);
+    t.tier_cus = compute_units;
     // Hidden weight-gradient partials from the network backward itself, on
     // request (CPDE_INKERNEL_WGRAD=1; hidden widths that are multiples of 16).
     // Measured on the Poisson graph epoch, whose 256-point one-row boundary

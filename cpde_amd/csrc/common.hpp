@@ -380,6 +380,7 @@ struct FusedTuning {
     int scaled = 1;                // network kernels keep Taylor-scaled sigmoid stacks (row alpha / alpha!)
     int inkernel_wgrad = 0;        // network backward kernels write hidden weight-gradient partials themselves
     int b_pairs = 1;               // 16-column products: each wave takes 32-neuron blocks, B loaded as float2
+    int tier_prio = 0, tier_cus = 256;  // one-pass epochs: wave priorities by dispatch round, and the CU count
     int stamps = 0;                // one-pass epochs write per-phase clock stamps over their output stack
 };
 // Whether the schema is closed under swapping variables 0 and 1 (the scaled

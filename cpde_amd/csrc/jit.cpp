@@ -661,6 +661,7 @@ static void emit_prologue(std::ostream& o, const Tables& t, const std::vector<in
     if (tuning.inkernel_wgrad) o << "#define CPDE_INKERNEL_WGRAD 1\n";
     if (tuning.b_pairs) o << "#define CPDE_B_PAIRS 1\n";
     if (tuning.stamps) o << "#define CPDE_STAMPS 1\n";
+    if (tuning.tier_prio) o << "#define CPDE_TIER_PRIO " << tuning.tier_prio << "\n#define CPDE_TIER_CUS " << tuning.tier_cus << "\n";
     // row splits of the compositions used by the network-fused kernels (scaled
     // forward compositions split over mirror lanes instead)
     std::vector<int> splits;
@@ -704,6 +705,7 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
        << "    float* const S = T;\n"
        << "#endif\n"
        << "    const int p0 = net_block(a) * kNPB, npts = kNPB == 1 ? 1 : min(kNPB, points - p0);\n"
+       << "    tier_priority(a, 0);\n"
        << prefetch << "    const float xin = input_ahead<" << neurons[0] << ">(a, p0, npts);  // for the input gradient\n"
        << "    net_input<" << neurons[0] << ", " << neurons[1] << ">(a, X, p0, npts);\n"
        << "    zero_pad(X, " << neurons[1] << ", " << (neurons[1] + 7) / 8 * 8 << ");\n"
@@ -712,10 +714,13 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
     // the last hidden layer's y (read from X by the output layer's partial) and
     // the first one's dE/dz (read from X by the input transition's) stay in the
     // workgroup: no later launch reads them
+    int marker = 0;
     for (int t = 1; t + 2 < L; ++t)
-        ep << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << (t + 3 == L ? ", false" : "") << ">(a, " << t
+        ep << "    tier_priority(a, " << ++marker << ");\n"
+           << "    net_hidden<" << neurons[t] << ", " << neurons[t + 1] << (t + 3 == L ? ", false" : "") << ">(a, " << t
            << ", X, T, p0, npts);\n";
     const std::string last = std::to_string(neurons[L - 2]);
+    ep << "    tier_priority(a, " << ++marker << ");\n";
     ep << "    UAhead<" << last << ", output_adjoint_split<" << last
        << ">()> ua;  // the last hidden layer's u rows, in flight during the output layer and the cost\n"
        << "    u_ahead<" << last << ", output_adjoint_split<" << last << ">()>(a, " << L - 2 << ", p0, npts, ua);\n"
@@ -723,10 +728,12 @@ static std::string epoch_body(const std::vector<int>& neurons, const std::string
        << "    w_ahead<" << last << ", " << NO << ">(a, " << L - 2 << ", npts, wa);\n"
        << "    net_output<" << neurons[L - 2] << ", " << NO << ">(a, " << L - 2 << ", X, p0, npts, O);\n"
        << "    __syncthreads();  // the output values of the block's columns are in O\n"
+       << "    tier_priority(a, " << ++marker << ");\n"
        << cost << "    net_output_backward<" << neurons[L - 2] << ", " << NO << ", true>(a, " << L - 2
        << ", X, p0, npts, ua, O + kNNC * " << NO << ", &wa);\n";
     for (int t = L - 3; t >= 1; --t)
-        ep << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << (t == 1 ? ", false" : "") << ">(a, "
+        ep << "    tier_priority(a, " << ++marker << ");\n"
+           << "    net_hidden_backward<" << neurons[t] << ", " << neurons[t + 1] << (t == 1 ? ", false" : "") << ">(a, "
            << t << ", X, T, p0, npts);\n";
     ep << "    net_input_gradient<" << neurons[0] << ", " << neurons[1] << ", true>(a, X, p0, npts, xin);\n";
     // Diagnostics (FusedTuning::stamps): a clock stamp after every phase --
